@@ -1,0 +1,166 @@
+/*
+ * ltx_hip.h -- C ABI of libltx_hip.so, the gfx950 (MI355X) kernels of the
+ * LTX-2.3 audio+video DiT denoise step.
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are device pointers.  bf16 tensors are passed as `void*`
+ *     (2-byte IEEE bfloat16 elements), fp32 tensors as `float*`.
+ *   - `stream` is a hipStream_t passed as `void*` (NULL = the null stream).
+ *     Every call only enqueues work on that stream; nothing synchronises the
+ *     host, allocates or frees memory, or keeps state between calls.
+ *   - Row-major 2-D tensors carry an explicit row stride in ELEMENTS.
+ *   - The return value is an LTX_* status code.  LTX_ERR_UNSUPPORTED means the
+ *     shape is outside what the kernel implements; the caller decides whether
+ *     a fallback expression applies (the reference's shape gates do exactly
+ *     that, see LTX_2_MLX/kernels/fused_ops.py:204-234, :369-395).
+ *
+ * Reference interfaces replaced (paths relative to the LTX-2-MLX tree):
+ *   ltx_adaln_norm_fused_bf16   <- kernels/fused_ops.py:237 adaln_norm_fused
+ *                                  (Metal kernel :104-180; inline forms
+ *                                  model/transformer/transformer.py:21-37,
+ *                                  :374-375, :535-580)
+ *   ltx_gated_add_fused_bf16    <- kernels/fused_ops.py:398 gated_add_fused
+ *                                  (Metal kernel :314-353; inline forms
+ *                                  transformer.py:40-50, :387, :484, :598, :625)
+ *   ltx_qknorm_rope_bf16        <- model/transformer/attention.py:578-584
+ *                                  (RMSNorm :320-329 + rope.py:16-89)
+ *   ltx_output_norm_modulate_bf16 <- model/transformer/model.py:1312-1342
+ *   ltx_euler_x0_step_bf16      <- model.py:1519-1525 (X0Model.denoise) +
+ *                                  components/diffusion_steps.py:19-69
+ *   ltx_timestep_embedding_f32  <- model/transformer/timestep_embedding.py:9-59
+ *   ltx_gemv_f32_bf16w          <- timestep_embedding.py:88-201 (AdaLN MLPs)
+ */
+#ifndef LTX_HIP_H_
+#define LTX_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LTX_OK 0
+#define LTX_ERR_INVALID_ARG (-1)
+#define LTX_ERR_UNSUPPORTED (-2)
+#define LTX_ERR_HIP (-3)
+#define LTX_ERR_ALIGNMENT (-4)
+
+/* Human-readable name of a status code (static storage). */
+const char* ltx_status_string(int status);
+
+/* Library version, encoded as major*10000 + minor*100 + patch. */
+int ltx_version(void);
+
+/* ---- flags for ltx_adaln_norm_fused_bf16 ---------------------------------- */
+/* Round the normalised row to bf16 before modulating: the reference's
+ * `mx.fast.rms_norm(x)` (bf16 output) followed by the fp32 modulation, i.e.
+ * transformer.py:36-37 / :374 / :535-580.  Without it the single-rounding
+ * fused-kernel semantics of fused_ops.py:172-175 apply. */
+#define LTX_ADALN_ROUND_NORM 1
+/* Skip the RMS normalisation: out = bf16(x*(1+scale)+shift), the text-context
+ * KV modulation of transformer.py:375. */
+#define LTX_ADALN_NO_NORM 2
+
+/*
+ * out[r, c] = bf16( rms(x[r,:]) * (1 + scale[c]) + shift[c] ),
+ *   rms(x) = x * rsqrt(mean(x^2) + eps), sum of squares in fp32.
+ * x: (rows, C) bf16 with row stride x_stride; out: (rows, C) bf16 with row
+ * stride out_stride (out may alias x).  scale/shift: fp32 (C).  C must be a
+ * multiple of 512 and at most 4096.  Replaces adaln_norm_fused
+ * (kernels/fused_ops.py:237-287).
+ */
+int ltx_adaln_norm_fused_bf16(const void* x, int64_t x_stride, const float* scale,
+                              const float* shift, void* out, int64_t out_stride,
+                              int64_t rows, int64_t C, float eps, int flags,
+                              void* stream);
+
+/* ---- flags for ltx_gated_add_fused_bf16 ----------------------------------- */
+/* Round branch*gate to bf16 before the add: `x + (attn_out*gate).astype(bf16)`
+ * of the text cross-attention (transformer.py:387, :484). */
+#define LTX_GATED_ROUND_PRODUCT 1
+
+/*
+ * out[r, c] = bf16( gate[c] * branch[r, c] + residual[r, c] ) in fp32.
+ * residual/branch/out: (rows, C) bf16, each with its own row stride; out may
+ * alias residual.  gate: fp32 (C).  C must be a multiple of 512 and at most
+ * 4096.  Replaces gated_add_fused (kernels/fused_ops.py:398-442).
+ */
+int ltx_gated_add_fused_bf16(const void* residual, int64_t residual_stride,
+                             const void* branch, int64_t branch_stride,
+                             const float* gate, void* out, int64_t out_stride,
+                             int64_t rows, int64_t C, int flags, void* stream);
+
+/*
+ * In-place QK-RMSNorm + split RoPE for one attention call
+ * (attention.py:578-584):
+ *   q[t,:] = bf16( rope( bf16( rms(q[t,:]) * wq ), cos_q[t], sin_q[t] ) )
+ *   k[t,:] = likewise with wk, cos_k, sin_k.
+ * The norm spans the whole inner dim D (= heads*head_dim), as the reference's
+ * RMSNorm(inner_dim) does.  Split RoPE (rope.py:37-50): within each head the
+ * first half of the channels rotates with the second half,
+ *   [x1*c - x2*s, x1*s + x2*c], evaluated in fp32.
+ * Tables are fp32, row-major (rows, D/2): entry [t, h*head_dim/2 + i] is the
+ * angle's cos/sin for head h, pair i -- the reference's (1, H, T, dh/2)
+ * tensor transposed to token-major.  Pass NULL tables to skip RoPE (text
+ * cross-attention).  q/k rows have strides q_stride/k_stride (elements), so
+ * they can live inside a fused QKV projection output.  D must be a multiple of
+ * 1024 and at most 4096; head_dim in {64, 128}.  rows_q or rows_k may be 0.
+ */
+int ltx_qknorm_rope_bf16(void* q, int64_t q_stride, int64_t rows_q, const float* wq,
+                         const float* cos_q, const float* sin_q, void* k,
+                         int64_t k_stride, int64_t rows_k, const float* wk,
+                         const float* cos_k, const float* sin_k, int64_t D,
+                         int64_t head_dim, float eps, void* stream);
+
+/*
+ * Output head modulation (model.py:1312-1342):
+ *   ss     = bf16(table[0:2, :] + emb[:])           (shift row 0, scale row 1)
+ *   n      = bf16(LayerNorm(x, no affine, eps))
+ *   out    = bf16(bf16(n * bf16(1 + scale)) + shift)  (bf16 arithmetic)
+ * x/out: (rows, C) bf16 with row strides; table: fp32 (2, C); emb: fp32 (C).
+ * C must be a multiple of 512 and at most 4096.
+ */
+int ltx_output_norm_modulate_bf16(const void* x, int64_t x_stride, const float* table,
+                                  const float* emb, void* out, int64_t out_stride,
+                                  int64_t rows, int64_t C, float eps, void* stream);
+
+/*
+ * One distilled Euler step fused with the X0 conversion
+ * (model.py:1519-1525, diffusion_steps.py:58-69), elementwise over n values:
+ *   x0  = fp32(latent) - sigma * fp32(velocity)
+ *   out = bf16( x0 + ratio * (fp32(latent) - x0) ),  ratio = fp32(sigma_next/sigma)
+ * Every product and sum is rounded separately, as in the reference.  out may
+ * alias latent.
+ */
+int ltx_euler_x0_step_bf16(const void* latent, const void* velocity, float sigma,
+                           float ratio, void* out, int64_t n, void* stream);
+
+/*
+ * Sinusoidal timestep embedding with flip_sin_to_cos=True, shift 0,
+ * max_period 10000 (timestep_embedding.py:9-59, :140-144):
+ *   out[i]        = cos(t * exp(-ln(10000) * i / half)),  i < half
+ *   out[half + i] = sin(...)
+ * for `count` timesteps t[j] = values[j] * multiplier; out is (count, dim).
+ */
+int ltx_timestep_embedding_f32(const float* values, int64_t count, float multiplier,
+                               float* out, int64_t dim, void* stream);
+
+/* ---- flags for ltx_gemv_f32_bf16w ----------------------------------------- */
+#define LTX_GEMV_SILU_INPUT 1  /* apply SiLU to x before the product */
+#define LTX_GEMV_SILU_OUTPUT 2 /* apply SiLU to y after the bias */
+
+/*
+ * y[b, n] = act( sum_k W[n, k] * act(x[b, k]) + bias[n] ), fp32 accumulation.
+ * x: fp32 (batch, K); W: bf16 (N, K) row-major; bias: fp32 (N) or NULL;
+ * y: fp32 (batch, N).  batch <= 8.  The AdaLN MLP layers run on a
+ * per-step scalar timestep (timestep_embedding.py:111-123, :186-201).
+ */
+int ltx_gemv_f32_bf16w(const float* x, int64_t batch, int64_t K, const void* W,
+                       const float* bias, float* y, int64_t N, int flags,
+                       void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LTX_HIP_H_ */

@@ -1,0 +1,563 @@
+// Bandwidth-bound fused row kernels of the DiT block: AdaLN (RMSNorm +
+// shift/scale), gated residual add, QK-RMSNorm + split RoPE and the output
+// head's LayerNorm modulation.
+//
+// Layout: one 64-lane wavefront owns one token row at a time.  Lane L reads
+// the 16-byte vectors L, L+64, L+128, ... of the row, so every load and store
+// instruction of a wave moves one contiguous 1 KiB span of HBM.  The
+// per-channel parameters (1+scale, shift, gate) depend only on the lane's
+// channels, so a wave loads them into registers once and keeps them across
+// all the rows it visits (grid-stride over rows, at most 8 waves per CU of
+// work in flight).  Row reductions are wave-local shuffles; no LDS, no
+// barriers, no atomics.
+#include "ltx_common.h"
+
+namespace ltx {
+
+constexpr int kRowBlock = 256;          // 4 waves per workgroup
+constexpr int kWavesPerBlock = kRowBlock / kWave;
+constexpr int64_t kMaxRowBlocks = 2048;  // 256 CUs x 8 waves / 4 waves per block... x4 headroom
+
+__device__ __forceinline__ void load8(const bf16* p, float* out) {
+  bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) out[i] = (float)v[i];
+}
+
+__device__ __forceinline__ void store8(bf16* p, const float* in) {
+  bf16x8 v;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = (bf16)in[i];
+  *reinterpret_cast<bf16x8*>(p) = v;
+}
+
+__device__ __forceinline__ void load8f(const float* p, float* out) {
+  f32x4 a = *reinterpret_cast<const f32x4*>(p);
+  f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+  out[0] = a[0]; out[1] = a[1]; out[2] = a[2]; out[3] = a[3];
+  out[4] = b[0]; out[5] = b[1]; out[6] = b[2]; out[7] = b[3];
+}
+
+// ---------------------------------------------------------------------------
+// AdaLN: out = bf16(rms(x) * (1 + scale) + shift)
+// VPL = vectors (8 bf16) per lane = C / 512.
+template <int VPL>
+__global__ __launch_bounds__(kRowBlock) void adaln_kernel(
+    const bf16* __restrict__ x, int64_t x_stride, const float* __restrict__ scale,
+    const float* __restrict__ shift, bf16* out, int64_t out_stride, int64_t rows,
+    float eps, int flags) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t wave0 = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
+  constexpr int C = VPL * 512;
+  const float inv_c = 1.0f / (float)C;
+  const bool round_norm = (flags & LTX_ADALN_ROUND_NORM) != 0;
+  const bool no_norm = (flags & LTX_ADALN_NO_NORM) != 0;
+
+  float onep[VPL][8], sh[VPL][8];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int c0 = (lane + j * kWave) * 8;
+    load8f(scale + c0, onep[j]);
+    load8f(shift + c0, sh[j]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) onep[j][i] = 1.0f + onep[j][i];
+  }
+
+  for (int64_t r = wave0; r < rows; r += nwaves) {
+    const bf16* xr = x + r * x_stride;
+    float xv[VPL][8];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) load8(xr + (lane + j * kWave) * 8, xv[j]);
+    float inv = 1.0f;
+    if (!no_norm) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int j = 0; j < VPL; ++j)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss = fmaf(xv[j][i], xv[j][i], ss);
+      ss = wave_sum(ss);
+      inv = rsqrt_rn(ss * inv_c + eps);
+    }
+    bf16* orow = out + r * out_stride;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      float o[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float n = xv[j][i] * inv;
+        if (round_norm) n = round_bf(n);
+        o[i] = n * onep[j][i] + sh[j][i];
+      }
+      store8(orow + (lane + j * kWave) * 8, o);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Gated residual add: out = bf16(gate * branch + residual)
+template <int VPL>
+__global__ __launch_bounds__(kRowBlock) void gated_add_kernel(
+    const bf16* residual, int64_t res_stride, const bf16* __restrict__ branch,
+    int64_t br_stride, const float* __restrict__ gate, bf16* out, int64_t out_stride,
+    int64_t rows, int flags) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t wave0 = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
+  const bool round_prod = (flags & LTX_GATED_ROUND_PRODUCT) != 0;
+
+  float g[VPL][8];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) load8f(gate + (lane + j * kWave) * 8, g[j]);
+
+  for (int64_t r = wave0; r < rows; r += nwaves) {
+    float rv[VPL][8], bv[VPL][8];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const int c0 = (lane + j * kWave) * 8;
+      load8(residual + r * res_stride + c0, rv[j]);
+      load8(branch + r * br_stride + c0, bv[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      float o[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (round_prod)
+          o[i] = round_bf(bv[j][i] * g[j][i]) + rv[j][i];
+        else
+          o[i] = fmaf(g[j][i], bv[j][i], rv[j][i]);
+      }
+      store8(out + r * out_stride + (lane + j * kWave) * 8, o);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// QK-RMSNorm + split RoPE, in place.
+//
+// Lane L owns PPL = D/1024 "pairs" p = L + 64*j.  A pair is two 8-channel
+// vectors of one head that rotate together: v1 in the first half of the head,
+// v2 = v1 + head_dim/16 in the second half.  Its RoPE angles are the 8
+// consecutive table entries [8p, 8p+8) of the token's (D/2)-wide table row, so
+// each lane reads its own cos/sin with two 16-byte loads per table.  The norm
+// weights live in LDS (read once per workgroup).
+template <int PPL, int HALF_VECS>
+__device__ __forceinline__ void qknorm_rope_row(bf16* row, const float* w_lds, const float* cosr,
+                                                const float* sinr, float eps, int lane,
+                                                float (&cs)[PPL][8], float (&sn)[PPL][8],
+                                                bool load_table) {
+  constexpr int D = PPL * 1024;
+  float a[PPL][8], b[PPL][8];
+  int v1[PPL];
+#pragma unroll
+  for (int j = 0; j < PPL; ++j) {
+    const int p = lane + j * kWave;
+    v1[j] = (p / HALF_VECS) * (2 * HALF_VECS) + (p % HALF_VECS);
+    load8(row + v1[j] * 8, a[j]);
+    load8(row + (v1[j] + HALF_VECS) * 8, b[j]);
+    if (load_table && cosr != nullptr) {
+      load8f(cosr + p * 8, cs[j]);
+      load8f(sinr + p * 8, sn[j]);
+    }
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < PPL; ++j)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss = fmaf(a[j][i], a[j][i], fmaf(b[j][i], b[j][i], ss));
+  ss = wave_sum(ss);
+  const float inv = rsqrt_rn(ss * (1.0f / (float)D) + eps);
+#pragma unroll
+  for (int j = 0; j < PPL; ++j) {
+    float wa[8], wb[8];
+    load8f(w_lds + v1[j] * 8, wa);
+    load8f(w_lds + (v1[j] + HALF_VECS) * 8, wb);
+    float oa[8], ob[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float x1 = round_bf(a[j][i] * inv * wa[i]);
+      const float x2 = round_bf(b[j][i] * inv * wb[i]);
+      if (cosr != nullptr) {
+        oa[i] = x1 * cs[j][i] - x2 * sn[j][i];
+        ob[i] = x1 * sn[j][i] + x2 * cs[j][i];
+      } else {
+        oa[i] = x1;
+        ob[i] = x2;
+      }
+    }
+    store8(row + v1[j] * 8, oa);
+    store8(row + (v1[j] + HALF_VECS) * 8, ob);
+  }
+}
+
+template <int PPL, int HALF_VECS>
+__global__ __launch_bounds__(kRowBlock) void qknorm_rope_kernel(
+    bf16* q, int64_t q_stride, int64_t rows_q, const float* __restrict__ wq,
+    const float* cos_q, const float* sin_q, bf16* k, int64_t k_stride, int64_t rows_k,
+    const float* __restrict__ wk, const float* cos_k, const float* sin_k, float eps) {
+  constexpr int D = PPL * 1024;
+  __shared__ float w_lds[2 * D];
+  for (int i = threadIdx.x; i < D; i += kRowBlock) {
+    w_lds[i] = rows_q > 0 ? wq[i] : 0.0f;
+    w_lds[D + i] = rows_k > 0 ? wk[i] : 0.0f;
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t wave0 = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
+  const int64_t rows = rows_q > rows_k ? rows_q : rows_k;
+  const int64_t half = D / 2;
+  const bool shared_table = (cos_q == cos_k) && (sin_q == sin_k);
+  float cs[PPL][8], sn[PPL][8];
+  for (int64_t t = wave0; t < rows; t += nwaves) {
+    bool have_table = false;
+    if (t < rows_q) {
+      qknorm_rope_row<PPL, HALF_VECS>(q + t * q_stride, w_lds,
+                                      cos_q ? cos_q + t * half : nullptr,
+                                      sin_q ? sin_q + t * half : nullptr, eps, lane, cs, sn,
+                                      true);
+      have_table = true;
+    }
+    if (t < rows_k) {
+      qknorm_rope_row<PPL, HALF_VECS>(k + t * k_stride, w_lds + D,
+                                      cos_k ? cos_k + t * half : nullptr,
+                                      sin_k ? sin_k + t * half : nullptr, eps, lane, cs, sn,
+                                      !(have_table && shared_table));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Output head: bf16 LayerNorm + bf16-arithmetic modulation.
+template <int VPL>
+__global__ __launch_bounds__(kRowBlock) void output_norm_kernel(
+    const bf16* __restrict__ x, int64_t x_stride, const float* __restrict__ table,
+    const float* __restrict__ emb, bf16* out, int64_t out_stride, int64_t rows, float eps) {
+  constexpr int C = VPL * 512;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t wave0 = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
+  float shf[VPL][8], ops[VPL][8];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int c0 = (lane + j * kWave) * 8;
+    float t0[8], t1[8], e[8];
+    load8f(table + c0, t0);
+    load8f(table + C + c0, t1);
+    load8f(emb + c0, e);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      shf[j][i] = round_bf(t0[i] + e[i]);
+      ops[j][i] = round_bf(1.0f + round_bf(t1[i] + e[i]));
+    }
+  }
+  for (int64_t r = wave0; r < rows; r += nwaves) {
+    float xv[VPL][8];
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      load8(x + r * x_stride + (lane + j * kWave) * 8, xv[j]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s += xv[j][i];
+    }
+    const float mean = wave_sum(s) * (1.0f / (float)C);
+    float v = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float d = xv[j][i] - mean;
+        v = fmaf(d, d, v);
+      }
+    const float inv = rsqrt_rn(wave_sum(v) * (1.0f / (float)C) + eps);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      float o[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float n = round_bf((xv[j][i] - mean) * inv);
+        o[i] = round_bf(n * ops[j][i]) + shf[j][i];
+      }
+      store8(out + r * out_stride + (lane + j * kWave) * 8, o);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void euler_kernel(const bf16* latent, const bf16* velocity,
+                                                    float sigma, float ratio, bf16* out,
+                                                    int64_t n) {
+  const int64_t nvec = n / 8;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nvec; i += stride) {
+    float l[8], v[8], o[8];
+    load8(latent + i * 8, l);
+    load8(velocity + i * 8, v);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x0 = sub_rn(l[e], mul_rn(sigma, v[e]));
+      o[e] = add_rn(x0, mul_rn(ratio, sub_rn(l[e], x0)));
+    }
+    store8(out + i * 8, o);
+  }
+  // scalar tail (n not a multiple of 8)
+  if (blockIdx.x == 0 && threadIdx.x < (n & 7)) {
+    const int64_t e = nvec * 8 + threadIdx.x;
+    const float l = (float)latent[e], v = (float)velocity[e];
+    const float x0 = sub_rn(l, mul_rn(sigma, v));
+    out[e] = (bf16)add_rn(x0, mul_rn(ratio, sub_rn(l, x0)));
+  }
+}
+
+__global__ void timestep_embedding_kernel(const float* values, int64_t count, float mult,
+                                          float* out, int64_t dim) {
+  const int64_t half = dim / 2;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= count * dim) return;
+  const int64_t b = idx / dim, c = idx % dim;
+  if (c >= 2 * half) {  // odd dim: zero pad
+    out[idx] = 0.0f;
+    return;
+  }
+  const int64_t i = c < half ? c : c - half;
+  // exponent = (-ln(10000) * i) / half, each step rounded to fp32 as in the
+  // reference's fp32 array arithmetic.
+  const float expo = __fdiv_rn(__fmul_rn(-9.210340371976184f, (float)i), (float)half);
+  const float t = __fmul_rn(values[b], mult);
+  const float arg = __fmul_rn(t, expf(expo));
+  out[idx] = c < half ? cosf(arg) : sinf(arg);
+}
+
+// GEMV: each wave computes ROWS_PER_WAVE outputs for every batch entry;
+// x is staged in LDS once per workgroup.
+constexpr int kGemvRowsPerWave = 4;
+constexpr int kGemvMaxK = 4096;
+constexpr int kGemvMaxBatch = 4;
+
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
+
+__global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, int batch,
+                                                   int K, const bf16* __restrict__ W,
+                                                   const float* __restrict__ bias,
+                                                   float* __restrict__ y, int64_t N, int flags) {
+  __shared__ float xs[kGemvMaxBatch * kGemvMaxK];
+  for (int i = threadIdx.x; i < batch * K; i += blockDim.x) {
+    float v = x[i];
+    if (flags & LTX_GEMV_SILU_INPUT) v = silu(v);
+    xs[i] = v;
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t wave = (int64_t)blockIdx.x * (blockDim.x / kWave) + (threadIdx.x >> 6);
+  const int64_t n0 = wave * kGemvRowsPerWave;
+  for (int rr = 0; rr < kGemvRowsPerWave; ++rr) {
+    const int64_t n = n0 + rr;
+    if (n >= N) break;
+    float acc[kGemvMaxBatch] = {0.f, 0.f, 0.f, 0.f};
+    const bf16* wr = W + n * (int64_t)K;
+    for (int k0 = lane * 8; k0 < K; k0 += kWave * 8) {
+      float wv[8];
+      load8(wr + k0, wv);
+      for (int b = 0; b < batch; ++b) {
+        const float* xb = xs + b * K + k0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[b] = fmaf(wv[i], xb[i], acc[b]);
+      }
+    }
+    for (int b = 0; b < batch; ++b) {
+      float v = wave_sum(acc[b]);
+      if (lane == 0) {
+        if (bias) v += bias[n];
+        if (flags & LTX_GEMV_SILU_OUTPUT) v = silu(v);
+        y[(int64_t)b * N + n] = v;
+      }
+    }
+  }
+}
+
+}  // namespace ltx
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+using namespace ltx;
+
+static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+static inline int row_grid(int64_t rows) {
+  int64_t blocks = (rows + kWavesPerBlock - 1) / kWavesPerBlock;
+  if (blocks > kMaxRowBlocks) blocks = kMaxRowBlocks;
+  if (blocks < 1) blocks = 1;
+  return (int)blocks;
+}
+
+extern "C" const char* ltx_status_string(int status) {
+  switch (status) {
+    case LTX_OK: return "ok";
+    case LTX_ERR_INVALID_ARG: return "invalid argument";
+    case LTX_ERR_UNSUPPORTED: return "unsupported shape";
+    case LTX_ERR_HIP: return "HIP launch error";
+    case LTX_ERR_ALIGNMENT: return "pointer or stride not 16-byte aligned";
+    default: return "unknown status";
+  }
+}
+
+extern "C" int ltx_version(void) { return 100; }
+
+extern "C" int ltx_adaln_norm_fused_bf16(const void* x, int64_t x_stride, const float* scale,
+                                         const float* shift, void* out, int64_t out_stride,
+                                         int64_t rows, int64_t C, float eps, int flags,
+                                         void* stream) {
+  if (rows < 0 || !x || !scale || !shift || !out) return LTX_ERR_INVALID_ARG;
+  if (C <= 0 || C % 512 != 0 || C > 4096) return LTX_ERR_UNSUPPORTED;
+  if (x_stride < C || out_stride < C) return LTX_ERR_INVALID_ARG;
+  if (!aligned16(x) || !aligned16(out) || !aligned16(scale) || !aligned16(shift) ||
+      x_stride % 8 || out_stride % 8)
+    return LTX_ERR_ALIGNMENT;
+  if (rows == 0) return LTX_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const bf16* xp = (const bf16*)x;
+  bf16* op = (bf16*)out;
+  const int grid = row_grid(rows);
+  switch (C / 512) {
+    case 1: adaln_kernel<1><<<grid, kRowBlock, 0, s>>>(xp, x_stride, scale, shift, op, out_stride, rows, eps, flags); break;
+    case 2: adaln_kernel<2><<<grid, kRowBlock, 0, s>>>(xp, x_stride, scale, shift, op, out_stride, rows, eps, flags); break;
+    case 4: adaln_kernel<4><<<grid, kRowBlock, 0, s>>>(xp, x_stride, scale, shift, op, out_stride, rows, eps, flags); break;
+    case 8: adaln_kernel<8><<<grid, kRowBlock, 0, s>>>(xp, x_stride, scale, shift, op, out_stride, rows, eps, flags); break;
+    default: return LTX_ERR_UNSUPPORTED;
+  }
+  return ltx_launch_status();
+}
+
+extern "C" int ltx_gated_add_fused_bf16(const void* residual, int64_t residual_stride,
+                                        const void* branch, int64_t branch_stride,
+                                        const float* gate, void* out, int64_t out_stride,
+                                        int64_t rows, int64_t C, int flags, void* stream) {
+  if (rows < 0 || !residual || !branch || !gate || !out) return LTX_ERR_INVALID_ARG;
+  if (C <= 0 || C % 512 != 0 || C > 4096) return LTX_ERR_UNSUPPORTED;
+  if (residual_stride < C || branch_stride < C || out_stride < C) return LTX_ERR_INVALID_ARG;
+  if (!aligned16(residual) || !aligned16(branch) || !aligned16(gate) || !aligned16(out) ||
+      residual_stride % 8 || branch_stride % 8 || out_stride % 8)
+    return LTX_ERR_ALIGNMENT;
+  if (rows == 0) return LTX_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const bf16* rp = (const bf16*)residual;
+  const bf16* bp = (const bf16*)branch;
+  bf16* op = (bf16*)out;
+  const int grid = row_grid(rows);
+  switch (C / 512) {
+    case 1: gated_add_kernel<1><<<grid, kRowBlock, 0, s>>>(rp, residual_stride, bp, branch_stride, gate, op, out_stride, rows, flags); break;
+    case 2: gated_add_kernel<2><<<grid, kRowBlock, 0, s>>>(rp, residual_stride, bp, branch_stride, gate, op, out_stride, rows, flags); break;
+    case 4: gated_add_kernel<4><<<grid, kRowBlock, 0, s>>>(rp, residual_stride, bp, branch_stride, gate, op, out_stride, rows, flags); break;
+    case 8: gated_add_kernel<8><<<grid, kRowBlock, 0, s>>>(rp, residual_stride, bp, branch_stride, gate, op, out_stride, rows, flags); break;
+    default: return LTX_ERR_UNSUPPORTED;
+  }
+  return ltx_launch_status();
+}
+
+extern "C" int ltx_qknorm_rope_bf16(void* q, int64_t q_stride, int64_t rows_q, const float* wq,
+                                    const float* cos_q, const float* sin_q, void* k,
+                                    int64_t k_stride, int64_t rows_k, const float* wk,
+                                    const float* cos_k, const float* sin_k, int64_t D,
+                                    int64_t head_dim, float eps, void* stream) {
+  if (rows_q < 0 || rows_k < 0) return LTX_ERR_INVALID_ARG;
+  if (rows_q > 0 && (!q || !wq || q_stride < D)) return LTX_ERR_INVALID_ARG;
+  if (rows_k > 0 && (!k || !wk || k_stride < D)) return LTX_ERR_INVALID_ARG;
+  if ((cos_q == nullptr) != (sin_q == nullptr) || (cos_k == nullptr) != (sin_k == nullptr))
+    return LTX_ERR_INVALID_ARG;
+  if (D <= 0 || D % 1024 != 0 || D > 4096) return LTX_ERR_UNSUPPORTED;
+  if (head_dim != 64 && head_dim != 128) return LTX_ERR_UNSUPPORTED;
+  if ((rows_q > 0 && (!aligned16(q) || q_stride % 8 || (cos_q && (!aligned16(cos_q) || !aligned16(sin_q))))) ||
+      (rows_k > 0 && (!aligned16(k) || k_stride % 8 || (cos_k && (!aligned16(cos_k) || !aligned16(sin_k))))))
+    return LTX_ERR_ALIGNMENT;
+  const int64_t rows = rows_q > rows_k ? rows_q : rows_k;
+  if (rows == 0) return LTX_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const int grid = row_grid(rows);
+  bf16* qp = (bf16*)q;
+  bf16* kp = (bf16*)k;
+#define LTX_QK_LAUNCH(PPL, HV)                                                              \
+  qknorm_rope_kernel<PPL, HV><<<grid, kRowBlock, 0, s>>>(qp, q_stride, rows_q, wq, cos_q,   \
+                                                        sin_q, kp, k_stride, rows_k, wk,    \
+                                                        cos_k, sin_k, eps)
+  const int ppl = (int)(D / 1024);
+  if (head_dim == 128) {
+    switch (ppl) {
+      case 1: LTX_QK_LAUNCH(1, 8); break;
+      case 2: LTX_QK_LAUNCH(2, 8); break;
+      case 4: LTX_QK_LAUNCH(4, 8); break;
+      default: return LTX_ERR_UNSUPPORTED;
+    }
+  } else {
+    switch (ppl) {
+      case 1: LTX_QK_LAUNCH(1, 4); break;
+      case 2: LTX_QK_LAUNCH(2, 4); break;
+      case 4: LTX_QK_LAUNCH(4, 4); break;
+      default: return LTX_ERR_UNSUPPORTED;
+    }
+  }
+#undef LTX_QK_LAUNCH
+  return ltx_launch_status();
+}
+
+extern "C" int ltx_output_norm_modulate_bf16(const void* x, int64_t x_stride, const float* table,
+                                             const float* emb, void* out, int64_t out_stride,
+                                             int64_t rows, int64_t C, float eps, void* stream) {
+  if (rows < 0 || !x || !table || !emb || !out) return LTX_ERR_INVALID_ARG;
+  if (C <= 0 || C % 512 != 0 || C > 4096) return LTX_ERR_UNSUPPORTED;
+  if (x_stride < C || out_stride < C) return LTX_ERR_INVALID_ARG;
+  if (!aligned16(x) || !aligned16(out) || !aligned16(table) || !aligned16(emb) ||
+      x_stride % 8 || out_stride % 8)
+    return LTX_ERR_ALIGNMENT;
+  if (rows == 0) return LTX_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const int grid = row_grid(rows);
+  const bf16* xp = (const bf16*)x;
+  bf16* op = (bf16*)out;
+  switch (C / 512) {
+    case 1: output_norm_kernel<1><<<grid, kRowBlock, 0, s>>>(xp, x_stride, table, emb, op, out_stride, rows, eps); break;
+    case 2: output_norm_kernel<2><<<grid, kRowBlock, 0, s>>>(xp, x_stride, table, emb, op, out_stride, rows, eps); break;
+    case 4: output_norm_kernel<4><<<grid, kRowBlock, 0, s>>>(xp, x_stride, table, emb, op, out_stride, rows, eps); break;
+    case 8: output_norm_kernel<8><<<grid, kRowBlock, 0, s>>>(xp, x_stride, table, emb, op, out_stride, rows, eps); break;
+    default: return LTX_ERR_UNSUPPORTED;
+  }
+  return ltx_launch_status();
+}
+
+extern "C" int ltx_euler_x0_step_bf16(const void* latent, const void* velocity, float sigma,
+                                      float ratio, void* out, int64_t n, void* stream) {
+  if (n < 0 || !latent || !velocity || !out) return LTX_ERR_INVALID_ARG;
+  if (!aligned16(latent) || !aligned16(velocity) || !aligned16(out)) return LTX_ERR_ALIGNMENT;
+  if (n == 0) return LTX_OK;
+  int64_t blocks = (n / 8 + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  if (blocks < 1) blocks = 1;
+  euler_kernel<<<(int)blocks, 256, 0, (hipStream_t)stream>>>(
+      (const bf16*)latent, (const bf16*)velocity, sigma, ratio, (bf16*)out, n);
+  return ltx_launch_status();
+}
+
+extern "C" int ltx_timestep_embedding_f32(const float* values, int64_t count, float multiplier,
+                                          float* out, int64_t dim, void* stream) {
+  if (count < 0 || dim < 2 || !values || !out) return LTX_ERR_INVALID_ARG;
+  if (count == 0) return LTX_OK;
+  const int64_t total = count * dim;
+  timestep_embedding_kernel<<<(int)((total + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+      values, count, multiplier, out, dim);
+  return ltx_launch_status();
+}
+
+extern "C" int ltx_gemv_f32_bf16w(const float* x, int64_t batch, int64_t K, const void* W,
+                                  const float* bias, float* y, int64_t N, int flags,
+                                  void* stream) {
+  if (!x || !W || !y || batch < 0 || N < 0) return LTX_ERR_INVALID_ARG;
+  if (batch > kGemvMaxBatch || K <= 0 || K > kGemvMaxK || K % 8) return LTX_ERR_UNSUPPORTED;
+  if (!aligned16(W)) return LTX_ERR_ALIGNMENT;
+  if (batch == 0 || N == 0) return LTX_OK;
+  const int64_t waves = (N + kGemvRowsPerWave - 1) / kGemvRowsPerWave;
+  const int64_t blocks = (waves + 3) / 4;
+  gemv_kernel<<<(int)blocks, 256, 0, (hipStream_t)stream>>>(x, (int)batch, (int)K,
+                                                            (const bf16*)W, bias, y, N, flags);
+  return ltx_launch_status();
+}

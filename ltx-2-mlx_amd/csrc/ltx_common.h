@@ -1,0 +1,72 @@
+// Shared device helpers for the LTX-2 denoise-path HIP kernels (gfx950 / CDNA4).
+//
+// Every kernel in this library is written for 64-wide wavefronts.  bf16 values
+// are carried as clang's native __bf16; float -> bf16 conversion lowers to the
+// hardware v_cvt_pk_bf16_f32 (round-to-nearest-even), which is the rounding
+// mode of every `.astype(mx.bfloat16)` on the reference path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/ltx_hip.h"
+
+namespace ltx {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf2f(bf16 v) { return (float)v; }
+__device__ __forceinline__ bf16 f2bf(float v) { return (bf16)v; }
+// Round an fp32 value to the nearest bf16 and return it widened again.
+__device__ __forceinline__ float round_bf(float v) { return (float)(bf16)v; }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+// Non-contractible fp32 arithmetic, used where the reference evaluates a
+// product and a sum as two separately rounded operations.
+// `#pragma clang fp contract(off)` keeps the backend from fusing these into
+// an FMA after inlining (HIP compiles with -ffp-contract=fast by default).
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+__device__ __forceinline__ float sub_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a - b;
+}
+
+// Correctly rounded 1/sqrt(v): the reference uses a precise rsqrt for the
+// RMSNorm normalizer.
+__device__ __forceinline__ float rsqrt_rn(float v) { return __frsqrt_rn(v); }
+
+}  // namespace ltx
+
+// Launch-status helper shared by the C entry points.
+static inline int ltx_launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? LTX_OK : LTX_ERR_HIP;
+}

@@ -1,0 +1,119 @@
+"""ctypes binding of libltx_hip.so (declarations mirror include/ltx_hip.h).
+
+The library is loaded lazily on first use.  A missing or unloadable library
+raises immediately: there is no silent CPU or eager fallback behind these
+entry points.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch
+
+LIB_NAME = "libltx_hip.so"
+LIB_PATH = Path(os.environ.get("LTX_HIP_LIB", Path(__file__).with_name(LIB_NAME)))
+
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_f32 = ctypes.c_float
+_vp = ctypes.c_void_p
+
+# name -> argtypes (every function returns int status)
+SIGNATURES: dict[str, list] = {
+    "ltx_version": [],
+    "ltx_adaln_norm_fused_bf16": [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _int, _vp],
+    "ltx_gated_add_fused_bf16": [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _int, _vp],
+    "ltx_qknorm_rope_bf16": [
+        _vp, _i64, _i64, _vp, _vp, _vp,
+        _vp, _i64, _i64, _vp, _vp, _vp,
+        _i64, _i64, _f32, _vp,
+    ],
+    "ltx_output_norm_modulate_bf16": [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _vp],
+    "ltx_euler_x0_step_bf16": [_vp, _vp, _f32, _f32, _vp, _i64, _vp],
+    "ltx_timestep_embedding_f32": [_vp, _i64, _f32, _vp, _i64, _vp],
+    "ltx_gemv_f32_bf16w": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _int, _vp],
+}
+
+# Flag values (include/ltx_hip.h)
+ADALN_ROUND_NORM = 1
+ADALN_NO_NORM = 2
+GATED_ROUND_PRODUCT = 1
+GEMV_SILU_INPUT = 1
+GEMV_SILU_OUTPUT = 2
+
+_LIB: ctypes.CDLL | None = None
+
+
+def lib() -> ctypes.CDLL:
+    """Return the loaded library, loading it on first call."""
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is not built; run `python ltx-2-mlx_amd/build_lib.py` "
+                "(or __graft_entry__.build())"
+            )
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = argtypes
+            fn.restype = ctypes.c_int
+        handle.ltx_status_string.argtypes = [ctypes.c_int]
+        handle.ltx_status_string.restype = ctypes.c_char_p
+        _LIB = handle
+    return _LIB
+
+
+class LtxKernelError(RuntimeError):
+    """A libltx_hip entry point returned a non-zero status."""
+
+    def __init__(self, name: str, status: int, detail: str = ""):
+        msg = lib().ltx_status_string(status).decode()
+        super().__init__(f"{name} failed with status {status} ({msg}){': ' + detail if detail else ''}")
+        self.status = status
+
+
+def call(name: str, *args, detail: str = "") -> None:
+    status = getattr(lib(), name)(*args)
+    if status != 0:
+        raise LtxKernelError(name, status, detail)
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError(f"expected a device tensor, got one on {t.device}")
+    return t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def row_view(t: torch.Tensor, cols: int) -> tuple[torch.Tensor, int]:
+    """Return (tensor, row_stride) such that `t` is seen as (rows, cols) rows
+    of unit column stride.  Copies only if the layout is not row-uniform."""
+    if t.shape[-1] != cols:
+        raise ValueError(f"last dim {t.shape[-1]} != {cols}")
+    if t.dim() == 1:
+        return t.contiguous(), cols
+    if t.stride(-1) == 1:
+        # leading dims must collapse to one uniform stride
+        lead = t.shape[:-1]
+        strides = t.stride()[:-1]
+        row_stride = strides[-1]
+        expect = row_stride
+        ok = True
+        for size, stride in zip(reversed(lead), reversed(strides)):
+            if size != 1 and stride != expect:
+                ok = False
+                break
+            expect = stride * size if size != 1 else expect
+        if ok:
+            return t, row_stride
+    t = t.contiguous()
+    return t, cols
