@@ -159,6 +159,66 @@ int ltx_gemv_f32_bf16w(const float* x, int64_t batch, int64_t K, const void* W,
                        const float* bias, float* y, int64_t N, int flags,
                        void* stream);
 
+/* ---- projection GEMMs ------------------------------------------------------
+ * C[m, n] = epilogue( sum_k A[m, k] * W[n, k] + bias[n] ),
+ * fp32 accumulation on bf16 matrix cores (v_mfma_f32_32x32x16_bf16).
+ * A: bf16 (M, K) row stride lda.  W in nn.Linear layout (N, K), row stride ldw,
+ * as bf16, int8 (+ fp32 per-row scale) or MXFP8 (E4M3 codes + E8M0 scale per
+ * 32 consecutive k, scale row stride ld_scale bytes).  Quantised weights are
+ * dequantised to bf16 exactly per their definition before the bf16 MFMA:
+ *   int8 : w = bf16(fp32(q) * s[n])
+ *   MXFP8: w = bf16(e4m3(q) * 2^(e - 127))
+ * bias: fp32 (N) or NULL.  C: bf16 (M, N) row stride ldc.
+ * Requirements: K % 64 == 0, N % 8 == 0, 16-byte aligned pointers and row
+ * strides.  `epilogue` is one of LTX_GEMM_EPI_* optionally OR-ed with a tile
+ * override (LTX_GEMM_TILE_256 / LTX_GEMM_TILE_128; default: by problem size).
+ * Replaces mx.addmm / nn.Linear (attention.py:425-437, feed_forward.py:91-112)
+ * and mx.quantized_matmul(mode="mxfp8") (loader/transformer_cache.py:177-193).
+ */
+#define LTX_GEMM_EPI_BIAS 0           /* C = bf16(acc + bias) */
+#define LTX_GEMM_EPI_GELU 1           /* C = bf16(gelu_tanh(bf16(acc + bias))) (feed_forward.py:101-102) */
+#define LTX_GEMM_EPI_RESIDUAL 2       /* C = bf16(R + gate * bf16(acc + bias)) (fused_ops.py:345-348) */
+#define LTX_GEMM_EPI_RESIDUAL_ROUND 3 /* C = bf16(R + bf16(gate * bf16(acc + bias))) (transformer.py:387, :484) */
+#define LTX_GEMM_EPI_SIGMOID2 4       /* C = bf16(2 * bf16(sigmoid(bf16(acc + bias)))) (attention.py:563-569) */
+#define LTX_GEMM_TILE_256 (1 << 8)
+#define LTX_GEMM_TILE_128 (2 << 8)
+
+int ltx_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, const float* bias,
+                  void* C, int64_t ldc, int64_t M, int64_t N, int64_t K, int epilogue,
+                  const void* residual, int64_t ldr, const float* gate, void* stream);
+
+int ltx_gemm_w8a16_bf16(const void* A, int64_t lda, const int8_t* Wq, int64_t ldw,
+                        const float* w_scale, const float* bias, void* C, int64_t ldc,
+                        int64_t M, int64_t N, int64_t K, int epilogue, const void* residual,
+                        int64_t ldr, const float* gate, void* stream);
+
+int ltx_gemm_mxfp8_bf16(const void* A, int64_t lda, const uint8_t* Wq, int64_t ldw,
+                        const uint8_t* w_scale, int64_t ld_scale, const float* bias, void* C,
+                        int64_t ldc, int64_t M, int64_t N, int64_t K, int epilogue,
+                        const void* residual, int64_t ldr, const float* gate, void* stream);
+
+/* ---- weight formats (load-time) --------------------------------------------
+ * MXFP8, OCP Microscaling v1.0 with E4M3 elements, blocks of 32 along K and an
+ * E8M0 scale (the storage of loader/transformer_cache.py:1255-1267; codes (N,K)
+ * uint8 are byte-identical to the reference's (N, K/4) uint32 words):
+ *   X = floor(log2(max|w|)) - 8 clamped to [-127, 127] (-127 for a zero block),
+ *   scale = X + 127, code = E4M3(w / 2^X), round-to-nearest-even, saturated to
+ *   +-448.  The reference's own encoder is MLX-internal; this is the OCP rule.
+ * int8 W8A16, symmetric per output channel (defined for the W8A16 GEMMs):
+ *   s[n] = max|w[n,:]| / 127 (fp32), q = clamp(rint(w / s), -127, 127),
+ *   q = 0 for a zero row.  Decode: bf16(fp32(q) * s[n]).
+ * W: bf16 (N, K) row stride ldw.  Decoders write bf16 (N, K) row stride ldo.
+ */
+int ltx_quantize_mxfp8_bf16(const void* W, int64_t ldw, int64_t N, int64_t K, uint8_t* q,
+                            int64_t ldq, uint8_t* scales, int64_t ld_scale, void* stream);
+int ltx_dequantize_mxfp8_bf16(const uint8_t* q, int64_t ldq, const uint8_t* scales,
+                              int64_t ld_scale, int64_t N, int64_t K, void* out, int64_t ldo,
+                              void* stream);
+int ltx_quantize_w8_bf16(const void* W, int64_t ldw, int64_t N, int64_t K, int8_t* q,
+                         int64_t ldq, float* scale, void* stream);
+int ltx_dequantize_w8_bf16(const int8_t* q, int64_t ldq, const float* scale, int64_t N,
+                           int64_t K, void* out, int64_t ldo, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

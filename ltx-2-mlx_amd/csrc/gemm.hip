@@ -1,0 +1,497 @@
+// Projection GEMMs of the DiT block on CDNA4 matrix cores.
+//
+//   C[m, n] = epilogue( sum_k A[m, k] * W[n, k] + bias[n] )
+//
+// A: bf16 activations (M, K) row-major.  W: the weight in its storage layout
+// (N, K) row-major -- nn.Linear's layout -- in one of three formats:
+//   bf16                          (reference: nn.Linear / mx.addmm,
+//                                  attention.py:425-437, feed_forward.py:91-112)
+//   int8 + fp32 per-row scale     (W8A16: w = bf16(fp32(q) * s))
+//   MXFP8: E4M3 codes + E8M0 scale per 32 consecutive k
+//                                 (loader/transformer_cache.py:1255-1267; the
+//                                  reference dequantises to bf16 and runs a bf16
+//                                  MMA, docs/PERFORMANCE_NOTES.md:1450-1470)
+// Both operands are K-contiguous, which is what the MFMA fragments want.
+//
+// Kernel structure (one 256-thread workgroup = 4 waves in a 2x2 grid):
+//   * block tile BM x BN, K step 64, 2 or 4 LDS stages filled by direct
+//     global->LDS DMA (global_load_lds_dwordx4): no staging registers, the
+//     loads of later stages fly while the MFMAs of stage k run; one barrier
+//     per K step.
+//   * quantised weights travel to LDS as their 8-bit codes (half the bytes)
+//     and are dequantised to bf16 as each lane reads its MFMA fragment, with
+//     the exact format arithmetic, so the bf16 MFMA sees bit-exact weights.
+//   * LDS rows are 128 bytes (64 bf16; 64 codes for 8-bit weights); 16-byte
+//     chunks are XOR-swizzled ((row/2)%8, or (row/4)%4 for 64-byte rows) so
+//     the fragment reads of consecutive rows spread over the banks.  The DMA
+//     source address of each lane implements the swizzle.
+//   * fragments of k-step kk+1 are read from LDS before the MFMAs of kk issue.
+//   * v_mfma_f32_32x32x16_bf16 with the weight fragment as the MFMA "A"
+//     operand: each lane then holds 4 consecutive output columns, so the
+//     epilogue packs 4 bf16 per LDS write and streams the tile out through LDS
+//     in coalesced 16-byte chunks, fusing bias, GELU-tanh, the 2*sigmoid head
+//     gate or the gated residual add (fused_ops.py:345-348 semantics).
+//   * blockIdx -> tile: consecutive tiles go to the same XCD (the hardware
+//     round-robins workgroups over the 8 XCDs), grouped 8 tile-rows at a time.
+#include "ltx_common.h"
+
+namespace ltx {
+
+enum BKind { B_BF16 = 0, B_INT8 = 1, B_MXFP8 = 2 };
+
+struct GemmArgs {
+  const bf16* A;
+  int64_t lda;
+  const void* B;
+  int64_t ldb;
+  const void* bscale;  // int8: fp32 (N); mxfp8: uint8 (N, K/32)
+  int64_t ld_scale;    // mxfp8 scale row stride (bytes)
+  const float* bias;   // fp32 (N) or null
+  bf16* C;
+  int64_t ldc;
+  const bf16* R;       // residual (gated epilogues), may alias C
+  int64_t ldr;
+  const float* gate;   // fp32 (N)
+  int M, N, K;
+  int tiles_m, tiles_n;
+};
+
+constexpr int kBK = 64;
+constexpr int kGemmThreads = 256;
+constexpr int kGroupM = 8;
+constexpr int kNumXcd = 8;
+
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
+  const float u = k0 * (x + 0.044715f * x * x * x);
+  return 0.5f * x * (1.0f + tanhf(u));
+}
+
+__device__ __forceinline__ float e8m0_to_f32(uint32_t s) {
+  if (s == 0xffu) return __uint_as_float(0x7fc00000u);
+  if (s == 0u) return __uint_as_float(0x00400000u);  // 2^-127
+  return __uint_as_float(s << 23);
+}
+
+__device__ __forceinline__ void tile_coords(int bid, int nblocks, int tiles_m, int tiles_n, int& tm,
+                                            int& tn) {
+  // XCD-contiguous renumbering: hardware sends block b to XCD b % 8.
+  const int q = nblocks / kNumXcd, r = nblocks % kNumXcd;
+  const int xcd = bid % kNumXcd, idx = bid / kNumXcd;
+  const int logical = xcd * q + (xcd < r ? xcd : r) + idx;
+  // grouped ordering: kGroupM tile-rows sweep the tile-columns together
+  const int per_group = kGroupM * tiles_n;
+  const int group = logical / per_group;
+  const int first_m = group * kGroupM;
+  const int gsize = (tiles_m - first_m) < kGroupM ? (tiles_m - first_m) : kGroupM;
+  const int in_group = logical % per_group;
+  tm = first_m + in_group % gsize;
+  tn = in_group / gsize;
+}
+
+// LDS-DMA helpers: each lane of a wave writes the 16 bytes it loads to
+// `lds_wave_base + 16 * lane`; the per-lane source address implements the
+// swizzle (the data a lane fetches is the data its LDS slot must hold).
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef __attribute__((address_space(1))) const void* gbl_ptr_t;
+
+__device__ __forceinline__ void dma16(const void* src, char* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)lds_wave_base, 16, 0, 0);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int BM, int BN, int BKIND, int EPI>
+struct GemmCfg {
+  static constexpr int WM = BM / 2, WN = BN / 2;    // wave tile (2 x 2 waves)
+  static constexpr int TM = WM / 32, TN = WN / 32;  // 32x32 MFMA tiles per wave
+  static constexpr bool B8 = BKIND != B_BF16;
+  static constexpr int A_ROWB = kBK * 2;             // 128 B per bf16 row
+  static constexpr int B_ROWB = B8 ? kBK : kBK * 2;  // 64 B per 8-bit row
+  static constexpr int A_BYTES = BM * A_ROWB, B_BYTES = BN * B_ROWB;
+  static constexpr int STAGE = A_BYTES + B_BYTES;
+  // MXFP8 scales ride in registers one stage ahead, so that format keeps two
+  // stages; the others use four when they fit.
+  static constexpr int STAGES = (BKIND != B_MXFP8 && 4 * STAGE <= 160 * 1024 - 8192) ? 4 : 2;
+  // per-lane DMA instructions per stage (each wave instruction moves 1 KiB)
+  static constexpr int A_DMA = A_BYTES / 1024 / 4;
+  static constexpr int B_DMA = B_BYTES / 1024 / 4;
+  static constexpr int EPI_ROWB = WN * 2 + 16;  // padded epilogue row
+  static constexpr int EPI_WAVE = WM * EPI_ROWB;
+  static constexpr int EPI_BYTES = 4 * EPI_WAVE;
+  static constexpr int LDS_BYTES = (STAGES * STAGE > EPI_BYTES) ? STAGES * STAGE : EPI_BYTES;
+};
+
+template <int BM, int BN, int BKIND, int EPI>
+__global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
+  using Cfg = GemmCfg<BM, BN, BKIND, EPI>;
+  constexpr int WM = Cfg::WM, WN = Cfg::WN, TM = Cfg::TM, TN = Cfg::TN;
+  constexpr bool B8 = Cfg::B8;
+  constexpr int STAGES = Cfg::STAGES;
+  constexpr int STAGE = Cfg::STAGE;
+  constexpr int A_BYTES = Cfg::A_BYTES;
+  constexpr int A_ROWB = Cfg::A_ROWB, B_ROWB = Cfg::B_ROWB;
+  constexpr int A_DMA = Cfg::A_DMA, B_DMA = Cfg::B_DMA;
+  constexpr int EPI_ROWB = Cfg::EPI_ROWB, EPI_WAVE = Cfg::EPI_WAVE;
+  __shared__ __attribute__((aligned(1024))) char lds[Cfg::LDS_BYTES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  int tmi, tni;
+  tile_coords(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, tmi, tni);
+  const int m0 = tmi * BM, n0 = tni * BN;
+  const int KT = p.K / kBK;
+
+  // ---- DMA source addresses (k = 0).  A: wave instruction i covers tile rows
+  // 8*(4*i + wave) .. +8, lane -> row +lane/8, LDS slot lane%8 which holds
+  // logical chunk (lane%8) ^ ((row/2)%8).
+  const char* a_src[A_DMA];
+#pragma unroll
+  for (int i = 0; i < A_DMA; ++i) {
+    const int r = 8 * (4 * i + wave) + (lane >> 3);
+    int gm = m0 + r;
+    gm = gm < p.M ? gm : p.M - 1;
+    const int chunk = (lane & 7) ^ ((r >> 1) & 7);
+    a_src[i] = (const char*)(p.A + (int64_t)gm * p.lda) + chunk * 16;
+  }
+  // B: bf16 like A; 8-bit rows are 64 B: 16 rows per wave instruction, lane ->
+  // row +lane/4, 16-byte slot lane%4 holding chunk (lane%4) ^ ((row/4)%4).
+  const char* b_src[B_DMA];
+#pragma unroll
+  for (int i = 0; i < B_DMA; ++i) {
+    int r, chunk;
+    if (B8) {
+      r = 16 * (4 * i + wave) + (lane >> 2);
+      chunk = (lane & 3) ^ ((r >> 2) & 3);
+    } else {
+      r = 8 * (4 * i + wave) + (lane >> 3);
+      chunk = (lane & 7) ^ ((r >> 1) & 7);
+    }
+    int gn = n0 + r;
+    gn = gn < p.N ? gn : p.N - 1;
+    b_src[i] = (const char*)p.B + (int64_t)gn * p.ldb * (B8 ? 1 : 2) + chunk * 16;
+  }
+
+  // Per-lane weight rows of the B fragments and their scales.
+  const int frag_r = lane & 31;
+  const int frag_c = lane >> 5;
+  float s_i8[TN];
+  const uint8_t* sc_row[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    int gn = n0 + wn * WN + j * 32 + frag_r;
+    gn = gn < p.N ? gn : p.N - 1;
+    if (BKIND == B_INT8) s_i8[j] = ((const float*)p.bscale)[gn];
+    if (BKIND == B_MXFP8) sc_row[j] = (const uint8_t*)p.bscale + (int64_t)gn * p.ld_scale;
+  }
+  // MXFP8 scales of one stage: 2 E8M0 bytes (k blocks 0/1 of the 64) per row.
+  uint32_t sc_cur[TN], sc_next[TN];
+
+  auto issue_stage = [&](int kt, int buf) {
+    char* As = lds + buf * STAGE;
+    char* Bs = As + A_BYTES;
+    const int64_t ka = (int64_t)kt * kBK * 2;
+#pragma unroll
+    for (int i = 0; i < A_DMA; ++i) dma16(a_src[i] + ka, As + (4 * i + wave) * 1024);
+    const int64_t kb = (int64_t)kt * kBK * (B8 ? 1 : 2);
+#pragma unroll
+    for (int i = 0; i < B_DMA; ++i) dma16(b_src[i] + kb, Bs + (4 * i + wave) * 1024);
+    if (BKIND == B_MXFP8) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        sc_next[j] = *reinterpret_cast<const uint16_t*>(sc_row[j] + kt * 2);
+    }
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  int a_off[TM], b_off[TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) a_off[i] = (wm * WM + i * 32 + frag_r) * A_ROWB;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) b_off[j] = (wn * WN + j * 32 + frag_r) * B_ROWB;
+  const int a_swz = (frag_r >> 1) & 7;  // (row/2)%8 for rows i*32+frag_r
+  const int b_swz = B8 ? ((frag_r >> 2) & 3) : a_swz;
+
+  // prologue: stages 0 .. STAGES-2 in flight
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s) {
+    if (s < KT) issue_stage(s, s);
+    if (BKIND == B_MXFP8 && s == 0) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) sc_cur[j] = sc_next[j];
+    }
+  }
+
+  for (int kt = 0; kt < KT; ++kt) {
+    // wait for stage kt: at most STAGES-2 later stages may still be in flight
+    if (kt + STAGES - 2 < KT) {
+      if constexpr (STAGES == 4) wait_vmcnt<2 * (A_DMA + B_DMA)>();
+      else wait_vmcnt<0>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    __syncthreads();
+    if (BKIND == B_MXFP8) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) sc_cur[j] = sc_next[j];
+    }
+    if (kt + STAGES - 1 < KT) issue_stage(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+    const char* As = lds + (kt % STAGES) * STAGE;
+    const char* Bs = As + A_BYTES;
+    // Fragments of k-step kk+1 are read while the MFMAs of kk run.
+    bf16x8 af[2][TM], bw[2][TN];
+    auto read_frags = [&](int kk, bf16x8* fa, bf16x8* fb) {
+      const int ca = ((kk * 2 + frag_c) ^ a_swz) * 16;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[i] = *reinterpret_cast<const bf16x8*>(As + a_off[i] + ca);
+      if (!B8) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) fb[j] = *reinterpret_cast<const bf16x8*>(Bs + b_off[j] + ca);
+      } else {
+        const int c8 = kk * 2 + frag_c;  // 8-byte chunk of the 64-byte row
+        const int cb = ((c8 >> 1) ^ b_swz) * 16 + (c8 & 1) * 8;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const u32x2 raw = *reinterpret_cast<const u32x2*>(Bs + b_off[j] + cb);
+          uint32_t o[4];
+          if (BKIND == B_INT8) {
+            const float s = s_i8[j], nb = -128.0f * s;
+#pragma unroll
+            for (int d = 0; d < 2; ++d) {
+              const uint32_t u = raw[d] ^ 0x80808080u;
+              bf16x2 p0, p1;
+              p0[0] = (bf16)fmaf((float)(u & 0xffu), s, nb);
+              p0[1] = (bf16)fmaf((float)((u >> 8) & 0xffu), s, nb);
+              p1[0] = (bf16)fmaf((float)((u >> 16) & 0xffu), s, nb);
+              p1[1] = (bf16)fmaf((float)(u >> 24), s, nb);
+              o[2 * d] = __builtin_bit_cast(uint32_t, p0);
+              o[2 * d + 1] = __builtin_bit_cast(uint32_t, p1);
+            }
+          } else {
+            const float sc = e8m0_to_f32((sc_cur[j] >> (8 * (kk >> 1))) & 0xffu);
+#pragma unroll
+            for (int d = 0; d < 2; ++d) {
+              o[2 * d] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[d], sc, false));
+              o[2 * d + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[d], sc, true));
+            }
+          }
+          fb[j] = __builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]});
+        }
+      }
+    };
+    read_frags(0, af[0], bw[0]);
+#pragma unroll
+    for (int kk = 0; kk < kBK / 16; ++kk) {
+      const int cb = kk & 1;
+      // Fence the schedule: fragment reads of step kk+1 are issued before
+      // the MFMAs of step kk, so their LDS latency hides behind 16 MFMAs.
+      if (kk + 1 < kBK / 16) read_frags(kk + 1, af[cb ^ 1], bw[cb ^ 1]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[cb][j], af[cb][i], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  __syncthreads();  // all waves done with the stage buffers before reuse
+
+  // ---- epilogue phase 1: registers -> bf16 tile in LDS (per wave) ----
+  // acc[i][j] reg 4g+e holds C[m][n] with m = i*32 + lane%32 and
+  // n = j*32 + 8g + 4*(lane/32) + e (wave-local coordinates).
+  char* E = lds + wave * EPI_WAVE;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int nl = j * 32 + 8 * g + 4 * frag_c;
+      const int gn = n0 + wn * WN + nl;
+      float bias4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bias4[e] = (p.bias && gn + e < p.N) ? p.bias[gn + e] : 0.0f;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        bf16x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float y = round_bf(acc[i][j][4 * g + e] + bias4[e]);
+          if (EPI == LTX_GEMM_EPI_GELU) y = gelu_tanh(y);
+          if (EPI == LTX_GEMM_EPI_SIGMOID2) y = 2.0f * round_bf(1.0f / (1.0f + expf(-y)));
+          v[e] = (bf16)y;
+        }
+        *reinterpret_cast<bf16x4*>(E + (i * 32 + frag_r) * EPI_ROWB + nl * 2) = v;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- epilogue phase 2: coalesced 16-byte stores (+ gated residual) ----
+  constexpr int CHUNKS = WN / 8;  // 16-byte chunks per wave-tile row
+  constexpr int ROWS_PER_IT = 64 / CHUNKS;
+  const int ch = lane % CHUNKS;
+  const int rsub = lane / CHUNKS;
+  const int gn = n0 + wn * WN + ch * 8;
+  float g8[8];
+  if (EPI == LTX_GEMM_EPI_RESIDUAL || EPI == LTX_GEMM_EPI_RESIDUAL_ROUND) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) g8[e] = gn + e < p.N ? p.gate[gn + e] : 0.0f;
+  }
+  for (int rr = 0; rr < WM; rr += ROWS_PER_IT) {
+    const int ml = rr + rsub;
+    const int gm = m0 + wm * WM + ml;
+    if (gm >= p.M || gn >= p.N) continue;
+    bf16x8 v = *reinterpret_cast<const bf16x8*>(E + ml * EPI_ROWB + ch * 16);
+    if (EPI == LTX_GEMM_EPI_RESIDUAL || EPI == LTX_GEMM_EPI_RESIDUAL_ROUND) {
+      const bf16x8 res = *reinterpret_cast<const bf16x8*>(p.R + (int64_t)gm * p.ldr + gn);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float y = (float)v[e];
+        float o;
+        if (EPI == LTX_GEMM_EPI_RESIDUAL)
+          o = fmaf(g8[e], y, (float)res[e]);
+        else
+          o = round_bf(y * g8[e]) + (float)res[e];
+        v[e] = (bf16)o;
+      }
+    }
+    *reinterpret_cast<bf16x8*>(p.C + (int64_t)gm * p.ldc + gn) = v;
+  }
+}
+
+template <int BM, int BN, int BKIND, int EPI>
+static void launch_tile(GemmArgs p, hipStream_t s) {
+  p.tiles_m = (p.M + BM - 1) / BM;
+  p.tiles_n = (p.N + BN - 1) / BN;
+  gemm_kernel<BM, BN, BKIND, EPI><<<p.tiles_m * p.tiles_n, kGemmThreads, 0, s>>>(p);
+}
+
+template <int BKIND, int EPI>
+static void launch_epi(const GemmArgs& p, int tile, hipStream_t s) {
+  if (tile == 0) {
+    // Large tiles when they still give most CUs a tile; 128x128 otherwise.
+    const int64_t big = (int64_t)((p.M + 255) / 256) * ((p.N + 255) / 256);
+    tile = big >= 160 ? 1 : 2;
+  }
+  if (tile == 1)
+    launch_tile<256, 256, BKIND, EPI>(p, s);
+  else
+    launch_tile<128, 128, BKIND, EPI>(p, s);
+}
+
+template <int BKIND>
+static int launch_kind(const GemmArgs& p, int epilogue, hipStream_t s) {
+  const int epi = epilogue & 0xff;
+  const int tile = (epilogue >> 8) & 0xf;
+  if (tile > 2) return LTX_ERR_INVALID_ARG;
+  switch (epi) {
+    case LTX_GEMM_EPI_BIAS: launch_epi<BKIND, LTX_GEMM_EPI_BIAS>(p, tile, s); break;
+    case LTX_GEMM_EPI_GELU: launch_epi<BKIND, LTX_GEMM_EPI_GELU>(p, tile, s); break;
+    case LTX_GEMM_EPI_RESIDUAL: launch_epi<BKIND, LTX_GEMM_EPI_RESIDUAL>(p, tile, s); break;
+    case LTX_GEMM_EPI_RESIDUAL_ROUND: launch_epi<BKIND, LTX_GEMM_EPI_RESIDUAL_ROUND>(p, tile, s); break;
+    case LTX_GEMM_EPI_SIGMOID2: launch_epi<BKIND, LTX_GEMM_EPI_SIGMOID2>(p, tile, s); break;
+    default: return LTX_ERR_INVALID_ARG;
+  }
+  return ltx_launch_status();
+}
+
+}  // namespace ltx
+
+using namespace ltx;
+
+static inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+static int gemm_check(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc,
+                      int64_t M, int64_t N, int64_t K, int epilogue, const void* R, int64_t ldr,
+                      const float* gate, int b_elem_bytes) {
+  if (!A || !B || !C || M < 0 || N < 0 || K < 0) return LTX_ERR_INVALID_ARG;
+  if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 2) return LTX_ERR_UNSUPPORTED;
+  const int epi = epilogue & 0xff;
+  if ((epi == LTX_GEMM_EPI_RESIDUAL || epi == LTX_GEMM_EPI_RESIDUAL_ROUND) && (!R || !gate || ldr < N))
+    return LTX_ERR_INVALID_ARG;
+  if (K % 64 != 0 || N % 8 != 0) return LTX_ERR_UNSUPPORTED;
+  if (lda < K || ldb < K || ldc < N) return LTX_ERR_INVALID_ARG;
+  if (!al16(A) || !al16(B) || !al16(C) || lda % 8 || ldc % 8 || (ldb * b_elem_bytes) % 16 ||
+      (R && (!al16(R) || ldr % 8)))
+    return LTX_ERR_ALIGNMENT;
+  return LTX_OK;
+}
+
+static GemmArgs make_args(const void* A, int64_t lda, const void* B, int64_t ldb, const void* bscale,
+                          int64_t ld_scale, const float* bias, void* C, int64_t ldc, int64_t M,
+                          int64_t N, int64_t K, const void* R, int64_t ldr, const float* gate) {
+  GemmArgs p;
+  p.A = (const bf16*)A;
+  p.lda = lda;
+  p.B = B;
+  p.ldb = ldb;
+  p.bscale = bscale;
+  p.ld_scale = ld_scale;
+  p.bias = bias;
+  p.C = (bf16*)C;
+  p.ldc = ldc;
+  p.R = (const bf16*)R;
+  p.ldr = ldr;
+  p.gate = gate;
+  p.M = (int)M;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.tiles_m = p.tiles_n = 0;
+  return p;
+}
+
+extern "C" int ltx_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw,
+                             const float* bias, void* C, int64_t ldc, int64_t M, int64_t N,
+                             int64_t K, int epilogue, const void* residual, int64_t ldr,
+                             const float* gate, void* stream) {
+  int st = gemm_check(A, lda, W, ldw, C, ldc, M, N, K, epilogue, residual, ldr, gate, 2);
+  if (st != LTX_OK) return st;
+  if (M == 0 || N == 0) return LTX_OK;
+  if (K == 0) return LTX_ERR_UNSUPPORTED;
+  GemmArgs p = make_args(A, lda, W, ldw, nullptr, 0, bias, C, ldc, M, N, K, residual, ldr, gate);
+  return launch_kind<B_BF16>(p, epilogue, (hipStream_t)stream);
+}
+
+extern "C" int ltx_gemm_w8a16_bf16(const void* A, int64_t lda, const int8_t* Wq, int64_t ldw,
+                                   const float* w_scale, const float* bias, void* C, int64_t ldc,
+                                   int64_t M, int64_t N, int64_t K, int epilogue,
+                                   const void* residual, int64_t ldr, const float* gate,
+                                   void* stream) {
+  int st = gemm_check(A, lda, Wq, ldw, C, ldc, M, N, K, epilogue, residual, ldr, gate, 1);
+  if (st != LTX_OK) return st;
+  if (!w_scale) return LTX_ERR_INVALID_ARG;
+  if (M == 0 || N == 0) return LTX_OK;
+  if (K == 0) return LTX_ERR_UNSUPPORTED;
+  GemmArgs p = make_args(A, lda, Wq, ldw, w_scale, 0, bias, C, ldc, M, N, K, residual, ldr, gate);
+  return launch_kind<B_INT8>(p, epilogue, (hipStream_t)stream);
+}
+
+extern "C" int ltx_gemm_mxfp8_bf16(const void* A, int64_t lda, const uint8_t* Wq, int64_t ldw,
+                                   const uint8_t* w_scale, int64_t ld_scale, const float* bias,
+                                   void* C, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                                   int epilogue, const void* residual, int64_t ldr,
+                                   const float* gate, void* stream) {
+  int st = gemm_check(A, lda, Wq, ldw, C, ldc, M, N, K, epilogue, residual, ldr, gate, 1);
+  if (st != LTX_OK) return st;
+  if (!w_scale || ld_scale < K / 32) return LTX_ERR_INVALID_ARG;
+  if (M == 0 || N == 0) return LTX_OK;
+  if (K == 0) return LTX_ERR_UNSUPPORTED;
+  GemmArgs p = make_args(A, lda, Wq, ldw, w_scale, ld_scale, bias, C, ldc, M, N, K, residual, ldr,
+                         gate);
+  return launch_kind<B_MXFP8>(p, epilogue, (hipStream_t)stream);
+}

@@ -1,0 +1,208 @@
+// Weight formats of the quantised projections: encoders and bf16 decoders.
+//
+// MXFP8 (OCP Microscaling v1.0, element E4M3, block 32 along K, scale E8M0):
+//   the storage of LTX_2_MLX's `mx.quantize(W, 32, 8, mode="mxfp8")`
+//   (loader/transformer_cache.py:1255-1267): codes (N, K) uint8 -- the same
+//   bytes as the reference's (N, K/4) uint32 words -- and scales (N, K/32).
+//   The reference's encoder is MLX-internal; this one follows the OCP rule:
+//     X = floor(log2(max|w|)) - 8 (8 = E4M3 emax), clamped to [-127, 127],
+//     scale byte = X + 127, code = E4M3(w / 2^X) rounded to nearest-even and
+//     saturated to +-448.  An all-zero block gets X = -127.
+// int8 W8A16 (per output channel, symmetric):
+//     s[n] = max_k |w[n,k]| / 127 (fp32), q = clamp(rint(w / s), -127, 127);
+//     a zero row has s = 0 and q = 0.  Decode: w' = bf16(fp32(q) * s).
+#include "ltx_common.h"
+
+namespace ltx {
+
+__device__ __forceinline__ uint32_t e4m3_encode_sat(float v) {
+  const uint32_t sign = (__float_as_uint(v) >> 24) & 0x80u;
+  const float a = fabsf(v);
+  if (a != a) return 0x7Fu | sign;  // NaN
+  if (a >= 448.0f) return 0x7Eu | sign;
+  if (a < 0.015625f) {  // below 2^-6: subnormal steps of 2^-9 (8 -> min normal)
+    return sign | (uint32_t)rintf(a * 512.0f);
+  }
+  int e;
+  frexpf(a, &e);
+  int E = e - 1;  // a in [2^E, 2^(E+1))
+  float m = rintf(ldexpf(a, 3 - E));  // [8, 16]
+  if (m == 16.0f) {
+    E += 1;
+    m = 8.0f;
+  }
+  uint32_t code = ((uint32_t)(E + 7) << 3) | ((uint32_t)m - 8u);
+  if (code > 0x7Eu) code = 0x7Eu;
+  return sign | code;
+}
+
+// One thread per 32-element block.
+__global__ void mxfp8_quantize_kernel(const bf16* __restrict__ W, int64_t ldw, int64_t N,
+                                      int64_t K, uint8_t* __restrict__ q, int64_t ldq,
+                                      uint8_t* __restrict__ sc, int64_t lds) {
+  const int64_t nb = K / 32;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= N * nb) return;
+  const int64_t n = idx / nb, b = idx % nb;
+  const bf16* src = W + n * ldw + b * 32;
+  float v[32];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; i += 8) {
+    bf16x8 x = *reinterpret_cast<const bf16x8*>(src + i);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      v[i + e] = (float)x[e];
+      amax = fmaxf(amax, fabsf(v[i + e]));
+    }
+  }
+  int X = -127;
+  if (amax > 0.0f) {
+    int e;
+    frexpf(amax, &e);
+    X = (e - 1) - 8;
+    X = X < -127 ? -127 : (X > 127 ? 127 : X);
+  }
+  sc[n * lds + b] = (uint8_t)(X + 127);
+  uint32_t words[8];
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) word |= e4m3_encode_sat(ldexpf(v[4 * w + e], -X)) << (8 * e);
+    words[w] = word;
+  }
+  uint8_t* dst = q + n * ldq + b * 32;
+  *reinterpret_cast<u32x4*>(dst) = u32x4{words[0], words[1], words[2], words[3]};
+  *reinterpret_cast<u32x4*>(dst + 16) = u32x4{words[4], words[5], words[6], words[7]};
+}
+
+__global__ void mxfp8_dequantize_kernel(const uint8_t* __restrict__ q, int64_t ldq,
+                                        const uint8_t* __restrict__ sc, int64_t lds, int64_t N,
+                                        int64_t K, bf16* __restrict__ out, int64_t ldo) {
+  const int64_t per_row = K / 8;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= N * per_row) return;
+  const int64_t n = idx / per_row, c = idx % per_row;
+  const u32x2 raw = *reinterpret_cast<const u32x2*>(q + n * ldq + c * 8);
+  const uint32_t s = sc[n * lds + (c * 8) / 32];
+  const float scale = s == 0xffu ? __uint_as_float(0x7fc00000u)
+                                 : (s == 0u ? __uint_as_float(0x00400000u) : __uint_as_float(s << 23));
+  uint32_t o[4];
+#pragma unroll
+  for (int d = 0; d < 2; ++d) {
+    o[2 * d] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[d], scale, false));
+    o[2 * d + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[d], scale, true));
+  }
+  *reinterpret_cast<u32x4*>(out + n * ldo + c * 8) = u32x4{o[0], o[1], o[2], o[3]};
+}
+
+// One wave per row.
+__global__ __launch_bounds__(256) void w8_quantize_kernel(const bf16* __restrict__ W, int64_t ldw,
+                                                          int64_t N, int64_t K,
+                                                          int8_t* __restrict__ q, int64_t ldq,
+                                                          float* __restrict__ scale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const bf16* row = W + n * ldw;
+  float amax = 0.0f;
+  for (int64_t k = lane * 8; k < K; k += 512) {
+    bf16x8 x = *reinterpret_cast<const bf16x8*>(row + k);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf((float)x[e]));
+  }
+  amax = wave_max(amax);
+  const float s = __fdiv_rn(amax, 127.0f);
+  if (lane == 0) scale[n] = s;
+  int8_t* qrow = q + n * ldq;
+  for (int64_t k = lane * 8; k < K; k += 512) {
+    bf16x8 x = *reinterpret_cast<const bf16x8*>(row + k);
+    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float r = s > 0.0f ? rintf(__fdiv_rn((float)x[e], s)) : 0.0f;
+      r = fminf(fmaxf(r, -127.0f), 127.0f);
+      const uint32_t b = (uint32_t)((int32_t)r & 0xff);
+      if (e < 4) w0 |= b << (8 * e); else w1 |= b << (8 * (e - 4));
+    }
+    *reinterpret_cast<u32x2*>(qrow + k) = u32x2{w0, w1};
+  }
+}
+
+__global__ void w8_dequantize_kernel(const int8_t* __restrict__ q, int64_t ldq,
+                                     const float* __restrict__ scale, int64_t N, int64_t K,
+                                     bf16* __restrict__ out, int64_t ldo) {
+  const int64_t per_row = K / 8;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= N * per_row) return;
+  const int64_t n = idx / per_row, c = idx % per_row;
+  const u32x2 raw = *reinterpret_cast<const u32x2*>(q + n * ldq + c * 8);
+  const float s = scale[n];
+  bf16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int32_t v = (int32_t)(int8_t)((raw[e / 4] >> (8 * (e % 4))) & 0xffu);
+    o[e] = (bf16)mul_rn((float)v, s);
+  }
+  *reinterpret_cast<bf16x8*>(out + n * ldo + c * 8) = o;
+}
+
+}  // namespace ltx
+
+using namespace ltx;
+
+static inline bool a16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+extern "C" int ltx_quantize_mxfp8_bf16(const void* W, int64_t ldw, int64_t N, int64_t K,
+                                       uint8_t* q, int64_t ldq, uint8_t* scales, int64_t ld_scale,
+                                       void* stream) {
+  if (!W || !q || !scales || N < 0 || K < 0) return LTX_ERR_INVALID_ARG;
+  if (K % 32) return LTX_ERR_UNSUPPORTED;
+  if (ldw < K || ldq < K || ld_scale < K / 32) return LTX_ERR_INVALID_ARG;
+  if (!a16(W) || !a16(q) || ldw % 8 || ldq % 16) return LTX_ERR_ALIGNMENT;
+  const int64_t total = N * (K / 32);
+  if (total == 0) return LTX_OK;
+  mxfp8_quantize_kernel<<<(int)((total + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+      (const bf16*)W, ldw, N, K, q, ldq, scales, ld_scale);
+  return ltx_launch_status();
+}
+
+extern "C" int ltx_dequantize_mxfp8_bf16(const uint8_t* q, int64_t ldq, const uint8_t* scales,
+                                         int64_t ld_scale, int64_t N, int64_t K, void* out,
+                                         int64_t ldo, void* stream) {
+  if (!q || !scales || !out || N < 0 || K < 0) return LTX_ERR_INVALID_ARG;
+  if (K % 32) return LTX_ERR_UNSUPPORTED;
+  if (ldq < K || ldo < K || ld_scale < K / 32) return LTX_ERR_INVALID_ARG;
+  if (!a16(out) || (uintptr_t)q % 8 || ldq % 8 || ldo % 8) return LTX_ERR_ALIGNMENT;
+  const int64_t total = N * (K / 8);
+  if (total == 0) return LTX_OK;
+  mxfp8_dequantize_kernel<<<(int)((total + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+      q, ldq, scales, ld_scale, N, K, (bf16*)out, ldo);
+  return ltx_launch_status();
+}
+
+extern "C" int ltx_quantize_w8_bf16(const void* W, int64_t ldw, int64_t N, int64_t K, int8_t* q,
+                                    int64_t ldq, float* scale, void* stream) {
+  if (!W || !q || !scale || N < 0 || K < 0) return LTX_ERR_INVALID_ARG;
+  if (K % 8) return LTX_ERR_UNSUPPORTED;
+  if (ldw < K || ldq < K) return LTX_ERR_INVALID_ARG;
+  if (!a16(W) || (uintptr_t)q % 8 || ldw % 8 || ldq % 8) return LTX_ERR_ALIGNMENT;
+  if (N == 0) return LTX_OK;
+  w8_quantize_kernel<<<(int)((N + 3) / 4), 256, 0, (hipStream_t)stream>>>((const bf16*)W, ldw, N,
+                                                                        K, q, ldq, scale);
+  return ltx_launch_status();
+}
+
+extern "C" int ltx_dequantize_w8_bf16(const int8_t* q, int64_t ldq, const float* scale, int64_t N,
+                                      int64_t K, void* out, int64_t ldo, void* stream) {
+  if (!q || !scale || !out || N < 0 || K < 0) return LTX_ERR_INVALID_ARG;
+  if (K % 8) return LTX_ERR_UNSUPPORTED;
+  if (ldq < K || ldo < K) return LTX_ERR_INVALID_ARG;
+  if (!a16(out) || (uintptr_t)q % 8 || ldq % 8 || ldo % 8) return LTX_ERR_ALIGNMENT;
+  const int64_t total = N * (K / 8);
+  if (total == 0) return LTX_OK;
+  w8_dequantize_kernel<<<(int)((total + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+      q, ldq, scale, N, K, (bf16*)out, ldo);
+  return ltx_launch_status();
+}

@@ -35,6 +35,13 @@ SIGNATURES: dict[str, list] = {
     "ltx_euler_x0_step_bf16": [_vp, _vp, _f32, _f32, _vp, _i64, _vp],
     "ltx_timestep_embedding_f32": [_vp, _i64, _f32, _vp, _i64, _vp],
     "ltx_gemv_f32_bf16w": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _int, _vp],
+    "ltx_gemm_bf16": [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64, _vp, _vp],
+    "ltx_gemm_w8a16_bf16": [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64, _vp, _vp],
+    "ltx_gemm_mxfp8_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64, _vp, _vp],
+    "ltx_quantize_mxfp8_bf16": [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp],
+    "ltx_dequantize_mxfp8_bf16": [_vp, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _vp],
+    "ltx_quantize_w8_bf16": [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp],
+    "ltx_dequantize_w8_bf16": [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp],
 }
 
 # Flag values (include/ltx_hip.h)
@@ -43,6 +50,13 @@ ADALN_NO_NORM = 2
 GATED_ROUND_PRODUCT = 1
 GEMV_SILU_INPUT = 1
 GEMV_SILU_OUTPUT = 2
+GEMM_EPI_BIAS = 0
+GEMM_EPI_GELU = 1
+GEMM_EPI_RESIDUAL = 2
+GEMM_EPI_RESIDUAL_ROUND = 3
+GEMM_EPI_SIGMOID2 = 4
+GEMM_TILE_256 = 1 << 8
+GEMM_TILE_128 = 2 << 8
 
 _LIB: ctypes.CDLL | None = None
 

@@ -1,0 +1,168 @@
+"""Projection GEMMs: ``y = epilogue(x @ W.T + b)`` on gfx950 matrix cores.
+
+One entry point, :func:`linear`, for the three resident weight formats of
+:class:`LinearWeight` (bf16, int8 W8A16, MXFP8).  It replaces ``nn.Linear`` /
+``mx.addmm`` (model/transformer/attention.py:425-437,
+feed_forward.py:91-112) and ``mx.quantized_matmul`` for the mxfp8 cache
+(loader/transformer_cache.py:177-193).  The epilogues fuse what the reference
+evaluates right after the projection:
+
+* ``EPI_BIAS``            ``bf16(x W^T + b)``
+* ``EPI_GELU``            ``bf16(gelu_tanh(bf16(x W^T + b)))`` (feed_forward.py:101-102)
+* ``EPI_RESIDUAL``        ``bf16(res + gate * bf16(x W^T + b))``, the gated residual add
+                          of fused_ops.py:345-348 / transformer.py:598, :625
+* ``EPI_RESIDUAL_ROUND``  ``bf16(res + bf16(gate * bf16(x W^T + b)))`` (transformer.py:387, :484)
+* ``EPI_SIGMOID2``        ``bf16(2 * bf16(sigmoid(bf16(x W^T + b))))``, the per-head gate
+                          (attention.py:563-569)
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from .. import _lib
+
+EPI_BIAS = _lib.GEMM_EPI_BIAS
+EPI_GELU = _lib.GEMM_EPI_GELU
+EPI_RESIDUAL = _lib.GEMM_EPI_RESIDUAL
+EPI_RESIDUAL_ROUND = _lib.GEMM_EPI_RESIDUAL_ROUND
+EPI_SIGMOID2 = _lib.GEMM_EPI_SIGMOID2
+TILE_AUTO, TILE_256, TILE_128 = 0, 1, 2
+
+FORMATS = ("bf16", "int8", "mxfp8")
+
+
+@dataclass
+class LinearWeight:
+    """A projection weight resident in HBM.
+
+    ``w`` is (N, K) in nn.Linear layout: bf16, int8 codes, or E4M3 codes
+    (uint8).  ``scale`` is fp32 (N) for int8 and E8M0 uint8 (N, K/32) for
+    mxfp8.  ``bias`` is fp32 (N) or None.
+    """
+
+    kind: str
+    w: torch.Tensor
+    scale: torch.Tensor | None = None
+    bias: torch.Tensor | None = None
+
+    @property
+    def out_features(self) -> int:
+        return self.w.shape[0]
+
+    @property
+    def in_features(self) -> int:
+        return self.w.shape[1]
+
+    def nbytes(self) -> int:
+        n = self.w.numel() * self.w.element_size()
+        for t in (self.scale, self.bias):
+            if t is not None:
+                n += t.numel() * t.element_size()
+        return n
+
+
+def _quantize(kind: str, w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    n, k = w.shape
+    w = w.contiguous()
+    stream = _lib.stream_of(w)
+    if kind == "int8":
+        q = torch.empty((n, k), dtype=torch.int8, device=w.device)
+        s = torch.empty((n,), dtype=torch.float32, device=w.device)
+        _lib.call("ltx_quantize_w8_bf16", w.data_ptr(), k, n, k, q.data_ptr(), k, s.data_ptr(), stream,
+                  detail=f"N={n} K={k}")
+        return q, s
+    if kind == "mxfp8":
+        q = torch.empty((n, k), dtype=torch.uint8, device=w.device)
+        s = torch.empty((n, k // 32), dtype=torch.uint8, device=w.device)
+        _lib.call("ltx_quantize_mxfp8_bf16", w.data_ptr(), k, n, k, q.data_ptr(), k, s.data_ptr(), k // 32,
+                  stream, detail=f"N={n} K={k}")
+        return q, s
+    raise ValueError(f"unknown quantised format {kind!r}")
+
+
+def make_weight(w: torch.Tensor, bias: torch.Tensor | None = None, kind: str = "bf16") -> LinearWeight:
+    """Build a resident weight from a bf16 (N, K) device tensor.
+
+    ``kind="int8"`` / ``"mxfp8"`` quantise on the device with the library's
+    encoders (include/ltx_hip.h "weight formats").
+    """
+    if w.dtype != torch.bfloat16 or w.dim() != 2 or not w.is_cuda:
+        raise ValueError("make_weight expects a 2-D bf16 device tensor")
+    b = None if bias is None else bias.detach().to(device=w.device, dtype=torch.float32).contiguous()
+    if kind == "bf16":
+        return LinearWeight("bf16", w.contiguous(), None, b)
+    q, s = _quantize(kind, w)
+    return LinearWeight(kind, q, s, b)
+
+
+def dequantize(weight: LinearWeight) -> torch.Tensor:
+    """bf16 (N, K) values of a weight, decoded exactly per its format."""
+    n, k = weight.w.shape
+    if weight.kind == "bf16":
+        return weight.w
+    out = torch.empty((n, k), dtype=torch.bfloat16, device=weight.w.device)
+    stream = _lib.stream_of(out)
+    if weight.kind == "int8":
+        _lib.call("ltx_dequantize_w8_bf16", weight.w.data_ptr(), k, weight.scale.data_ptr(), n, k,
+                  out.data_ptr(), k, stream)
+    else:
+        _lib.call("ltx_dequantize_mxfp8_bf16", weight.w.data_ptr(), k, weight.scale.data_ptr(), k // 32, n, k,
+                  out.data_ptr(), k, stream)
+    return out
+
+
+def linear(x: torch.Tensor, weight: LinearWeight, *, epilogue: int = EPI_BIAS,
+           out: torch.Tensor | None = None, residual: torch.Tensor | None = None,
+           gate: torch.Tensor | None = None, tile: int = TILE_AUTO) -> torch.Tensor:
+    """``epilogue(x @ W.T + b)`` for x (..., K) bf16; returns (..., N) bf16.
+
+    For the residual epilogues, ``residual`` (..., N) bf16 and ``gate`` fp32
+    (N) are required; ``out`` may be ``residual`` itself (in-place update).
+    """
+    k = weight.in_features
+    n = weight.out_features
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"linear expects bf16 activations, got {x.dtype}")
+    xv, lda = _lib.row_view(x, k)
+    m = x.numel() // k
+    lead = x.shape[:-1]
+    if out is None:
+        out = torch.empty((*lead, n), dtype=torch.bfloat16, device=x.device)
+    ov, ldc = _lib.row_view(out, n)
+    if ov.data_ptr() != out.data_ptr():
+        raise ValueError("out must be a row-strided view")
+    rptr, ldr, gptr = None, 0, None
+    if epilogue in (EPI_RESIDUAL, EPI_RESIDUAL_ROUND):
+        if residual is None or gate is None:
+            raise ValueError("residual epilogues need residual and gate")
+        rv, ldr = _lib.row_view(residual, n)
+        if rv.data_ptr() != residual.data_ptr():
+            raise ValueError("residual must be a row-strided view")
+        rptr = rv.data_ptr()
+        g = gate.reshape(-1)
+        if g.dtype != torch.float32 or g.numel() != n:
+            raise ValueError("gate must be fp32 with N elements")
+        gate = g.contiguous()
+        gptr = gate.data_ptr()
+    flags = epilogue | (tile << 8)
+    bias = weight.bias
+    bptr = None if bias is None else bias.data_ptr()
+    stream = _lib.stream_of(x)
+    detail = f"{weight.kind} M={m} N={n} K={k} epi={epilogue}"
+    if weight.kind == "bf16":
+        _lib.call("ltx_gemm_bf16", xv.data_ptr(), lda, weight.w.data_ptr(), weight.w.stride(0), bptr,
+                  ov.data_ptr(), ldc, m, n, k, flags, rptr, ldr, gptr, stream, detail=detail)
+    elif weight.kind == "int8":
+        _lib.call("ltx_gemm_w8a16_bf16", xv.data_ptr(), lda, weight.w.data_ptr(), weight.w.stride(0),
+                  weight.scale.data_ptr(), bptr, ov.data_ptr(), ldc, m, n, k, flags, rptr, ldr, gptr, stream,
+                  detail=detail)
+    elif weight.kind == "mxfp8":
+        _lib.call("ltx_gemm_mxfp8_bf16", xv.data_ptr(), lda, weight.w.data_ptr(), weight.w.stride(0),
+                  weight.scale.data_ptr(), weight.scale.stride(0), bptr, ov.data_ptr(), ldc, m, n, k, flags,
+                  rptr, ldr, gptr, stream, detail=detail)
+    else:
+        raise ValueError(f"unknown weight format {weight.kind!r}")
+    return out

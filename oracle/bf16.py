@@ -12,7 +12,7 @@ import numpy as np
 
 def bf16r(a) -> np.ndarray:
     """Round to the nearest bf16 (ties to even); returns float32 values."""
-    a = np.ascontiguousarray(a, dtype=np.float32)
+    a = np.array(a, dtype=np.float32, order="C")  # keeps 0-d inputs 0-d
     bits = a.view(np.uint32).astype(np.uint64)
     lsb = (bits >> 16) & 1
     rounded = (bits + 0x7FFF + lsb) & 0xFFFF0000

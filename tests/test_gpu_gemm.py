@@ -1,0 +1,202 @@
+"""GPU parity of the weight-format kernels and the projection GEMMs.
+
+* Encoders/decoders: bit-exact against the oracle (oracle/quant.py).
+* In-GEMM dequantisation: bit-exact, shown with A = identity, for which
+  C = I @ W'^T is exactly the decoded weight transposed.
+* GEMM + epilogues: bf16 tolerance against the fp32-accumulating oracle --
+  normwise max relative error <= 1e-2 (the north-star bf16 gate), cosine >=
+  0.9999 and >= 90 % of outputs bit-identical (the remainder differ by the
+  fp32 summation order moving a value across a bf16 rounding boundary).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _util import bf16_from_torch, cos_sim, max_rel_err, ulp_diff_bf16
+from oracle import quant as oq
+from oracle.bf16 import bf16r
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _bf(rng, shape, scale=1.0):
+    return bf16r(rng.standard_normal(shape).astype(np.float32) * np.float32(scale))
+
+
+def _t(a, dtype=torch.bfloat16):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dtype).to(DEV)
+
+
+def _weight_matrix(rng, n, k):
+    W = _bf(rng, (n, k), 0.02)
+    W[1] = 0.0                       # zero row / zero blocks
+    W[2, :64] = bf16r(np.linspace(-3, 3, 64, dtype=np.float32))  # wide range
+    W[3, 32:64] = 0.0
+    return W
+
+
+def test_int8_encoder_and_decoder_bitexact():
+    from ltx_amd.kernels import gemm
+
+    rng = np.random.default_rng(0)
+    W = _weight_matrix(rng, 512, 4096)
+    wt = gemm.make_weight(_t(W), kind="int8")
+    torch.cuda.synchronize()
+    q, s = oq.int8_quantize(W)
+    np.testing.assert_array_equal(wt.scale.cpu().numpy(), s)
+    np.testing.assert_array_equal(wt.w.cpu().numpy(), q)
+    deq = bf16_from_torch(gemm.dequantize(wt))
+    np.testing.assert_array_equal(deq, oq.int8_dequantize(q, s))
+
+
+def test_mxfp8_encoder_and_decoder_bitexact():
+    from ltx_amd.kernels import gemm
+
+    rng = np.random.default_rng(1)
+    W = _weight_matrix(rng, 512, 4096)
+    W[4, :32] = bf16r(np.array([448.0 * 2 ** -3] + [1e-3] * 31, np.float32))
+    wt = gemm.make_weight(_t(W), kind="mxfp8")
+    torch.cuda.synchronize()
+    codes, scales = oq.mxfp8_quantize(W)
+    np.testing.assert_array_equal(wt.scale.cpu().numpy(), scales)
+    np.testing.assert_array_equal(wt.w.cpu().numpy(), codes)
+    deq = bf16_from_torch(gemm.dequantize(wt))
+    np.testing.assert_array_equal(deq, oq.mxfp8_dequantize(codes, scales))
+
+
+def test_mxfp8_decoder_all_codes_bitexact():
+    """Every E4M3 code under a spread of E8M0 scales decodes exactly."""
+    from ltx_amd import _lib
+
+    codes = np.tile(np.arange(256, dtype=np.uint8), 8).reshape(64, 32)  # 64 blocks
+    scales = np.array([127, 128, 126, 100, 150, 60, 200, 1] * 8, np.uint8).reshape(64, 1)
+    ct, st = _t(codes, torch.uint8), _t(scales, torch.uint8)
+    out = torch.empty((64, 32), dtype=torch.bfloat16, device=DEV)
+    _lib.call("ltx_dequantize_mxfp8_bf16", ct.data_ptr(), 32, st.data_ptr(), 1, 64, 32, out.data_ptr(), 32,
+              _lib.stream_of(out))
+    got = bf16_from_torch(out)
+    ref = oq.mxfp8_dequantize(codes, scales)
+    finite = ~np.isnan(ref)
+    np.testing.assert_array_equal(got[finite], ref[finite])
+    assert np.isnan(got[~finite]).all()
+
+
+@pytest.mark.parametrize("kind", ["bf16", "int8", "mxfp8"])
+@pytest.mark.parametrize("tile", [1, 2])
+def test_gemm_identity_returns_decoded_weight(kind, tile):
+    """C = I @ W'^T: each output is one product 1.0 * w' plus exact zeros."""
+    from ltx_amd.kernels import gemm
+
+    rng = np.random.default_rng(2)
+    K, N = 512, 384
+    W = _weight_matrix(rng, N, K)
+    wt = gemm.make_weight(_t(W), kind=kind)
+    eye = torch.eye(K, dtype=torch.bfloat16, device=DEV)
+    out = gemm.linear(eye, wt, tile=tile)
+    deq = gemm.dequantize(wt)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bf16_from_torch(out), bf16_from_torch(deq).T)
+
+
+def _decoded(kind, W):
+    if kind == "bf16":
+        return W
+    if kind == "int8":
+        return oq.int8_dequantize(*oq.int8_quantize(W))
+    return oq.mxfp8_dequantize(*oq.mxfp8_quantize(W))
+
+
+def _check(got, ref, min_exact=0.9):
+    assert max_rel_err(got, ref) <= 1e-2
+    assert cos_sim(got, ref) >= 0.9999
+    assert (ulp_diff_bf16(got, ref) == 0).mean() >= min_exact
+
+
+@pytest.mark.parametrize("kind", ["bf16", "int8", "mxfp8"])
+@pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 16384), (16384, 4096)])
+def test_gemm_block_shapes(kind, K, N):
+    """The projection shapes of one video block at M = 3456 tokens."""
+    from ltx_amd.kernels import gemm
+
+    rng = np.random.default_rng(K + N)
+    M = 3456
+    x = _bf(rng, (M, K))
+    W = _bf(rng, (N, K), 0.02)
+    b = bf16r(rng.standard_normal(N).astype(np.float32) * 0.02)
+    wt = gemm.make_weight(_t(W), _t(b, torch.float32), kind=kind)
+    out = gemm.linear(_t(x), wt)
+    torch.cuda.synchronize()
+    ref = oq.linear(x, _decoded(kind, W), b)
+    _check(bf16_from_torch(out), ref)
+
+
+@pytest.mark.parametrize("epi", ["gelu", "sigmoid2", "residual", "residual_round"])
+@pytest.mark.parametrize("tile", [1, 2])
+def test_gemm_epilogues(epi, tile):
+    from ltx_amd.kernels import gemm
+
+    codes = {"gelu": gemm.EPI_GELU, "sigmoid2": gemm.EPI_SIGMOID2, "residual": gemm.EPI_RESIDUAL,
+             "residual_round": gemm.EPI_RESIDUAL_ROUND}
+    rng = np.random.default_rng(3)
+    M, K, N = 700, 1024, 1536
+    x = _bf(rng, (M, K))
+    W = _bf(rng, (N, K), 0.05)
+    b = rng.standard_normal(N).astype(np.float32) * 0.1
+    res = _bf(rng, (M, N))
+    g = rng.standard_normal(N).astype(np.float32) * 0.5
+    wt = gemm.make_weight(_t(W), _t(b, torch.float32))
+    rt, gt = _t(res), _t(g, torch.float32)
+    if epi.startswith("residual"):  # in place on the residual stream
+        out = gemm.linear(_t(x), wt, epilogue=codes[epi], out=rt, residual=rt, gate=gt, tile=tile)
+        assert out.data_ptr() == rt.data_ptr()
+    else:
+        out = gemm.linear(_t(x), wt, epilogue=codes[epi], tile=tile)
+    torch.cuda.synchronize()
+    ref = oq.linear(x, W, b, epilogue=epi, residual=res, gate=g)
+    _check(bf16_from_torch(out), ref, min_exact=0.85)
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 4096), (68, 2048, 2048), (68, 2048, 6144), (256, 4096, 8192),
+                                   (3456, 4096, 32), (3456, 4096, 128), (3456, 128, 4096), (130, 64, 8)])
+def test_gemm_edge_shapes(M, K, N):
+    from ltx_amd.kernels import gemm
+
+    rng = np.random.default_rng(M + K + N)
+    x = _bf(rng, (M, K))
+    W = _bf(rng, (N, K), 0.03)
+    b = rng.standard_normal(N).astype(np.float32) * 0.02
+    wt = gemm.make_weight(_t(W), _t(b, torch.float32))
+    out = gemm.linear(_t(x), wt)
+    torch.cuda.synchronize()
+    _check(bf16_from_torch(out), oq.linear(x, W, b))
+
+
+def test_gemm_strided_operands():
+    """A and C as column slices of wider row-major buffers (fused QKV layout)."""
+    from ltx_amd.kernels import gemm
+
+    rng = np.random.default_rng(4)
+    M, K, N = 1000, 2048, 1024
+    big_x = _bf(rng, (M, 3 * K))
+    W = _bf(rng, (N, K), 0.03)
+    wt = gemm.make_weight(_t(W))
+    xt = _t(big_x)
+    outbuf = torch.zeros((M, 3 * N), dtype=torch.bfloat16, device=DEV)
+    gemm.linear(xt[:, K:2 * K], wt, out=outbuf[:, 2 * N:])
+    torch.cuda.synchronize()
+    got = bf16_from_torch(outbuf)
+    _check(got[:, 2 * N:], oq.linear(big_x[:, K:2 * K], W))
+    assert not got[:, :2 * N].any()
+
+
+def test_gemm_rejects_bad_shapes():
+    from ltx_amd import _lib
+    from ltx_amd.kernels import gemm
+
+    wt = gemm.make_weight(torch.zeros((64, 100 * 0 + 96), dtype=torch.bfloat16, device=DEV))
+    with pytest.raises(_lib.LtxKernelError):  # K = 96 is not a multiple of 64
+        gemm.linear(torch.zeros((4, 96), dtype=torch.bfloat16, device=DEV), wt)
