@@ -219,6 +219,28 @@ int ltx_quantize_w8_bf16(const void* W, int64_t ldw, int64_t N, int64_t K, int8_
 int ltx_dequantize_w8_bf16(const int8_t* q, int64_t ldq, const float* scale, int64_t N,
                            int64_t K, void* out, int64_t ldo, void* stream);
 
+/* ---- attention ---------------------------------------------------------------
+ * Flash attention with the per-head output gate fused (replaces
+ * attention.py:283-302 -> kernels/steel_attention.py:251-280 and the gate of
+ * attention.py:594-598):
+ *   O[q, h*dh + :] = bf16( bf16( softmax_k(Q_h[q] . K_h[k] * scale) V_h ) * gate[q, h] )
+ * bf16 inputs, fp32 scores, online softmax and accumulation, bf16 P for the
+ * second product; no mask (the reference's T2V calls pass none,
+ * pipelines/common.py:242-252).
+ * Q (Tq, H*head_dim), K (Tk, H*head_dim), O (Tq, H*head_dim): token-major
+ * rows with row strides q_rs/k_rs/o_rs (elements), head h at columns
+ * [h*head_dim, (h+1)*head_dim).  V is passed pre-transposed as Vt (H,
+ * head_dim, tk_pad), produced by ltx_attn_transpose_v_bf16.  gate: bf16 (Tq, H)
+ * with row stride gate_rs, or NULL.  head_dim in {64, 128}.
+ */
+int64_t ltx_attn_vt_padded_len(int64_t Tk);
+int ltx_attn_transpose_v_bf16(const void* V, int64_t v_rs, int64_t Tk, int64_t H,
+                              int64_t head_dim, void* Vt, int64_t tk_pad, void* stream);
+int ltx_flash_attn_bf16(const void* Q, int64_t q_rs, const void* K, int64_t k_rs,
+                        const void* Vt, int64_t tk_pad, void* O, int64_t o_rs,
+                        const void* gate, int64_t gate_rs, int64_t Tq, int64_t Tk,
+                        int64_t H, int64_t head_dim, float scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

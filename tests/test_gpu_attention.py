@@ -1,0 +1,113 @@
+"""GPU parity of the flash-attention kernel against the oracle.
+
+Tolerance: P is rounded to bf16 before the second product (as the
+reference's STEEL kernel does) while the oracle keeps fp32, so outputs agree
+to bf16 precision: normwise max relative error <= 1e-2 (north-star gate) and
+cosine >= 0.9999.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _util import bf16_from_torch, cos_sim, max_rel_err
+from oracle.attention import attention as oattn
+from oracle.bf16 import bf16r
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _bf(rng, shape, scale=1.0):
+    return bf16r(rng.standard_normal(shape).astype(np.float32) * np.float32(scale))
+
+
+def _t(a, dtype=torch.bfloat16):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dtype).to(DEV)
+
+
+@pytest.mark.parametrize("tk,dh", [(68, 64), (3456, 128), (256, 128), (1, 64)])
+def test_transpose_v_layout(tk, dh):
+    from ltx_amd.kernels import attention as A
+
+    rng = np.random.default_rng(tk)
+    H = 4
+    v = _bf(rng, (tk, H * dh))
+    vt = A.transpose_v(_t(v), H)
+    torch.cuda.synchronize()
+    got = bf16_from_torch(vt)
+    tkp = A.vt_padded_len(tk)
+    assert got.shape == (H, dh, tkp)
+    # position p of each 16-key group holds key 8*((p%8)//4) + 4*(p//8 % 2) + p%4
+    pos = np.arange(tkp)
+    p16 = pos % 16
+    key = (pos // 16) * 16 + 8 * ((p16 % 8) // 4) + 4 * (p16 // 8) + (p16 % 4)
+    ref = np.zeros((H, dh, tkp), np.float32)
+    valid = key < tk
+    vh = v.reshape(tk, H, dh).transpose(1, 2, 0)  # (H, dh, tk)
+    ref[:, :, valid] = vh[:, :, key[valid]]
+    np.testing.assert_array_equal(got, ref)
+
+
+CASES = [  # (Tq, Tk, H, dh): the block's attention calls at 768x512x65, plus ragged sizes
+    (3456, 3456, 32, 128),  # video self-attention
+    (3456, 256, 32, 128),   # video text cross-attention
+    (3456, 68, 32, 64),     # audio -> video
+    (68, 3456, 32, 64),     # video -> audio
+    (68, 68, 32, 64),       # audio self-attention
+    (68, 256, 32, 64),      # audio text cross-attention
+    (1, 1, 2, 64),
+    (300, 37, 3, 128),
+]
+
+
+@pytest.mark.parametrize("tq,tk,H,dh", CASES)
+def test_flash_attention_matches_oracle(tq, tk, H, dh):
+    from ltx_amd.kernels import attention as A
+
+    rng = np.random.default_rng(tq * 7 + tk)
+    q = _bf(rng, (tq, H * dh), 2.0)
+    k = _bf(rng, (tk, H * dh), 2.0)
+    v = _bf(rng, (tk, H * dh))
+    out = A.flash_attention(_t(q), _t(k), _t(v), H)
+    torch.cuda.synchronize()
+    got = bf16_from_torch(out)
+    ref = oattn(q, k, v, H)
+    assert max_rel_err(got, ref) <= 1e-2
+    assert cos_sim(got, ref) >= 0.9999
+
+
+def test_flash_attention_gate_and_strided_qkv():
+    """q/k/v as column blocks of one fused projection output; gate fused."""
+    from ltx_amd.kernels import attention as A
+
+    rng = np.random.default_rng(5)
+    T, H, dh = 777, 32, 128
+    D = H * dh
+    qkv = _bf(rng, (T, 3 * D), 2.0)
+    g = bf16r(rng.uniform(0, 2, (T, H)).astype(np.float32))
+    t = _t(qkv)
+    out = torch.empty((T, D), dtype=torch.bfloat16, device=DEV)
+    A.flash_attention(t[:, D:2 * D], t[:, 2 * D:], t[:, :D], H, gate=_t(g), out=out)
+    torch.cuda.synchronize()
+    ref = oattn(qkv[:, D:2 * D], qkv[:, 2 * D:], qkv[:, :D], H, gate=g)
+    got = bf16_from_torch(out)
+    assert max_rel_err(got, ref) <= 1e-2 and cos_sim(got, ref) >= 0.9999
+
+
+def test_maybe_steel_attention_reference_api():
+    from ltx_amd.kernels.attention import maybe_steel_attention
+
+    rng = np.random.default_rng(6)
+    T, H, dh = 600, 32, 64
+    x = _t(_bf(rng, (1, T, 3, H, dh)))
+    q, k, v = (x[:, :, i].transpose(1, 2) for i in range(3))  # (1, H, T, dh) strided views
+    out = maybe_steel_attention(q, k, v, scale=dh ** -0.5)
+    assert out is not None and out.shape == (1, H, T, dh)
+    ref = torch.nn.functional.scaled_dot_product_attention(q.float().cpu(), k.float().cpu(), v.float().cpu())
+    got = out.float().cpu()
+    assert max_rel_err(got.numpy(), ref.numpy()) <= 1e-2
+    assert maybe_steel_attention(q, k, v, mask=torch.zeros(1, device=DEV)) is None
+    assert maybe_steel_attention(q.float(), k.float(), v.float()) is None
