@@ -159,6 +159,14 @@ int ltx_gemv_f32_bf16w(const float* x, int64_t batch, int64_t K, const void* W,
                        const float* bias, float* y, int64_t N, int flags,
                        void* stream);
 
+/*
+ * out[b, i] = table[b, i] + vec[i] for b < nb, i < n (fp32): the AdaLN
+ * modulation rows of every block, `scale_shift_table + timestep`
+ * (transformer.py:286-342), computed for all blocks in one launch per step.
+ */
+int ltx_broadcast_add_f32(const float* table, const float* vec, float* out, int64_t nb,
+                          int64_t n, void* stream);
+
 /* ---- projection GEMMs ------------------------------------------------------
  * C[m, n] = epilogue( sum_k A[m, k] * W[n, k] + bias[n] ),
  * fp32 accumulation on bf16 matrix cores (v_mfma_f32_32x32x16_bf16).
@@ -172,6 +180,9 @@ int ltx_gemv_f32_bf16w(const float* x, int64_t batch, int64_t K, const void* W,
  * Requirements: K % 64 == 0, N % 8 == 0, 16-byte aligned pointers and row
  * strides.  `epilogue` is one of LTX_GEMM_EPI_* optionally OR-ed with a tile
  * override (LTX_GEMM_TILE_256 / LTX_GEMM_TILE_128; default: by problem size).
+ * With LTX_GEMM_EPI_BIAS, output columns n >= sigmoid_from get the head-gate
+ * epilogue of LTX_GEMM_EPI_SIGMOID2 instead (pass N for none): the per-head
+ * gate logits ride along with the Q / QKV projection in one GEMM.
  * Replaces mx.addmm / nn.Linear (attention.py:425-437, feed_forward.py:91-112)
  * and mx.quantized_matmul(mode="mxfp8") (loader/transformer_cache.py:177-193).
  */
@@ -185,17 +196,19 @@ int ltx_gemv_f32_bf16w(const float* x, int64_t batch, int64_t K, const void* W,
 
 int ltx_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, const float* bias,
                   void* C, int64_t ldc, int64_t M, int64_t N, int64_t K, int epilogue,
-                  const void* residual, int64_t ldr, const float* gate, void* stream);
+                  const void* residual, int64_t ldr, const float* gate, int64_t sigmoid_from,
+                  void* stream);
 
 int ltx_gemm_w8a16_bf16(const void* A, int64_t lda, const int8_t* Wq, int64_t ldw,
                         const float* w_scale, const float* bias, void* C, int64_t ldc,
                         int64_t M, int64_t N, int64_t K, int epilogue, const void* residual,
-                        int64_t ldr, const float* gate, void* stream);
+                        int64_t ldr, const float* gate, int64_t sigmoid_from, void* stream);
 
 int ltx_gemm_mxfp8_bf16(const void* A, int64_t lda, const uint8_t* Wq, int64_t ldw,
                         const uint8_t* w_scale, int64_t ld_scale, const float* bias, void* C,
                         int64_t ldc, int64_t M, int64_t N, int64_t K, int epilogue,
-                        const void* residual, int64_t ldr, const float* gate, void* stream);
+                        const void* residual, int64_t ldr, const float* gate, int64_t sigmoid_from,
+                        void* stream);
 
 /* ---- weight formats (load-time) --------------------------------------------
  * MXFP8, OCP Microscaling v1.0 with E4M3 elements, blocks of 32 along K and an

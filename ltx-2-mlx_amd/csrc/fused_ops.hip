@@ -376,6 +376,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
   }
 }
 
+// out[b, i] = table[b, i] + vec[i]  (per-block AdaLN modulation rows)
+__global__ void broadcast_add_kernel(const float* __restrict__ table, const float* __restrict__ vec,
+                                     float* __restrict__ out, int64_t nb, int64_t n) {
+  const int64_t total = nb * n;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride)
+    out[i] = table[i] + vec[i % n];
+}
+
 }  // namespace ltx
 
 // ===========================================================================
@@ -559,5 +568,16 @@ extern "C" int ltx_gemv_f32_bf16w(const float* x, int64_t batch, int64_t K, cons
   const int64_t blocks = (waves + 3) / 4;
   gemv_kernel<<<(int)blocks, 256, 0, (hipStream_t)stream>>>(x, (int)batch, (int)K,
                                                             (const bf16*)W, bias, y, N, flags);
+  return ltx_launch_status();
+}
+
+extern "C" int ltx_broadcast_add_f32(const float* table, const float* vec, float* out, int64_t nb,
+                                     int64_t n, void* stream) {
+  if (!table || !vec || !out || nb < 0 || n < 0) return LTX_ERR_INVALID_ARG;
+  const int64_t total = nb * n;
+  if (total == 0) return LTX_OK;
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  broadcast_add_kernel<<<(int)blocks, 256, 0, (hipStream_t)stream>>>(table, vec, out, nb, n);
   return ltx_launch_status();
 }

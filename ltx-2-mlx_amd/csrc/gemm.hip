@@ -52,6 +52,7 @@ struct GemmArgs {
   const bf16* R;       // residual (gated epilogues), may alias C
   int64_t ldr;
   const float* gate;   // fp32 (N)
+  int sig_from;        // columns n >= sig_from get the 2*sigmoid head-gate epilogue
   int M, N, K;
   int tiles_m, tiles_n;
 };
@@ -332,7 +333,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
         for (int e = 0; e < 4; ++e) {
           float y = round_bf(acc[i][j][4 * g + e] + bias4[e]);
           if (EPI == LTX_GEMM_EPI_GELU) y = gelu_tanh(y);
-          if (EPI == LTX_GEMM_EPI_SIGMOID2) y = 2.0f * round_bf(1.0f / (1.0f + expf(-y)));
+          if (EPI == LTX_GEMM_EPI_SIGMOID2 || (EPI == LTX_GEMM_EPI_BIAS && gn + e >= p.sig_from))
+            y = 2.0f * round_bf(1.0f / (1.0f + expf(-y)));
           v[e] = (bf16)y;
         }
         *reinterpret_cast<bf16x4*>(E + (i * 32 + frag_r) * EPI_ROWB + nl * 2) = v;
@@ -434,7 +436,8 @@ static int gemm_check(const void* A, int64_t lda, const void* B, int64_t ldb, vo
 
 static GemmArgs make_args(const void* A, int64_t lda, const void* B, int64_t ldb, const void* bscale,
                           int64_t ld_scale, const float* bias, void* C, int64_t ldc, int64_t M,
-                          int64_t N, int64_t K, const void* R, int64_t ldr, const float* gate) {
+                          int64_t N, int64_t K, const void* R, int64_t ldr, const float* gate,
+                          int64_t sigmoid_from) {
   GemmArgs p;
   p.A = (const bf16*)A;
   p.lda = lda;
@@ -448,6 +451,7 @@ static GemmArgs make_args(const void* A, int64_t lda, const void* B, int64_t ldb
   p.R = (const bf16*)R;
   p.ldr = ldr;
   p.gate = gate;
+  p.sig_from = (int)(sigmoid_from < N ? (sigmoid_from < 0 ? 0 : sigmoid_from) : N);
   p.M = (int)M;
   p.N = (int)N;
   p.K = (int)K;
@@ -458,12 +462,13 @@ static GemmArgs make_args(const void* A, int64_t lda, const void* B, int64_t ldb
 extern "C" int ltx_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw,
                              const float* bias, void* C, int64_t ldc, int64_t M, int64_t N,
                              int64_t K, int epilogue, const void* residual, int64_t ldr,
-                             const float* gate, void* stream) {
+                             const float* gate, int64_t sigmoid_from, void* stream) {
   int st = gemm_check(A, lda, W, ldw, C, ldc, M, N, K, epilogue, residual, ldr, gate, 2);
   if (st != LTX_OK) return st;
   if (M == 0 || N == 0) return LTX_OK;
   if (K == 0) return LTX_ERR_UNSUPPORTED;
-  GemmArgs p = make_args(A, lda, W, ldw, nullptr, 0, bias, C, ldc, M, N, K, residual, ldr, gate);
+  GemmArgs p = make_args(A, lda, W, ldw, nullptr, 0, bias, C, ldc, M, N, K, residual, ldr, gate,
+                         sigmoid_from);
   return launch_kind<B_BF16>(p, epilogue, (hipStream_t)stream);
 }
 
@@ -471,13 +476,14 @@ extern "C" int ltx_gemm_w8a16_bf16(const void* A, int64_t lda, const int8_t* Wq,
                                    const float* w_scale, const float* bias, void* C, int64_t ldc,
                                    int64_t M, int64_t N, int64_t K, int epilogue,
                                    const void* residual, int64_t ldr, const float* gate,
-                                   void* stream) {
+                                   int64_t sigmoid_from, void* stream) {
   int st = gemm_check(A, lda, Wq, ldw, C, ldc, M, N, K, epilogue, residual, ldr, gate, 1);
   if (st != LTX_OK) return st;
   if (!w_scale) return LTX_ERR_INVALID_ARG;
   if (M == 0 || N == 0) return LTX_OK;
   if (K == 0) return LTX_ERR_UNSUPPORTED;
-  GemmArgs p = make_args(A, lda, Wq, ldw, w_scale, 0, bias, C, ldc, M, N, K, residual, ldr, gate);
+  GemmArgs p = make_args(A, lda, Wq, ldw, w_scale, 0, bias, C, ldc, M, N, K, residual, ldr, gate,
+                         sigmoid_from);
   return launch_kind<B_INT8>(p, epilogue, (hipStream_t)stream);
 }
 
@@ -485,13 +491,13 @@ extern "C" int ltx_gemm_mxfp8_bf16(const void* A, int64_t lda, const uint8_t* Wq
                                    const uint8_t* w_scale, int64_t ld_scale, const float* bias,
                                    void* C, int64_t ldc, int64_t M, int64_t N, int64_t K,
                                    int epilogue, const void* residual, int64_t ldr,
-                                   const float* gate, void* stream) {
+                                   const float* gate, int64_t sigmoid_from, void* stream) {
   int st = gemm_check(A, lda, Wq, ldw, C, ldc, M, N, K, epilogue, residual, ldr, gate, 1);
   if (st != LTX_OK) return st;
   if (!w_scale || ld_scale < K / 32) return LTX_ERR_INVALID_ARG;
   if (M == 0 || N == 0) return LTX_OK;
   if (K == 0) return LTX_ERR_UNSUPPORTED;
   GemmArgs p = make_args(A, lda, Wq, ldw, w_scale, ld_scale, bias, C, ldc, M, N, K, residual, ldr,
-                         gate);
+                         gate, sigmoid_from);
   return launch_kind<B_MXFP8>(p, epilogue, (hipStream_t)stream);
 }

@@ -35,15 +35,18 @@ SIGNATURES: dict[str, list] = {
     "ltx_euler_x0_step_bf16": [_vp, _vp, _f32, _f32, _vp, _i64, _vp],
     "ltx_timestep_embedding_f32": [_vp, _i64, _f32, _vp, _i64, _vp],
     "ltx_gemv_f32_bf16w": [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _int, _vp],
-    "ltx_gemm_bf16": [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64, _vp, _vp],
-    "ltx_gemm_w8a16_bf16": [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64, _vp, _vp],
-    "ltx_gemm_mxfp8_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64, _vp, _vp],
+    "ltx_gemm_bf16": [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64, _vp, _i64, _vp],
+    "ltx_gemm_w8a16_bf16": [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64, _vp,
+                            _i64, _vp],
+    "ltx_gemm_mxfp8_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64,
+                            _vp, _i64, _vp],
     "ltx_quantize_mxfp8_bf16": [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp],
     "ltx_dequantize_mxfp8_bf16": [_vp, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _vp],
     "ltx_quantize_w8_bf16": [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp],
     "ltx_dequantize_w8_bf16": [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp],
     "ltx_attn_transpose_v_bf16": [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp],
     "ltx_flash_attn_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _vp],
+    "ltx_broadcast_add_f32": [_vp, _vp, _vp, _i64, _i64, _vp],
 }
 
 # Flag values (include/ltx_hip.h)

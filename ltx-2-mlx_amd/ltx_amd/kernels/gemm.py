@@ -33,6 +33,11 @@ TILE_AUTO, TILE_256, TILE_128 = 0, 1, 2
 
 FORMATS = ("bf16", "int8", "mxfp8")
 
+# Optional launch observer: called as hook(phase, info) with phase "pre" /
+# "post" around every GEMM launch on the launching stream (used by bench.py
+# to time chosen launches with stream events).  None in normal operation.
+LAUNCH_HOOK = None
+
 
 @dataclass
 class LinearWeight:
@@ -116,11 +121,14 @@ def dequantize(weight: LinearWeight) -> torch.Tensor:
 
 def linear(x: torch.Tensor, weight: LinearWeight, *, epilogue: int = EPI_BIAS,
            out: torch.Tensor | None = None, residual: torch.Tensor | None = None,
-           gate: torch.Tensor | None = None, tile: int = TILE_AUTO) -> torch.Tensor:
+           gate: torch.Tensor | None = None, tile: int = TILE_AUTO,
+           sigmoid_from: int | None = None) -> torch.Tensor:
     """``epilogue(x @ W.T + b)`` for x (..., K) bf16; returns (..., N) bf16.
 
     For the residual epilogues, ``residual`` (..., N) bf16 and ``gate`` fp32
     (N) are required; ``out`` may be ``residual`` itself (in-place update).
+    With ``EPI_BIAS``, columns ``n >= sigmoid_from`` get the 2*sigmoid head
+    gate instead (fused gate-logit columns of a Q/QKV projection).
     """
     k = weight.in_features
     n = weight.out_features
@@ -148,21 +156,28 @@ def linear(x: torch.Tensor, weight: LinearWeight, *, epilogue: int = EPI_BIAS,
         gate = g.contiguous()
         gptr = gate.data_ptr()
     flags = epilogue | (tile << 8)
+    sig = n if sigmoid_from is None else int(sigmoid_from)
     bias = weight.bias
     bptr = None if bias is None else bias.data_ptr()
     stream = _lib.stream_of(x)
     detail = f"{weight.kind} M={m} N={n} K={k} epi={epilogue}"
+    hook = LAUNCH_HOOK
+    info = (weight.kind, m, n, k, epilogue) if hook is not None else None
+    if hook is not None:
+        hook("pre", info)
     if weight.kind == "bf16":
         _lib.call("ltx_gemm_bf16", xv.data_ptr(), lda, weight.w.data_ptr(), weight.w.stride(0), bptr,
-                  ov.data_ptr(), ldc, m, n, k, flags, rptr, ldr, gptr, stream, detail=detail)
+                  ov.data_ptr(), ldc, m, n, k, flags, rptr, ldr, gptr, sig, stream, detail=detail)
     elif weight.kind == "int8":
         _lib.call("ltx_gemm_w8a16_bf16", xv.data_ptr(), lda, weight.w.data_ptr(), weight.w.stride(0),
-                  weight.scale.data_ptr(), bptr, ov.data_ptr(), ldc, m, n, k, flags, rptr, ldr, gptr, stream,
+                  weight.scale.data_ptr(), bptr, ov.data_ptr(), ldc, m, n, k, flags, rptr, ldr, gptr, sig, stream,
                   detail=detail)
     elif weight.kind == "mxfp8":
         _lib.call("ltx_gemm_mxfp8_bf16", xv.data_ptr(), lda, weight.w.data_ptr(), weight.w.stride(0),
                   weight.scale.data_ptr(), weight.scale.stride(0), bptr, ov.data_ptr(), ldc, m, n, k, flags,
-                  rptr, ldr, gptr, stream, detail=detail)
+                  rptr, ldr, gptr, sig, stream, detail=detail)
     else:
         raise ValueError(f"unknown weight format {weight.kind!r}")
+    if hook is not None:
+        hook("post", info)
     return out

@@ -1,0 +1,88 @@
+"""Gated multi-head attention of the LTX-2.3 block on gfx950 kernels.
+
+Mirrors ``Attention`` (model/transformer/attention.py:361-603): gate logits
+-> V, Q, K projections -> QK-RMSNorm over the whole inner dim -> split RoPE ->
+attention core -> per-head gate 2*sigmoid -> to_out.  The projections are
+fused into as few GEMMs as the data flow allows:
+
+* self-attention: one GEMM against [Wq; Wk; Wv; Wg] (the gate-logit columns
+  get the 2*sigmoid epilogue in the same launch);
+* cross-attention: [Wq; Wg] on the query input and [Wk; Wv] on the context.
+
+QK-norm + RoPE run in place on the fused output, V is transposed into the
+attention kernel's layout, the head gate is applied inside the attention
+kernel, and ``to_out`` is left to the caller so it can fuse the block's
+residual update into its epilogue.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from ...kernels import attention as attn_k
+from ...kernels import gemm
+from ...kernels.rope_ops import qknorm_rope_
+
+
+class Attention:
+    """Resident weights of one attention module and its core forward."""
+
+    def __init__(self, query_dim: int, context_dim: int | None, heads: int, dim_head: int,
+                 proj_q: gemm.LinearWeight, proj_kv: gemm.LinearWeight | None,
+                 to_out: gemm.LinearWeight, q_norm: torch.Tensor, k_norm: torch.Tensor,
+                 norm_eps: float = 1e-6, gated: bool = True):
+        self.query_dim = query_dim
+        self.self_attention = context_dim is None
+        self.context_dim = query_dim if context_dim is None else context_dim
+        self.heads = heads
+        self.dim_head = dim_head
+        self.inner_dim = heads * dim_head
+        self.proj_q = proj_q      # self: [q|k|v|g] (3*inner + heads); cross: [q|g] (inner + heads)
+        self.proj_kv = proj_kv    # cross only: [k|v] (2*inner)
+        self.to_out = to_out
+        self.q_norm = q_norm
+        self.k_norm = k_norm
+        self.norm_eps = norm_eps
+        self.gated = gated
+
+    def weights(self) -> list[gemm.LinearWeight]:
+        return [w for w in (self.proj_q, self.proj_kv, self.to_out) if w is not None]
+
+    def core(self, x: torch.Tensor, context: torch.Tensor | None = None,
+             pe: tuple | None = None, k_pe: tuple | None = None) -> torch.Tensor:
+        """Everything up to (not including) ``to_out``; returns (Tq, inner) bf16.
+
+        x: (Tq, query_dim) bf16; context: (Tk, context_dim) bf16 for
+        cross-attention.  pe / k_pe: token-major (cos, sin) tables or None.
+        """
+        inner, heads = self.inner_dim, self.heads
+        gate_cols = heads if self.gated else 0
+        if self.self_attention:
+            buf = gemm.linear(x, self.proj_q, sigmoid_from=3 * inner)
+            q, k, v = buf[:, :inner], buf[:, inner:2 * inner], buf[:, 2 * inner:3 * inner]
+            g = buf[:, 3 * inner:3 * inner + gate_cols] if self.gated else None
+            k_tab = pe
+        else:
+            qb = gemm.linear(x, self.proj_q, sigmoid_from=inner)
+            kvb = gemm.linear(context, self.proj_kv)
+            q = qb[:, :inner]
+            g = qb[:, inner:inner + gate_cols] if self.gated else None
+            k, v = kvb[:, :inner], kvb[:, inner:]
+            k_tab = pe if k_pe is None else k_pe
+            if pe is None:
+                k_tab = None
+        qknorm_rope_(q, self.q_norm, pe, k, self.k_norm, k_tab, heads, self.norm_eps)
+        vt = attn_k.transpose_v(v, heads)
+        return attn_k.flash_attention(q, k, None, heads, vt=vt, gate=g)
+
+    def __call__(self, x: torch.Tensor, context: torch.Tensor | None = None, mask=None,
+                 pe: tuple | None = None, k_pe: tuple | None = None) -> torch.Tensor:
+        """Full module forward (attention.py:528-603) on (B=1, T, D) or (T, D)."""
+        if mask is not None:
+            raise NotImplementedError("attention masks are not on the T2V hot path")
+        squeeze = x.dim() == 3
+        x2 = x[0] if squeeze else x
+        c2 = None if context is None else (context[0] if context.dim() == 3 else context)
+        o = self.core(x2, c2, pe, k_pe)
+        out = gemm.linear(o, self.to_out)
+        return out[None] if squeeze else out

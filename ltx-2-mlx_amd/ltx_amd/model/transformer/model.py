@@ -1,0 +1,207 @@
+"""LTX-2.3 audio+video transformer with all blocks resident in HBM.
+
+Mirrors ``LTXModel`` / ``X0Model`` (model/transformer/model.py:497-1546) for
+the distilled text-to-video+audio path:
+
+* preprocess (:285-497): patchify projection, the four AdaLN MLPs per
+  modality (timestep, prompt, cross scale/shift, cross gate), RoPE tables;
+* block scheduler (:1044-1310): the reference streams or compiles groups of
+  blocks and materialises every N blocks; here all blocks' weights stay
+  resident (about 37 GB bf16 or 19 GB MXFP8 of the 288 GB HBM) and the loop
+  only enqueues kernels on one stream -- no host synchronisation inside a
+  step.  The modulation rows of every block are computed in one launch
+  (table + timestep embedding) before the loop;
+* output head (:1312-1342) and the X0 conversion (:1489-1542), the latter
+  fused with the Euler step in ``components.diffusion_steps``.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from ... import _lib
+from ...kernels import gemm
+from ...loader.weights import build_block, linear_weight
+from .rope import AUDIO_MAX_POS, VIDEO_MAX_POS, rope_tables
+from .timestep_embedding import SINUSOID_DIM, AdaLayerNormSingle
+from .transformer import ADA_ROWS, BasicAVTransformerBlock, TransformerArgs, TransformerConfig
+
+AUDIO_HEADS = 32
+AUDIO_HEAD_DIM = 64
+AUDIO_IN_CHANNELS = 128
+AUDIO_CROSS_PE_MAX_POS = 20
+
+
+@dataclass
+class Modality:
+    """Input modality (model.py:103-118): patchified latent (B, T, 128) bf16,
+    text context (B, S, D) bf16, scalar sigma, positions (B, n_dims, T, 2)."""
+
+    latent: torch.Tensor
+    context: torch.Tensor
+    sigma: float
+    positions: np.ndarray
+    enabled: bool = True
+    context_mask: torch.Tensor | None = None
+
+
+class LTXModel:
+    """Random-init LTX-2.3 AV transformer (model.py:497-1486)."""
+
+    def __init__(self, num_layers: int = 48, *, num_attention_heads: int = 32, attention_head_dim: int = 128,
+                 in_channels: int = 128, out_channels: int = 128, cross_attention_dim: int = 4096,
+                 norm_eps: float = 1e-6, timestep_scale_multiplier: float = 1000.0,
+                 av_ca_timestep_scale_multiplier: float = 1000.0, weight_format: str = "bf16",
+                 device: str | torch.device = "cuda", seed: int = 0, audio: bool = True):
+        self.device = torch.device(device)
+        self.num_layers = num_layers
+        self.norm_eps = norm_eps
+        self.timestep_scale_multiplier = timestep_scale_multiplier
+        self.av_ca_timestep_scale_multiplier = av_ca_timestep_scale_multiplier
+        self.weight_format = weight_format
+        self.video_dim = num_attention_heads * attention_head_dim
+        self.audio_dim = AUDIO_HEADS * AUDIO_HEAD_DIM
+        self.video_config = TransformerConfig(self.video_dim, num_attention_heads, attention_head_dim,
+                                              cross_attention_dim, True, True)
+        self.audio_config = (TransformerConfig(self.audio_dim, AUDIO_HEADS, AUDIO_HEAD_DIM, self.audio_dim, True, True)
+                             if audio else None)
+        gen = torch.Generator(device=self.device)
+        gen.manual_seed(seed)
+        dev = self.device
+        vd, ad = self.video_dim, self.audio_dim
+
+        # preprocess / output heads (bf16 weights; small, kept unquantised)
+        self.patchify_proj = linear_weight(vd, in_channels, gen=gen, device=dev, weight_format="bf16")
+        self.adaln_single = AdaLayerNormSingle(vd, 9, device=dev, generator=gen)
+        self.prompt_adaln_single = AdaLayerNormSingle(vd, 2, device=dev, generator=gen)
+        self.av_ca_video_scale_shift_adaln_single = AdaLayerNormSingle(vd, 4, device=dev, generator=gen)
+        self.av_ca_a2v_gate_adaln_single = AdaLayerNormSingle(vd, 1, device=dev, generator=gen)
+        self.scale_shift_table = (torch.randn((2, vd), generator=gen, device=dev) * 0.02).contiguous()
+        self.proj_out = linear_weight(out_channels, vd, gen=gen, device=dev, weight_format="bf16")
+        if audio:
+            self.audio_patchify_proj = linear_weight(ad, AUDIO_IN_CHANNELS, gen=gen, device=dev, weight_format="bf16")
+            self.audio_adaln_single = AdaLayerNormSingle(ad, 9, device=dev, generator=gen)
+            self.audio_prompt_adaln_single = AdaLayerNormSingle(ad, 2, device=dev, generator=gen)
+            self.av_ca_audio_scale_shift_adaln_single = AdaLayerNormSingle(ad, 4, device=dev, generator=gen)
+            self.av_ca_v2a_gate_adaln_single = AdaLayerNormSingle(ad, 1, device=dev, generator=gen)
+            self.audio_scale_shift_table = (torch.randn((2, ad), generator=gen, device=dev) * 0.02).contiguous()
+            self.audio_proj_out = linear_weight(out_channels, ad, gen=gen, device=dev, weight_format="bf16")
+
+        # all blocks' modulation tables packed for the one-launch row update
+        self.video_tables = torch.empty((num_layers, ADA_ROWS, vd), dtype=torch.float32, device=dev)
+        self.audio_tables = (torch.empty((num_layers, ADA_ROWS, ad), dtype=torch.float32, device=dev)
+                             if audio else None)
+        self.transformer_blocks: list[BasicAVTransformerBlock] = []
+        for i in range(num_layers):
+            w = build_block(self.video_config, self.audio_config, device=dev, weight_format=weight_format,
+                            generator=gen, norm_eps=norm_eps, video_tables=self.video_tables[i],
+                            audio_tables=None if self.audio_tables is None else self.audio_tables[i])
+            self.transformer_blocks.append(BasicAVTransformerBlock(i, self.video_config, self.audio_config,
+                                                                   norm_eps=norm_eps, weights=w))
+        # per-step buffers
+        self._temb_v = torch.empty((ADA_ROWS, vd), device=dev)
+        self._emb_v = torch.empty(vd, device=dev)
+        self._ada_v = torch.empty_like(self.video_tables)
+        if audio:
+            self._temb_a = torch.empty((ADA_ROWS, ad), device=dev)
+            self._emb_a = torch.empty(ad, device=dev)
+            self._ada_a = torch.empty_like(self.audio_tables)
+        self._rope_cache: dict = {}
+
+    # ------------------------------------------------------------------------
+    def weight_bytes(self) -> int:
+        n = sum(b.nbytes() for b in self.transformer_blocks)
+        mlps = [self.adaln_single, self.prompt_adaln_single, self.av_ca_video_scale_shift_adaln_single,
+                self.av_ca_a2v_gate_adaln_single]
+        if self.audio_config is not None:
+            mlps += [self.audio_adaln_single, self.audio_prompt_adaln_single,
+                     self.av_ca_audio_scale_shift_adaln_single, self.av_ca_v2a_gate_adaln_single]
+        return n + sum(m.nbytes() for m in mlps)
+
+    def rope(self, video_positions: np.ndarray, audio_positions: np.ndarray | None):
+        """Token-major RoPE tables for a stage: (video self, video cross, audio
+        self, audio cross); computed once per set of positions."""
+        key = (video_positions.shape, video_positions.tobytes()[:64], None if audio_positions is None
+               else (audio_positions.shape, audio_positions.tobytes()[:64]))
+        if key not in self._rope_cache:
+            dev = self.device
+            vpe = rope_tables(video_positions, self.video_dim, VIDEO_MAX_POS, dev)
+            vxpe = ape = axpe = None
+            if audio_positions is not None and self.audio_config is not None:
+                # cross PE: temporal axis only, dim = audio inner dim (model.py:392-416)
+                vxpe = rope_tables(video_positions[:, 0:1], self.audio_dim, (AUDIO_CROSS_PE_MAX_POS,), dev)
+                ape = rope_tables(audio_positions, self.audio_dim, AUDIO_MAX_POS, dev)
+                axpe = rope_tables(audio_positions[:, 0:1], self.audio_dim, (AUDIO_CROSS_PE_MAX_POS,), dev)
+            self._rope_cache[key] = (vpe, vxpe, ape, axpe)
+        return self._rope_cache[key]
+
+    def _timestep_rows(self, sigma_dev: torch.Tensor, cross_sigma_dev: torch.Tensor, video: bool) -> None:
+        """Fill the (16, D) timestep rows of one modality (model.py:160-187,
+        :305-314, :418-497) and its embedded timestep."""
+        d = self.video_dim if video else self.audio_dim
+        temb = self._temb_v if video else self._temb_a
+        emb = self._emb_v if video else self._emb_a
+        ts = self.timestep_scale_multiplier
+        if video:
+            mlps = (self.adaln_single, self.prompt_adaln_single, self.av_ca_video_scale_shift_adaln_single,
+                    self.av_ca_a2v_gate_adaln_single)
+        else:
+            mlps = (self.audio_adaln_single, self.audio_prompt_adaln_single,
+                    self.av_ca_audio_scale_shift_adaln_single, self.av_ca_v2a_gate_adaln_single)
+        flat = temb.view(-1)
+        mlps[0](sigma_dev, ts, flat[: 9 * d], embedded=emb)
+        mlps[1](sigma_dev, ts, flat[9 * d: 11 * d])
+        if self.audio_config is not None:
+            mlps[2](sigma_dev, ts, flat[11 * d: 15 * d])
+            mlps[3](cross_sigma_dev, self.av_ca_timestep_scale_multiplier, flat[15 * d: 16 * d])
+        else:
+            flat[11 * d:].zero_()
+
+    def velocity(self, video_latent: torch.Tensor, video_context: torch.Tensor, sigma_dev: torch.Tensor,
+                 pes: tuple, audio_latent: torch.Tensor | None = None,
+                 audio_context: torch.Tensor | None = None,
+                 profile_events: list | None = None) -> tuple[torch.Tensor, torch.Tensor | None]:
+        """One transformer forward -> (video velocity (T, 128), audio velocity).
+
+        Latents are 2-D (T, 128) bf16; contexts (S, D) bf16; ``sigma_dev`` is
+        the fp32 device scalar of this step's sigma.
+        """
+        vpe, vxpe, ape, axpe = pes
+        run_audio = self.audio_config is not None and audio_latent is not None and audio_latent.shape[0] > 0
+        # preprocess
+        vx = gemm.linear(video_latent, self.patchify_proj)
+        self._timestep_rows(sigma_dev, sigma_dev, video=True)
+        stream = _lib.stream_of(vx)
+        _lib.call("ltx_broadcast_add_f32", self.video_tables.data_ptr(), self._temb_v.data_ptr(),
+                  self._ada_v.data_ptr(), self.num_layers, ADA_ROWS * self.video_dim, stream)
+        video = TransformerArgs(x=vx, context=video_context, timesteps=self._temb_v[:9], positional_embeddings=vpe,
+                                cross_positional_embeddings=vxpe)
+        audio = None
+        if run_audio:
+            ax = gemm.linear(audio_latent, self.audio_patchify_proj)
+            self._timestep_rows(sigma_dev, sigma_dev, video=False)
+            _lib.call("ltx_broadcast_add_f32", self.audio_tables.data_ptr(), self._temb_a.data_ptr(),
+                      self._ada_a.data_ptr(), self.num_layers, ADA_ROWS * self.audio_dim, stream)
+            audio = TransformerArgs(x=ax, context=audio_context, timesteps=self._temb_a[:9],
+                                    positional_embeddings=ape, cross_positional_embeddings=axpe)
+        # blocks
+        for i, block in enumerate(self.transformer_blocks):
+            block.ada_rows_video = self._ada_v[i]
+            block.ada_rows_audio = self._ada_a[i] if run_audio else None
+            video, audio = block(video, audio, profile_events=profile_events)
+        # output heads
+        v_out = self._output(video.x, self.scale_shift_table, self._emb_v, self.proj_out)
+        a_out = None
+        if run_audio:
+            a_out = self._output(audio.x, self.audio_scale_shift_table, self._emb_a, self.audio_proj_out)
+        return v_out, a_out
+
+    def _output(self, x: torch.Tensor, table: torch.Tensor, emb: torch.Tensor, proj: gemm.LinearWeight) -> torch.Tensor:
+        t, d = x.shape
+        h = torch.empty_like(x)
+        _lib.call("ltx_output_norm_modulate_bf16", x.data_ptr(), d, table.data_ptr(), emb.data_ptr(), h.data_ptr(),
+                  d, t, d, float(self.norm_eps), _lib.stream_of(x))
+        return gemm.linear(h, proj)

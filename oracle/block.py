@@ -1,0 +1,218 @@
+"""Oracle for the audio+video transformer block and the denoise step.
+
+A float32 torch-CPU restatement of model/transformer/transformer.py:389-674,
+attention.py:528-603, feed_forward.py:64-112, model.py:285-497, :1312-1342,
+:1489-1542 and diffusion_steps.py:58-69, with every bf16 rounding of the
+reference (``bf`` marks them).  Weights are plain per-projection tensors
+(to_q, to_k, to_v, to_gate_logits, to_out, ...), decoded to their bf16
+values, as in the reference's modules.
+
+AdaLN follows the reference's dispatch default (transformer.py:85-110): the
+compiled inline form ``(rms_norm(x) * (1 + scale) + shift).astype(bf16)``
+whose rms_norm output is bf16 (``fused_adaln=False``); ``fused_adaln=True``
+is the single-rounding fused kernel (fused_ops.py:172-175).
+
+Pinning: built from the pinned pieces (oracle.fused_ops, oracle.rope,
+oracle.attention, oracle.quant.linear semantics), and checked in
+tests/test_oracle_block.py by invariants of the residual wiring (zero gates
+make every sub-layer vanish; a zero A2V gate decouples audio from video;
+per-token independence of the FF path).
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+EPS = 1e-6
+
+
+def bf(t: torch.Tensor) -> torch.Tensor:
+    return t.to(torch.bfloat16).to(torch.float32)
+
+
+def rms_inv(x: torch.Tensor, eps: float = EPS) -> torch.Tensor:
+    return torch.rsqrt(x.double().square().mean(-1, keepdim=True) + eps).float()
+
+
+def rms_norm_bf(x, eps=EPS):
+    """mx.fast.rms_norm(x) on bf16 x (no weight): bf16 output."""
+    return bf(x * rms_inv(x, eps))
+
+
+def adaln(x, scale, shift, eps=EPS, fused=False):
+    if fused:
+        return bf(x * rms_inv(x, eps) * (1 + scale) + shift)
+    return bf(rms_norm_bf(x, eps) * (1 + scale) + shift)
+
+
+def linear(x, w, b=None):
+    """nn.Linear / mx.addmm on bf16: fp32 accumulation, bf16 output."""
+    y = x @ w.T
+    if b is not None:
+        y = y + b
+    return bf(y)
+
+
+def gelu_tanh(x):
+    return 0.5 * x * (1.0 + torch.tanh(math.sqrt(2.0 / math.pi) * (x + 0.044715 * x ** 3)))
+
+
+def rope(x, cos, sin, heads):
+    """Split RoPE (rope.py:37-89) with token-major (T, D/2) tables."""
+    t, d = x.shape
+    dh = d // heads
+    xh = x.view(t, heads, dh)
+    c = cos.view(t, heads, dh // 2)
+    s = sin.view(t, heads, dh // 2)
+    x1, x2 = xh[..., : dh // 2], xh[..., dh // 2:]
+    return bf(torch.cat([x1 * c - x2 * s, x1 * s + x2 * c], -1).reshape(t, d))
+
+
+def sdpa(q, k, v, heads):
+    tq, d = q.shape
+    tk = k.shape[0]
+    dh = d // heads
+    qh = q.view(tq, heads, dh).transpose(0, 1)
+    kh = k.view(tk, heads, dh).transpose(0, 1)
+    vh = v.view(tk, heads, dh).transpose(0, 1)
+    p = torch.softmax(torch.matmul(qh, kh.transpose(1, 2).contiguous()) / math.sqrt(dh), -1)
+    return bf(torch.matmul(p, vh.contiguous()).transpose(0, 1).reshape(tq, d))
+
+
+def attention(w: dict, x, context=None, pe=None, k_pe=None, heads=32, eps=EPS):
+    """Attention.__call__ (attention.py:528-603)."""
+    context = x if context is None else context
+    g = bf(2.0 * bf(torch.sigmoid(linear(x, w["to_gate_logits"], w["to_gate_logits_b"]))))
+    v = linear(context, w["to_v"], w["to_v_b"])
+    q = linear(x, w["to_q"], w["to_q_b"])
+    k = linear(context, w["to_k"], w["to_k_b"])
+    q = bf(q * rms_inv(q, eps) * w["q_norm"])
+    k = bf(k * rms_inv(k, eps) * w["k_norm"])
+    if pe is not None:
+        q = rope(q, pe[0], pe[1], heads)
+        kp = pe if k_pe is None else k_pe
+        k = rope(k, kp[0], kp[1], heads)
+    o = sdpa(q, k, v, heads)
+    t, d = o.shape
+    o = bf(o.view(t, heads, d // heads) * g[:, :, None]).reshape(t, d)
+    return linear(o, w["to_out"], w["to_out_b"])
+
+
+def feed_forward(w: dict, x):
+    h = bf(gelu_tanh(linear(x, w["w1"], w["b1"])))
+    return linear(h, w["w2"], w["b2"])
+
+
+def block(W: dict, vx, ax, v_ada, a_ada, vctx, actx, vpe, vxpe, ape, axpe, *, fused_adaln=False, eps=EPS):
+    """BasicAVTransformerBlock.__call__ (transformer.py:389-674) on 2-D
+    streams; ``*_ada`` are the (16, D) modulation rows
+    [sst(9) | prompt(2) | av(5)] + timestep rows."""
+    r = v_ada
+    vh, ah = 32, 32
+    if vx is not None:
+        h = adaln(vx, r[1], r[0], eps, fused_adaln)
+        vx = bf(vx + attention(W["attn1"], h, pe=vpe, heads=vh) * r[2])
+        a = adaln(vx, r[7], r[6], eps)
+        c = bf(vctx * (1 + r[10]) + r[9])
+        vx = bf(vx + bf(attention(W["attn2"], a, c, heads=vh) * r[8]))
+    if ax is not None:
+        q = a_ada
+        h = adaln(ax, q[1], q[0], eps, fused_adaln)
+        ax = bf(ax + attention(W["audio_attn1"], h, pe=ape, heads=ah) * q[2])
+        a = adaln(ax, q[7], q[6], eps)
+        c = bf(actx * (1 + q[10]) + q[9])
+        ax = bf(ax + bf(attention(W["audio_attn2"], a, c, heads=ah) * q[8]))
+    if vx is not None and ax is not None:
+        vn, an = rms_norm_bf(vx, eps), rms_norm_bf(ax, eps)
+        q = a_ada
+        vs = bf(vn * (1 + r[11]) + r[12])
+        as_ = bf(an * (1 + q[11]) + q[12])
+        vx = bf(vx + attention(W["audio_to_video_attn"], vs, as_, pe=vxpe, k_pe=axpe, heads=ah) * r[15])
+        as2 = bf(an * (1 + q[13]) + q[14])
+        vs2 = bf(vn * (1 + r[13]) + r[14])
+        ax = bf(ax + attention(W["video_to_audio_attn"], as2, vs2, pe=axpe, k_pe=vxpe, heads=ah) * q[15])
+    if vx is not None:
+        h = adaln(vx, r[4], r[3], eps, fused_adaln)
+        vx = bf(vx + feed_forward(W["ff"], h) * r[5])
+    if ax is not None:
+        q = a_ada
+        h = adaln(ax, q[4], q[3], eps, fused_adaln)
+        ax = bf(ax + feed_forward(W["audio_ff"], h) * q[5])
+    return vx, ax
+
+
+# ---- step glue -------------------------------------------------------------
+def timestep_sinusoid(t: float, dim: int = 256) -> torch.Tensor:
+    """get_timestep_embedding(flip_sin_to_cos=True, shift=0) in float64 args."""
+    half = dim // 2
+    i = torch.arange(half, dtype=torch.float32)
+    expo = (torch.tensor(-math.log(10000.0), dtype=torch.float32) * i) / half
+    arg = torch.tensor(t, dtype=torch.float32) * torch.exp(expo.double()).float()
+    arg = arg.double()
+    return torch.cat([torch.cos(arg), torch.sin(arg)]).float()
+
+
+def adaln_mlp(w: dict, t: float):
+    """AdaLayerNormSingle (timestep_embedding.py:165-201) in fp32 with bf16
+    weights -> (emb (N*D), embedded_timestep (D))."""
+    s = timestep_sinusoid(t)
+    h = torch.nn.functional.silu(s @ w["w1"].T + w["b1"])
+    e = h @ w["w2"].T + w["b2"]
+    return torch.nn.functional.silu(e) @ w["w"].T + w["b"], e
+
+
+def output_head(x, table, emb, w, b, eps=EPS):
+    """model.py:1312-1326: bf16 arithmetic modulation, then proj_out."""
+    ss = bf(table + emb[None, :])
+    shift, scale = ss[0], ss[1]
+    mu = x.double().mean(-1, keepdim=True)
+    var = (x.double() - mu).square().mean(-1, keepdim=True)
+    n = bf(((x.double() - mu) / torch.sqrt(var + eps)).float())
+    y = bf(bf(n * bf(1 + scale)) + shift)
+    return linear(y, w, b)
+
+
+def euler_x0(latent, velocity, sigma: float, sigma_next: float):
+    """model.py:1519-1525 + diffusion_steps.py:58-69 in fp32."""
+    s = torch.tensor(sigma, dtype=torch.float32)
+    ratio = torch.tensor(sigma_next / sigma, dtype=torch.float32)
+    x0 = latent - s * velocity
+    return bf(x0 + ratio * (latent - x0))
+
+
+def model_step(MW: dict, vlat, alat, vctx, actx, sigma: float, sigma_next: float, pes, *, av_ca_mult=1000.0,
+               ts_mult=1000.0, eps=EPS):
+    """One distilled AV denoise step: LTXModel.__call__ (model.py:1344-1486)
+    + X0Model (:1489-1542) + Euler (diffusion_steps.py:58-69).
+
+    MW: {"patchify": (w, b), "audio_patchify": (w, b), "mlps_v": [4 mlp dicts],
+    "mlps_a": [...], "tables_v": (L, 16, D), "tables_a": ..., "blocks": [block
+    dicts], "sst_out_v": (2, D), "proj_out_v": (w, b), ...}.
+    """
+    vpe, vxpe, ape, axpe = pes
+    t = sigma * ts_mult
+    vx = linear(vlat, *MW["patchify"])
+    ax = linear(alat, *MW["audio_patchify"]) if alat is not None else None
+
+    def temb(mlps, d):
+        e9, emb = adaln_mlp(mlps[0], t)
+        e2, _ = adaln_mlp(mlps[1], t)
+        e4, _ = adaln_mlp(mlps[2], t)
+        e1, _ = adaln_mlp(mlps[3], sigma * av_ca_mult)
+        return torch.cat([e9, e2, e4, e1]).view(16, d), emb
+
+    tv, emb_v = temb(MW["mlps_v"], vx.shape[1])
+    ta, emb_a = temb(MW["mlps_a"], ax.shape[1]) if ax is not None else (None, None)
+    for i, W in enumerate(MW["blocks"]):
+        v_ada = MW["tables_v"][i] + tv
+        a_ada = MW["tables_a"][i] + ta if ax is not None else None
+        vx, ax = block(W, vx, ax, v_ada, a_ada, vctx, actx, vpe, vxpe, ape, axpe, eps=eps)
+    vvel = output_head(vx, MW["sst_out_v"], emb_v, *MW["proj_out_v"], eps=eps)
+    new_v = euler_x0(vlat, vvel, sigma, sigma_next)
+    new_a = None
+    if ax is not None:
+        avel = output_head(ax, MW["sst_out_a"], emb_a, *MW["proj_out_a"], eps=eps)
+        new_a = euler_x0(alat, avel, sigma, sigma_next)
+    return new_v, new_a

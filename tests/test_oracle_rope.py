@@ -1,0 +1,82 @@
+"""Pin oracle.rope: frequency grid, positions (known answers), table
+invariants, rotation invariants; and the product's host tables equal it."""
+
+import math
+
+import numpy as np
+
+from oracle import rope as r
+from oracle.bf16 import bf16r
+
+
+def test_freq_grid_endpoints_and_log_spacing():
+    g = r.freq_grid_f64(10000.0, 3, 4096)
+    assert g.shape == (682,)
+    assert g[0] == np.float32(math.pi / 2) and g[-1] == np.float32(10000.0 * math.pi / 2)
+    ratios = np.diff(np.log(g.astype(np.float64)))
+    np.testing.assert_allclose(ratios, math.log(10000.0) / 681, rtol=1e-5)
+    assert r.freq_grid_f64(10000.0, 1, 2048).shape == (1024,)
+
+
+def test_video_positions_known_values():
+    pos = r.video_positions(2, 1, 2, fps=24.0)
+    assert pos.shape == (1, 3, 4, 2)
+    # frame 0: [0, 8) -> causal fix [max(0+1-8, 0), 8+1-8] = [0, 1] -> seconds /24
+    np.testing.assert_array_equal(pos[0, 0, 0], np.array([0.0, 1.0 / 24], np.float32))
+    # frame 1: [8, 16) -> [1, 9] / 24
+    np.testing.assert_array_equal(pos[0, 0, 2], np.array([1.0, 9.0], np.float32) / np.float32(24))
+    # width index 1 -> pixels [32, 64); height row 0 -> [0, 32)
+    np.testing.assert_array_equal(pos[0, 2, 1], [32.0, 64.0])
+    np.testing.assert_array_equal(pos[0, 1, 3], [0.0, 32.0])
+
+
+def test_audio_positions_known_values():
+    pos = r.audio_positions(3)
+    # latent i -> mel 4i, causal max(4i+1-4, 0), x 160/16000 s
+    np.testing.assert_allclose(pos[0, 0, :, 0], [0.0, 0.01, 0.05], rtol=1e-6)
+    np.testing.assert_allclose(pos[0, 0, :, 1], [0.01, 0.05, 0.09], rtol=1e-6)
+
+
+def test_tables_identity_at_centre_and_pad_slots():
+    # a patch whose middle sits at half of max_pos has scaled position 0
+    pos = np.zeros((1, 3, 1, 2), np.float32)
+    pos[0, 0, 0] = [9.0, 11.0]        # mid 10 = 20/2
+    pos[0, 1, 0] = [1000.0, 1048.0]   # mid 1024 = 2048/2
+    pos[0, 2, 0] = [1020.0, 1028.0]
+    cos, sin = r.rope_tables(pos, 4096, 32, r.VIDEO_MAX_POS)
+    np.testing.assert_array_equal(cos, 1.0)
+    np.testing.assert_array_equal(sin, 0.0)
+    # pad slots (first 2048 - 3*682 = 2 entries) are identity for any position
+    cos, sin = r.rope_tables(r.video_positions(3, 2, 2, 24.0), 4096, 32, r.VIDEO_MAX_POS)
+    np.testing.assert_array_equal(cos[:, :2], 1.0)
+    np.testing.assert_array_equal(sin[:, :2], 0.0)
+    assert not np.all(cos[:, 2:] == 1.0)
+
+
+def test_rotation_preserves_pair_norms_and_inverts(rng):
+    heads = 4
+    x = bf16r(rng.standard_normal((5, heads * 64)).astype(np.float32))
+    ang = rng.uniform(-3, 3, (5, heads * 32))
+    cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    y = r.apply_split_rope(x, cos, sin, heads).astype(np.float64)
+    xh, yh = x.reshape(5, heads, 64).astype(np.float64), y.reshape(5, heads, 64)
+    n_in = xh[..., :32] ** 2 + xh[..., 32:] ** 2
+    n_out = yh[..., :32] ** 2 + yh[..., 32:] ** 2
+    np.testing.assert_allclose(n_out, n_in, rtol=2e-2, atol=1e-2)
+    back = r.apply_split_rope(y.astype(np.float32), cos, -sin, heads)
+    np.testing.assert_allclose(back, x, atol=3e-2)
+
+
+def test_product_tables_match_oracle_bitwise():
+    from ltx_amd.model.transformer import rope as prope
+
+    vpos = r.video_positions(9, 16, 24, 24.0)
+    np.testing.assert_array_equal(prope.video_positions(9, 16, 24, 24.0), vpos)
+    apos = r.audio_positions(68)
+    np.testing.assert_array_equal(prope.audio_positions(68), apos)
+    for pos, dim, mp in ((vpos, 4096, r.VIDEO_MAX_POS), (apos, 2048, r.AUDIO_MAX_POS),
+                         (vpos[:, 0:1], 2048, r.AUDIO_MAX_POS)):
+        oc, os_ = r.rope_tables(pos, dim, 32, mp)
+        pc, ps = prope.rope_tables_np(pos, dim, mp)
+        np.testing.assert_array_equal(pc, oc)
+        np.testing.assert_array_equal(ps, os_)
