@@ -108,12 +108,17 @@ __device__ __forceinline__ void dma16(const void* src, char* lds_wave_base) {
   __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)lds_wave_base, 16, 0, 0);
 }
 
+// s_waitcnt through the builtin (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] |
+// lgkmcnt[11:8] | vmcnt_hi[15:14]) so the compiler's own wait insertion
+// sees it.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x70 | 0xF00);
 }
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
-template <int BM, int BN, int BKIND, int EPI>
+template <int BM, int BN, int BKIND, int EPI, int SWZ = 0>
 struct GemmCfg {
   static constexpr int WM = BM / 2, WN = BN / 2;    // wave tile (2 x 2 waves)
   static constexpr int TM = WM / 32, TN = WN / 32;  // 32x32 MFMA tiles per wave
@@ -134,9 +139,14 @@ struct GemmCfg {
   static constexpr int LDS_BYTES = (STAGES * STAGE > EPI_BYTES) ? STAGES * STAGE : EPI_BYTES;
 };
 
-template <int BM, int BN, int BKIND, int EPI>
+// bf16 row swizzle (16-byte chunk index XOR): SWZ 0 uses (row/2)%8 (conflict-free
+// for 16-lane / 256-byte bank groups), SWZ 1 uses row%8 (8-lane / 128-byte).
+template <int SWZ>
+__device__ __forceinline__ int rswz(int r) { return SWZ == 0 ? ((r >> 1) & 7) : (r & 7); }
+
+template <int BM, int BN, int BKIND, int EPI, int SWZ = 0>
 __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
-  using Cfg = GemmCfg<BM, BN, BKIND, EPI>;
+  using Cfg = GemmCfg<BM, BN, BKIND, EPI, SWZ>;
   constexpr int WM = Cfg::WM, WN = Cfg::WN, TM = Cfg::TM, TN = Cfg::TN;
   constexpr bool B8 = Cfg::B8;
   constexpr int STAGES = Cfg::STAGES;
@@ -166,7 +176,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
     const int r = 8 * (4 * i + wave) + (lane >> 3);
     int gm = m0 + r;
     gm = gm < p.M ? gm : p.M - 1;
-    const int chunk = (lane & 7) ^ ((r >> 1) & 7);
+    const int chunk = (lane & 7) ^ rswz<SWZ>(r);
     a_src[i] = (const char*)(p.A + (int64_t)gm * p.lda) + chunk * 16;
   }
   // B: bf16 like A; 8-bit rows are 64 B: 16 rows per wave instruction, lane ->
@@ -180,7 +190,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
       chunk = (lane & 3) ^ ((r >> 2) & 3);
     } else {
       r = 8 * (4 * i + wave) + (lane >> 3);
-      chunk = (lane & 7) ^ ((r >> 1) & 7);
+      chunk = (lane & 7) ^ rswz<SWZ>(r);
     }
     int gn = n0 + r;
     gn = gn < p.N ? gn : p.N - 1;
@@ -202,6 +212,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
   // MXFP8 scales of one stage: 2 E8M0 bytes (k blocks 0/1 of the 64) per row.
   uint32_t sc_cur[TN], sc_next[TN];
 
+  // One stage's A and B tiles by LDS DMA (MXFP8 scales travel separately).
   auto issue_stage = [&](int kt, int buf) {
     char* As = lds + buf * STAGE;
     char* Bs = As + A_BYTES;
@@ -211,10 +222,25 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
     const int64_t kb = (int64_t)kt * kBK * (B8 ? 1 : 2);
 #pragma unroll
     for (int i = 0; i < B_DMA; ++i) dma16(b_src[i] + kb, Bs + (4 * i + wave) * 1024);
-    if (BKIND == B_MXFP8) {
+  };
+  auto load_scales = [&](int kt) {
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
-        sc_next[j] = *reinterpret_cast<const uint16_t*>(sc_row[j] + kt * 2);
+    for (int j = 0; j < TN; ++j) sc_next[j] = *reinterpret_cast<const uint16_t*>(sc_row[j] + kt * 2);
+  };
+  // Wait until the oldest outstanding stage has landed while `ahead` later
+  // stages may stay in flight (vmcnt counts this lane's DMA instructions).
+  constexpr int L = A_DMA + B_DMA;
+  auto wait_ahead = [&](int ahead) {
+    if constexpr (BKIND == B_MXFP8) {
+      wait_vmcnt<0>();  // scale loads share the counter
+    } else if constexpr (STAGES == 4) {
+      if (ahead >= 3) wait_vmcnt<3 * L>();
+      else if (ahead == 2) wait_vmcnt<2 * L>();
+      else if (ahead == 1) wait_vmcnt<L>();
+      else wait_vmcnt<0>();
+    } else {
+      if (ahead >= 1) wait_vmcnt<L>();
+      else wait_vmcnt<0>();
     }
   };
 
@@ -231,92 +257,116 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
   for (int i = 0; i < TM; ++i) a_off[i] = (wm * WM + i * 32 + frag_r) * A_ROWB;
 #pragma unroll
   for (int j = 0; j < TN; ++j) b_off[j] = (wn * WN + j * 32 + frag_r) * B_ROWB;
-  const int a_swz = (frag_r >> 1) & 7;  // (row/2)%8 for rows i*32+frag_r
+  const int a_swz = rswz<SWZ>(frag_r);  // same for rows i*32+frag_r
   const int b_swz = B8 ? ((frag_r >> 2) & 3) : a_swz;
 
-  // prologue: stages 0 .. STAGES-2 in flight
+  // Fragment reads of k-step kk of the stage in buffer `buf` (8-bit weights
+  // dequantised here with the scales in sc_cur).
+  auto read_frags = [&](int buf, int kk, bf16x8* fa, bf16x8* fb) {
+    const char* As = lds + buf * STAGE;
+    const char* Bs = As + A_BYTES;
+    const int ca = ((kk * 2 + frag_c) ^ a_swz) * 16;
 #pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s) {
-    if (s < KT) issue_stage(s, s);
-    if (BKIND == B_MXFP8 && s == 0) {
+    for (int i = 0; i < TM; ++i) fa[i] = *reinterpret_cast<const bf16x8*>(As + a_off[i] + ca);
+    if (!B8) {
 #pragma unroll
-      for (int j = 0; j < TN; ++j) sc_cur[j] = sc_next[j];
-    }
-  }
-
-  for (int kt = 0; kt < KT; ++kt) {
-    // wait for stage kt: at most STAGES-2 later stages may still be in flight
-    if (kt + STAGES - 2 < KT) {
-      if constexpr (STAGES == 4) wait_vmcnt<2 * (A_DMA + B_DMA)>();
-      else wait_vmcnt<0>();
+      for (int j = 0; j < TN; ++j) fb[j] = *reinterpret_cast<const bf16x8*>(Bs + b_off[j] + ca);
     } else {
-      wait_vmcnt<0>();
+      const int c8 = kk * 2 + frag_c;  // 8-byte chunk of the 64-byte row
+      const int cb = ((c8 >> 1) ^ b_swz) * 16 + (c8 & 1) * 8;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const u32x2 raw = *reinterpret_cast<const u32x2*>(Bs + b_off[j] + cb);
+        uint32_t o[4];
+        if (BKIND == B_INT8) {
+          const float s = s_i8[j], nb = -128.0f * s;
+#pragma unroll
+          for (int d = 0; d < 2; ++d) {
+            const uint32_t u = raw[d] ^ 0x80808080u;
+            bf16x2 p0, p1;
+            p0[0] = (bf16)fmaf((float)(u & 0xffu), s, nb);
+            p0[1] = (bf16)fmaf((float)((u >> 8) & 0xffu), s, nb);
+            p1[0] = (bf16)fmaf((float)((u >> 16) & 0xffu), s, nb);
+            p1[1] = (bf16)fmaf((float)(u >> 24), s, nb);
+            o[2 * d] = __builtin_bit_cast(uint32_t, p0);
+            o[2 * d + 1] = __builtin_bit_cast(uint32_t, p1);
+          }
+        } else {
+          const float sc = e8m0_to_f32((sc_cur[j] >> (8 * (kk >> 1))) & 0xffu);
+#pragma unroll
+          for (int d = 0; d < 2; ++d) {
+            o[2 * d] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[d], sc, false));
+            o[2 * d + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[d], sc, true));
+          }
+        }
+        fb[j] = __builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]});
+      }
     }
-    __syncthreads();
+  };
+  auto mfmas = [&](const bf16x8* fa, const bf16x8* fb) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
+  };
+
+  // Software pipeline: stages fill all STAGES buffers ahead; fragments of the
+  // next k-step are read while the MFMAs of the current one run, including
+  // across the stage boundary, whose barrier sits between the fragment reads
+  // of k-step 3 and its MFMAs.
+  bf16x8 fa[2][TM], fb[2][TN];
+  const int pro = KT < STAGES ? KT : STAGES;
+#pragma unroll
+  for (int st = 0; st < STAGES; ++st)
+    if (st < KT) issue_stage(st, st);
+  if (BKIND == B_MXFP8) load_scales(0);
+  wait_ahead(pro - 1);
+  if (BKIND == B_MXFP8) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) sc_cur[j] = sc_next[j];
+    if (KT > 1) load_scales(1);
+  }
+  __syncthreads();
+  read_frags(0, 0, fa[0], fb[0]);
+  wait_lgkmcnt0();
+
+  // k-steps 0..2 of the stage in `buf`: read k-step kk+1, then MFMAs of kk.
+  // The fragments of kk were issued one MFMA block earlier; waiting for them
+  // before issuing the next reads keeps at most one group (TM+TN <= 8 reads)
+  // in flight, which the 4-bit LDS counter can track exactly.
+  auto first3 = [&](int buf) {
+#pragma unroll
+    for (int kk = 0; kk < kBK / 16 - 1; ++kk) {
+      wait_lgkmcnt0();
+      read_frags(buf, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas(fa[kk & 1], fb[kk & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  for (int kt = 0; kt < KT - 1; ++kt) {
+    const int buf = kt % STAGES;
+    first3(buf);
+    const int ahead = (KT - 2 - kt) < (STAGES - 2) ? (KT - 2 - kt) : (STAGES - 2);
+    wait_ahead(ahead);
+    __syncthreads();  // stage kt+1 visible; stage kt's buffer free
     if (BKIND == B_MXFP8) {
 #pragma unroll
       for (int j = 0; j < TN; ++j) sc_cur[j] = sc_next[j];
     }
-    if (kt + STAGES - 1 < KT) issue_stage(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
-    const char* As = lds + (kt % STAGES) * STAGE;
-    const char* Bs = As + A_BYTES;
-    // Fragments of k-step kk+1 are read while the MFMAs of kk run.
-    bf16x8 af[2][TM], bw[2][TN];
-    auto read_frags = [&](int kk, bf16x8* fa, bf16x8* fb) {
-      const int ca = ((kk * 2 + frag_c) ^ a_swz) * 16;
-#pragma unroll
-      for (int i = 0; i < TM; ++i) fa[i] = *reinterpret_cast<const bf16x8*>(As + a_off[i] + ca);
-      if (!B8) {
-#pragma unroll
-        for (int j = 0; j < TN; ++j) fb[j] = *reinterpret_cast<const bf16x8*>(Bs + b_off[j] + ca);
-      } else {
-        const int c8 = kk * 2 + frag_c;  // 8-byte chunk of the 64-byte row
-        const int cb = ((c8 >> 1) ^ b_swz) * 16 + (c8 & 1) * 8;
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          const u32x2 raw = *reinterpret_cast<const u32x2*>(Bs + b_off[j] + cb);
-          uint32_t o[4];
-          if (BKIND == B_INT8) {
-            const float s = s_i8[j], nb = -128.0f * s;
-#pragma unroll
-            for (int d = 0; d < 2; ++d) {
-              const uint32_t u = raw[d] ^ 0x80808080u;
-              bf16x2 p0, p1;
-              p0[0] = (bf16)fmaf((float)(u & 0xffu), s, nb);
-              p0[1] = (bf16)fmaf((float)((u >> 8) & 0xffu), s, nb);
-              p1[0] = (bf16)fmaf((float)((u >> 16) & 0xffu), s, nb);
-              p1[1] = (bf16)fmaf((float)(u >> 24), s, nb);
-              o[2 * d] = __builtin_bit_cast(uint32_t, p0);
-              o[2 * d + 1] = __builtin_bit_cast(uint32_t, p1);
-            }
-          } else {
-            const float sc = e8m0_to_f32((sc_cur[j] >> (8 * (kk >> 1))) & 0xffu);
-#pragma unroll
-            for (int d = 0; d < 2; ++d) {
-              o[2 * d] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[d], sc, false));
-              o[2 * d + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[d], sc, true));
-            }
-          }
-          fb[j] = __builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]});
-        }
-      }
-    };
-    read_frags(0, af[0], bw[0]);
-#pragma unroll
-    for (int kk = 0; kk < kBK / 16; ++kk) {
-      const int cb = kk & 1;
-      // Fence the schedule: fragment reads of step kk+1 are issued before
-      // the MFMAs of step kk, so their LDS latency hides behind 16 MFMAs.
-      if (kk + 1 < kBK / 16) read_frags(kk + 1, af[cb ^ 1], bw[cb ^ 1]);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[cb][j], af[cb][i], acc[i][j], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+    if (kt + STAGES < KT) issue_stage(kt + STAGES, buf);
+    if (BKIND == B_MXFP8 && kt + 2 < KT) load_scales(kt + 2);
+    read_frags((kt + 1) % STAGES, 0, fa[0], fb[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(fa[1], fb[1]);  // k-step 3 of stage kt behind the next stage's first reads
+    __builtin_amdgcn_sched_barrier(0);
   }
+  first3((KT - 1) % STAGES);
+  wait_lgkmcnt0();
+  __builtin_amdgcn_sched_barrier(0);
+  mfmas(fa[1], fb[1]);
+  __builtin_amdgcn_sched_barrier(0);
   __syncthreads();  // all waves done with the stage buffers before reuse
 
   // ---- epilogue phase 1: registers -> bf16 tile in LDS (per wave) ----
@@ -382,11 +432,11 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
   }
 }
 
-template <int BM, int BN, int BKIND, int EPI>
+template <int BM, int BN, int BKIND, int EPI, int SWZ = 0>
 static void launch_tile(GemmArgs p, hipStream_t s) {
   p.tiles_m = (p.M + BM - 1) / BM;
   p.tiles_n = (p.N + BN - 1) / BN;
-  gemm_kernel<BM, BN, BKIND, EPI><<<p.tiles_m * p.tiles_n, kGemmThreads, 0, s>>>(p);
+  gemm_kernel<BM, BN, BKIND, EPI, SWZ><<<p.tiles_m * p.tiles_n, kGemmThreads, 0, s>>>(p);
 }
 
 template <int BKIND, int EPI>
@@ -398,15 +448,19 @@ static void launch_epi(const GemmArgs& p, int tile, hipStream_t s) {
   }
   if (tile == 1)
     launch_tile<256, 256, BKIND, EPI>(p, s);
-  else
+  else if (tile == 2)
     launch_tile<128, 128, BKIND, EPI>(p, s);
+  else if (tile == 3)
+    launch_tile<256, 256, BKIND, EPI, 1>(p, s);
+  else
+    launch_tile<128, 128, BKIND, EPI, 1>(p, s);
 }
 
 template <int BKIND>
 static int launch_kind(const GemmArgs& p, int epilogue, hipStream_t s) {
   const int epi = epilogue & 0xff;
   const int tile = (epilogue >> 8) & 0xf;
-  if (tile > 2) return LTX_ERR_INVALID_ARG;
+  if (tile > 4) return LTX_ERR_INVALID_ARG;
   switch (epi) {
     case LTX_GEMM_EPI_BIAS: launch_epi<BKIND, LTX_GEMM_EPI_BIAS>(p, tile, s); break;
     case LTX_GEMM_EPI_GELU: launch_epi<BKIND, LTX_GEMM_EPI_GELU>(p, tile, s); break;
