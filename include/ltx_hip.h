@@ -193,6 +193,7 @@ int ltx_broadcast_add_f32(const float* table, const float* vec, float* out, int6
 #define LTX_GEMM_EPI_SIGMOID2 4       /* C = bf16(2 * bf16(sigmoid(bf16(acc + bias)))) (attention.py:563-569) */
 #define LTX_GEMM_TILE_256 (1 << 8)
 #define LTX_GEMM_TILE_128 (2 << 8)
+#define LTX_GEMM_TILE_256_DMA (3 << 8) /* 256x256, LDS-DMA loader */
 
 int ltx_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, const float* bias,
                   void* C, int64_t ldc, int64_t M, int64_t N, int64_t K, int epilogue,

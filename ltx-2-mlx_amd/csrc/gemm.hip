@@ -14,30 +14,43 @@
 // Both operands are K-contiguous, which is what the MFMA fragments want.
 //
 // Kernel structure (one 256-thread workgroup = 4 waves in a 2x2 grid):
-//   * block tile BM x BN, K step 64, 2 or 4 LDS stages filled by direct
-//     global->LDS DMA (global_load_lds_dwordx4): no staging registers, the
-//     loads of later stages fly while the MFMAs of stage k run; one barrier
-//     per K step.
+//   * block tile BM x BN (256x256 or 128x128), K step 64, two LDS stages plus
+//     a third stage in flight, by one of two loaders:
+//       - registers (default): the global loads of stage k+2 go to VGPRs while
+//         stage k computes; during stage k each lane writes its registers of
+//         stage k+1 to LDS and reloads them with stage k+2, one pair every
+//         few MFMAs, so loads and LDS writes never idle the matrix pipe;
+//       - LDS DMA (global_load_lds_dwordx4) straight into the freed buffer,
+//         spread over the last k-step's MFMAs.
+//     One barrier per K step.
 //   * quantised weights travel to LDS as their 8-bit codes (half the bytes)
 //     and are dequantised to bf16 as each lane reads its MFMA fragment, with
 //     the exact format arithmetic, so the bf16 MFMA sees bit-exact weights.
 //   * LDS rows are 128 bytes (64 bf16; 64 codes for 8-bit weights); 16-byte
 //     chunks are XOR-swizzled ((row/2)%8, or (row/4)%4 for 64-byte rows) so
-//     the fragment reads of consecutive rows spread over the banks.  The DMA
+//     the fragment reads of consecutive rows spread over the banks.  The load
 //     source address of each lane implements the swizzle.
-//   * fragments of k-step kk+1 are read from LDS before the MFMAs of kk issue.
+//   * fragments of k-step kk+1 are read from LDS before the MFMAs of kk issue,
+//     across the stage boundary too.
 //   * v_mfma_f32_32x32x16_bf16 with the weight fragment as the MFMA "A"
 //     operand: each lane then holds 4 consecutive output columns, so the
 //     epilogue packs 4 bf16 per LDS write and streams the tile out through LDS
 //     in coalesced 16-byte chunks, fusing bias, GELU-tanh, the 2*sigmoid head
-//     gate or the gated residual add (fused_ops.py:345-348 semantics).
+//     gate or the gated residual add (fused_ops.py:345-348 semantics).  Bias
+//     and gate columns come from LDS and residual rows are fetched before the
+//     tile is staged, so the epilogue never waits on memory per element.
 //   * blockIdx -> tile: consecutive tiles go to the same XCD (the hardware
 //     round-robins workgroups over the 8 XCDs), grouped 8 tile-rows at a time.
+#include <type_traits>
+
 #include "ltx_common.h"
 
 namespace ltx {
 
 enum BKind { B_BF16 = 0, B_INT8 = 1, B_MXFP8 = 2 };
+// How stage tiles reach LDS: LDS DMA (global_load_lds), or global loads into
+// registers one stage ahead that are written to LDS during the next stage.
+enum Loader { LOAD_DMA = 0, LOAD_REG = 1 };
 
 struct GemmArgs {
   const bf16* A;
@@ -57,23 +70,28 @@ struct GemmArgs {
   int tiles_m, tiles_n;
 };
 
-constexpr int kBK = 64;
 constexpr int kGemmThreads = 256;
 constexpr int kGroupM = 8;
 constexpr int kNumXcd = 8;
 
-__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
-
 // GELU with the tanh approximation (feed_forward.py:8-14).  tanh(u) is
-// evaluated as 1 - 2 / (exp(2u) + 1) with the hardware exp2: a few
-// instructions instead of the libm tanh, absolute error ~1e-7, far below
-// the bf16 rounding of the result; saturates correctly at +-inf.
+// evaluated as 1 - 2 / (exp(2u) + 1) with the hardware exp2 and reciprocal
+// a few instructions instead of the libm tanh and an IEEE division, absolute
+// error ~2e-7, far below the bf16 rounding of the result; saturates correctly
+// at +-inf.
 __device__ __forceinline__ float gelu_tanh(float x) {
   const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
   const float u = k0 * (x + 0.044715f * x * x * x);
-  const float e = exp2f(u * 2.8853900817779268f);  // exp(2u)
-  const float t = 1.0f - 2.0f / (e + 1.0f);
+  const float e = __builtin_amdgcn_exp2f(u * 2.8853900817779268f);  // exp(2u)
+  const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
   return 0.5f * x * (1.0f + t);
+}
+
+// 2 * bf16(sigmoid(y)) -- the head gate of attention.py:586-590 -- with the
+// hardware exp2 and reciprocal (relative error ~2e-7 before the bf16 rounding).
+__device__ __forceinline__ float sigmoid2_bf(float y) {
+  const float e = __builtin_amdgcn_exp2f(-1.4426950408889634f * y);
+  return 2.0f * round_bf(__builtin_amdgcn_rcpf(1.0f + e));
 }
 
 __device__ __forceinline__ float e8m0_to_f32(uint32_t s) {
@@ -118,44 +136,57 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
-template <int BM, int BN, int BKIND, int EPI, int SWZ = 0>
+template <int BM, int BN, int BK, int STAGES_, int BKIND, int EPI, int SWZ, int LOADER>
 struct GemmCfg {
   static constexpr int WM = BM / 2, WN = BN / 2;    // wave tile (2 x 2 waves)
   static constexpr int TM = WM / 32, TN = WN / 32;  // 32x32 MFMA tiles per wave
   static constexpr bool B8 = BKIND != B_BF16;
-  static constexpr int A_ROWB = kBK * 2;             // 128 B per bf16 row
-  static constexpr int B_ROWB = B8 ? kBK : kBK * 2;  // 64 B per 8-bit row
+  static constexpr int KSTEPS = BK / 16;             // MFMA k-steps per stage
+  static constexpr int A_ROWB = BK * 2;              // bytes per LDS row
+  static constexpr int B_ROWB = B8 ? BK : BK * 2;
   static constexpr int A_BYTES = BM * A_ROWB, B_BYTES = BN * B_ROWB;
   static constexpr int STAGE = A_BYTES + B_BYTES;
-  // MXFP8 scales ride in registers one stage ahead, so that format keeps two
-  // stages; the others use four when they fit.
-  static constexpr int STAGES = (BKIND != B_MXFP8 && 4 * STAGE <= 160 * 1024 - 8192) ? 4 : 2;
+  static constexpr int STAGES = STAGES_;
   // per-lane DMA instructions per stage (each wave instruction moves 1 KiB)
   static constexpr int A_DMA = A_BYTES / 1024 / 4;
   static constexpr int B_DMA = B_BYTES / 1024 / 4;
+  static constexpr int L = A_DMA + B_DMA;
   static constexpr int EPI_ROWB = WN * 2 + 16;  // padded epilogue row
   static constexpr int EPI_WAVE = WM * EPI_ROWB;
   static constexpr int EPI_BYTES = 4 * EPI_WAVE;
   static constexpr int LDS_BYTES = (STAGES * STAGE > EPI_BYTES) ? STAGES * STAGE : EPI_BYTES;
+  static_assert(BK == 32 || BK == 64, "K step");
+  static_assert(!B8 || BK == 64, "8-bit weights use 64-byte rows");
+  static_assert(BKIND != B_MXFP8 || STAGES == 2, "MXFP8 scales ride one stage ahead");
+  static_assert(LOADER == LOAD_DMA || STAGES == 2, "register staging is the third stage");
+  static constexpr int COL_BYTES = 2 * BN * 4;  // epilogue bias + gate columns
+  static_assert(LDS_BYTES + COL_BYTES <= 160 * 1024, "LDS");
+  static_assert((STAGES - 1) * L < 64, "vmcnt range");
 };
 
-// bf16 row swizzle (16-byte chunk index XOR): SWZ 0 uses (row/2)%8 (conflict-free
-// for 16-lane / 256-byte bank groups), SWZ 1 uses row%8 (8-lane / 128-byte).
-template <int SWZ>
-__device__ __forceinline__ int rswz(int r) { return SWZ == 0 ? ((r >> 1) & 7) : (r & 7); }
+// 16-byte chunk XOR of an LDS row.  128-byte rows: SWZ 0 uses (row/2)%8
+// (conflict-free per 16 lanes over 256 bytes of banks), SWZ 1 uses row%8.
+// 64-byte rows: (row/4)%4.
+template <int ROWB, int SWZ>
+__device__ __forceinline__ int chunk_xor(int r) {
+  if constexpr (ROWB == 128) return SWZ == 0 ? ((r >> 1) & 7) : (r & 7);
+  else return (r >> 2) & 3;
+}
 
-template <int BM, int BN, int BKIND, int EPI, int SWZ = 0>
+template <int BM, int BN, int BK, int STAGES_, int BKIND, int EPI, int SWZ, int LOADER>
 __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
-  using Cfg = GemmCfg<BM, BN, BKIND, EPI, SWZ>;
+  using Cfg = GemmCfg<BM, BN, BK, STAGES_, BKIND, EPI, SWZ, LOADER>;
+  constexpr bool REG = LOADER == LOAD_REG;
   constexpr int WM = Cfg::WM, WN = Cfg::WN, TM = Cfg::TM, TN = Cfg::TN;
   constexpr bool B8 = Cfg::B8;
-  constexpr int STAGES = Cfg::STAGES;
+  constexpr int STAGES = Cfg::STAGES, KSTEPS = Cfg::KSTEPS;
   constexpr int STAGE = Cfg::STAGE;
   constexpr int A_BYTES = Cfg::A_BYTES;
   constexpr int A_ROWB = Cfg::A_ROWB, B_ROWB = Cfg::B_ROWB;
-  constexpr int A_DMA = Cfg::A_DMA, B_DMA = Cfg::B_DMA;
+  constexpr int A_DMA = Cfg::A_DMA, B_DMA = Cfg::B_DMA, L = Cfg::L;
   constexpr int EPI_ROWB = Cfg::EPI_ROWB, EPI_WAVE = Cfg::EPI_WAVE;
-  __shared__ __attribute__((aligned(1024))) char lds[Cfg::LDS_BYTES];
+  __shared__ __attribute__((aligned(1024))) char lds[Cfg::LDS_BYTES + Cfg::COL_BYTES];
+  constexpr bool RESID = EPI == LTX_GEMM_EPI_RESIDUAL || EPI == LTX_GEMM_EPI_RESIDUAL_ROUND;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -165,33 +196,37 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
   int tmi, tni;
   tile_coords(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, tmi, tni);
   const int m0 = tmi * BM, n0 = tni * BN;
-  const int KT = p.K / kBK;
+  const int KT = p.K / BK;
 
-  // ---- DMA source addresses (k = 0).  A: wave instruction i covers tile rows
-  // 8*(4*i + wave) .. +8, lane -> row +lane/8, LDS slot lane%8 which holds
-  // logical chunk (lane%8) ^ ((row/2)%8).
+  // The epilogue's per-column vectors (bias; gate of the residual forms) are
+  // loaded once here, one column per thread, and reach the epilogue through
+  // LDS, so no column group waits on global memory there.
+  float col_bias = 0.0f, col_gate = 0.0f;
+  if (tid < BN && n0 + tid < p.N) {
+    if (p.bias) col_bias = p.bias[n0 + tid];
+    if (RESID) col_gate = p.gate[n0 + tid];
+  }
+  float* col_lds = reinterpret_cast<float*>(lds + Cfg::LDS_BYTES);
+
+  // ---- DMA source addresses (k = 0).  Wave instruction i of a tile covers
+  // its 1 KiB block 4*i + wave: rows (1024 / ROWB) * (4*i + wave) + lane / LPR
+  // with LPR = ROWB / 16 lanes per row; lane slot lane % LPR holds logical
+  // chunk slot ^ chunk_xor(row).  Rows past M / N re-read the last row.
+  constexpr int A_LPR = A_ROWB / 16, B_LPR = B_ROWB / 16;
   const char* a_src[A_DMA];
 #pragma unroll
   for (int i = 0; i < A_DMA; ++i) {
-    const int r = 8 * (4 * i + wave) + (lane >> 3);
+    const int r = (1024 / A_ROWB) * (4 * i + wave) + lane / A_LPR;
     int gm = m0 + r;
     gm = gm < p.M ? gm : p.M - 1;
-    const int chunk = (lane & 7) ^ rswz<SWZ>(r);
+    const int chunk = (lane % A_LPR) ^ chunk_xor<A_ROWB, SWZ>(r);
     a_src[i] = (const char*)(p.A + (int64_t)gm * p.lda) + chunk * 16;
   }
-  // B: bf16 like A; 8-bit rows are 64 B: 16 rows per wave instruction, lane ->
-  // row +lane/4, 16-byte slot lane%4 holding chunk (lane%4) ^ ((row/4)%4).
   const char* b_src[B_DMA];
 #pragma unroll
   for (int i = 0; i < B_DMA; ++i) {
-    int r, chunk;
-    if (B8) {
-      r = 16 * (4 * i + wave) + (lane >> 2);
-      chunk = (lane & 3) ^ ((r >> 2) & 3);
-    } else {
-      r = 8 * (4 * i + wave) + (lane >> 3);
-      chunk = (lane & 7) ^ rswz<SWZ>(r);
-    }
+    const int r = (1024 / B_ROWB) * (4 * i + wave) + lane / B_LPR;
+    const int chunk = (lane % B_LPR) ^ chunk_xor<B_ROWB, SWZ>(r);
     int gn = n0 + r;
     gn = gn < p.N ? gn : p.N - 1;
     b_src[i] = (const char*)p.B + (int64_t)gn * p.ldb * (B8 ? 1 : 2) + chunk * 16;
@@ -212,36 +247,44 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
   // MXFP8 scales of one stage: 2 E8M0 bytes (k blocks 0/1 of the 64) per row.
   uint32_t sc_cur[TN], sc_next[TN];
 
-  // One stage's A and B tiles by LDS DMA (MXFP8 scales travel separately).
-  auto issue_stage = [&](int kt, int buf) {
+  // DMA instruction d (0 <= d < L) of stage kt into buffer buf.  Every stage
+  // issues all L instructions; stages past the last one re-read stage KT-1
+  // into a buffer that is never read again, so the number of outstanding
+  // instructions per stage is the same everywhere.
+  auto dma_op = [&](int d, int kt, int buf) {
     char* As = lds + buf * STAGE;
-    char* Bs = As + A_BYTES;
-    const int64_t ka = (int64_t)kt * kBK * 2;
-#pragma unroll
-    for (int i = 0; i < A_DMA; ++i) dma16(a_src[i] + ka, As + (4 * i + wave) * 1024);
-    const int64_t kb = (int64_t)kt * kBK * (B8 ? 1 : 2);
-#pragma unroll
-    for (int i = 0; i < B_DMA; ++i) dma16(b_src[i] + kb, Bs + (4 * i + wave) * 1024);
+    if (d < A_DMA) {
+      dma16(a_src[d] + (int64_t)kt * (BK * 2), As + (4 * d + wave) * 1024);
+    } else {
+      const int i = d - A_DMA;
+      dma16(b_src[i] + (int64_t)kt * (B8 ? BK : BK * 2), As + A_BYTES + (4 * i + wave) * 1024);
+    }
+  };
+  // Register-staged loader: load d of stage kt into rg[d], and its LDS write.
+  typedef __attribute__((address_space(1))) const u32x4* g16_t;
+  u32x4 rg[REG ? L : 1];
+  auto gload = [&](int d, int kt) {
+    if constexpr (REG) {
+      if (d < A_DMA) rg[d] = *(g16_t)(a_src[d] + (int64_t)kt * (BK * 2));
+      else rg[d] = *(g16_t)(b_src[d - A_DMA] + (int64_t)kt * (B8 ? BK : BK * 2));
+    }
+  };
+  auto lwrite = [&](int d, int buf) {
+    if constexpr (REG) {
+      char* As = lds + buf * STAGE;
+      char* dst = d < A_DMA ? As + (4 * d + wave) * 1024 : As + A_BYTES + (4 * (d - A_DMA) + wave) * 1024;
+      *reinterpret_cast<u32x4*>(dst + lane * 16) = rg[d];
+    }
   };
   auto load_scales = [&](int kt) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) sc_next[j] = *reinterpret_cast<const uint16_t*>(sc_row[j] + kt * 2);
   };
-  // Wait until the oldest outstanding stage has landed while `ahead` later
-  // stages may stay in flight (vmcnt counts this lane's DMA instructions).
-  constexpr int L = A_DMA + B_DMA;
-  auto wait_ahead = [&](int ahead) {
-    if constexpr (BKIND == B_MXFP8) {
-      wait_vmcnt<0>();  // scale loads share the counter
-    } else if constexpr (STAGES == 4) {
-      if (ahead >= 3) wait_vmcnt<3 * L>();
-      else if (ahead == 2) wait_vmcnt<2 * L>();
-      else if (ahead == 1) wait_vmcnt<L>();
-      else wait_vmcnt<0>();
-    } else {
-      if (ahead >= 1) wait_vmcnt<L>();
-      else wait_vmcnt<0>();
-    }
+  // Stage kt+1 landed while the (STAGES-2) younger stages stay in flight.
+  auto wait_next_stage = [&]() {
+    if constexpr (REG) return;  // the compiler tracks register loads itself
+    else if constexpr (BKIND == B_MXFP8) wait_vmcnt<0>();  // scale loads share the counter
+    else wait_vmcnt<(STAGES - 2) * L>();
   };
 
   f32x16 acc[TM][TN];
@@ -257,8 +300,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
   for (int i = 0; i < TM; ++i) a_off[i] = (wm * WM + i * 32 + frag_r) * A_ROWB;
 #pragma unroll
   for (int j = 0; j < TN; ++j) b_off[j] = (wn * WN + j * 32 + frag_r) * B_ROWB;
-  const int a_swz = rswz<SWZ>(frag_r);  // same for rows i*32+frag_r
-  const int b_swz = B8 ? ((frag_r >> 2) & 3) : a_swz;
+  const int a_swz = chunk_xor<A_ROWB, SWZ>(frag_r);  // same for rows i*32+frag_r
+  const int b_swz = chunk_xor<B_ROWB, SWZ>(frag_r);
 
   // Fragment reads of k-step kk of the stage in buffer `buf` (8-bit weights
   // dequantised here with the scales in sc_cur).
@@ -310,135 +353,230 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
       for (int j = 0; j < TN; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
   };
+  // MFMAs of one k-step with memory instructions spread between them:
+  // op(m) issues what belongs after MFMA m.  Issuing loads or LDS writes this
+  // way never idles the matrix pipe.
+  auto mfmas_with = [&](const bf16x8* fa, const bf16x8* fb, auto&& op) {
+    constexpr int NM = TM * TN;
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      const int i = m / TN, j = m % TN;
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
+      op(m);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // the L loads of stage kt_src, spread over the NM MFMAs of one k-step
+  auto loads_at = [&](int kt_src, int buf) {
+    return [&, kt_src, buf](int m) {
+      constexpr int NM = TM * TN;
+#pragma unroll
+      for (int d = 0; d < L; ++d)
+        if ((d * NM) / L == m) {
+          dma_op(d, kt_src, buf);
+        }
+    };
+  };
 
-  // Software pipeline: stages fill all STAGES buffers ahead; fragments of the
+  // Software pipeline: all STAGES buffers are filled ahead; fragments of the
   // next k-step are read while the MFMAs of the current one run, including
   // across the stage boundary, whose barrier sits between the fragment reads
-  // of k-step 3 and its MFMAs.
+  // of the last k-step and its MFMAs.
   bf16x8 fa[2][TM], fb[2][TN];
-  const int pro = KT < STAGES ? KT : STAGES;
+  if constexpr (REG) {
 #pragma unroll
-  for (int st = 0; st < STAGES; ++st)
-    if (st < KT) issue_stage(st, st);
-  if (BKIND == B_MXFP8) load_scales(0);
-  wait_ahead(pro - 1);
+    for (int d = 0; d < L; ++d) gload(d, 0);
+#pragma unroll
+    for (int d = 0; d < L; ++d) lwrite(d, 0);
+#pragma unroll
+    for (int d = 0; d < L; ++d) gload(d, KT > 1 ? 1 : 0);
+  } else {
+#pragma unroll
+    for (int st = 0; st < STAGES; ++st)
+#pragma unroll
+      for (int d = 0; d < L; ++d) dma_op(d, st < KT ? st : KT - 1, st);
+  }
   if (BKIND == B_MXFP8) {
+    load_scales(0);
+    wait_vmcnt<0>();
 #pragma unroll
     for (int j = 0; j < TN; ++j) sc_cur[j] = sc_next[j];
-    if (KT > 1) load_scales(1);
+    load_scales(KT > 1 ? 1 : 0);
+  } else if constexpr (!REG) {
+    wait_vmcnt<(STAGES - 1) * L>();
   }
   __syncthreads();
   read_frags(0, 0, fa[0], fb[0]);
   wait_lgkmcnt0();
 
-  // k-steps 0..2 of the stage in `buf`: read k-step kk+1, then MFMAs of kk.
-  // The fragments of kk were issued one MFMA block earlier; waiting for them
-  // before issuing the next reads keeps at most one group (TM+TN <= 8 reads)
-  // in flight, which the 4-bit LDS counter can track exactly.
-  auto first3 = [&](int buf) {
+  // k-steps 0..KSTEPS-2 of the stage in `buf`: read k-step kk+1, then MFMAs of
+  // kk.  The fragments of kk were issued one MFMA block earlier; waiting for
+  // them before issuing the next reads keeps at most one group (TM+TN <= 8
+  // reads) in flight, which the 4-bit LDS counter can track exactly.
+  // With the register loader, the LDS writes of the next stage (into wbuf),
+  // each followed by the global load of the stage after it into the same
+  // registers (kt_load), are spread evenly over these k-steps' MFMAs.
+  auto leading_ksteps = [&](int buf, int wbuf, bool write, int kt_load) {
 #pragma unroll
-    for (int kk = 0; kk < kBK / 16 - 1; ++kk) {
+    for (int kk = 0; kk < KSTEPS - 1; ++kk) {
       wait_lgkmcnt0();
       read_frags(buf, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
       __builtin_amdgcn_sched_barrier(0);
-      mfmas(fa[kk & 1], fb[kk & 1]);
+      if constexpr (REG) {
+        constexpr int NM = TM * TN, SLOTS = (KSTEPS - 1) * NM;
+        mfmas_with(fa[kk & 1], fb[kk & 1], [&](int m) {
+#pragma unroll
+          for (int d = 0; d < L; ++d)
+            if ((d * SLOTS) / L == kk * NM + m && write) {
+              lwrite(d, wbuf);
+              gload(d, kt_load);
+            }
+        });
+      } else {
+        mfmas(fa[kk & 1], fb[kk & 1]);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
+  constexpr int LASTF = (KSTEPS - 1) & 1;  // fragment set of the last k-step
+  int buf = 0;
   for (int kt = 0; kt < KT - 1; ++kt) {
-    const int buf = kt % STAGES;
-    first3(buf);
-    const int ahead = (KT - 2 - kt) < (STAGES - 2) ? (KT - 2 - kt) : (STAGES - 2);
-    wait_ahead(ahead);
-    __syncthreads();  // stage kt+1 visible; stage kt's buffer free
+    const int nbuf = buf + 1 == STAGES ? 0 : buf + 1;
+    leading_ksteps(buf, nbuf, true, kt + 2 < KT ? kt + 2 : KT - 1);
+    wait_next_stage();
+    __syncthreads();  // stage kt+1 visible to all waves; stage kt's buffer free
     if (BKIND == B_MXFP8) {
 #pragma unroll
       for (int j = 0; j < TN; ++j) sc_cur[j] = sc_next[j];
     }
-    if (kt + STAGES < KT) issue_stage(kt + STAGES, buf);
-    if (BKIND == B_MXFP8 && kt + 2 < KT) load_scales(kt + 2);
-    read_frags((kt + 1) % STAGES, 0, fa[0], fb[0]);
+    read_frags(nbuf, 0, fa[0], fb[0]);
     __builtin_amdgcn_sched_barrier(0);
-    mfmas(fa[1], fb[1]);  // k-step 3 of stage kt behind the next stage's first reads
-    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (REG) {
+      mfmas(fa[LASTF], fb[LASTF]);
+    } else {  // DMA of stage kt+STAGES into the freed buffer
+      const int kt_src = kt + STAGES < KT ? kt + STAGES : KT - 1;
+      mfmas_with(fa[LASTF], fb[LASTF], loads_at(kt_src, buf));
+    }
+    if (BKIND == B_MXFP8) load_scales(kt + 2 < KT ? kt + 2 : KT - 1);
+    buf = nbuf;
   }
-  first3((KT - 1) % STAGES);
+  leading_ksteps(buf, buf, false, 0);
   wait_lgkmcnt0();
   __builtin_amdgcn_sched_barrier(0);
-  mfmas(fa[1], fb[1]);
+  mfmas(fa[LASTF], fb[LASTF]);
   __builtin_amdgcn_sched_barrier(0);
-  __syncthreads();  // all waves done with the stage buffers before reuse
-
-  // ---- epilogue phase 1: registers -> bf16 tile in LDS (per wave) ----
-  // acc[i][j] reg 4g+e holds C[m][n] with m = i*32 + lane%32 and
-  // n = j*32 + 8g + 4*(lane/32) + e (wave-local coordinates).
-  char* E = lds + wave * EPI_WAVE;
-#pragma unroll
-  for (int j = 0; j < TN; ++j) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int nl = j * 32 + 8 * g + 4 * frag_c;
-      const int gn = n0 + wn * WN + nl;
-      float bias4[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) bias4[e] = (p.bias && gn + e < p.N) ? p.bias[gn + e] : 0.0f;
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        bf16x4 v;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float y = round_bf(acc[i][j][4 * g + e] + bias4[e]);
-          if (EPI == LTX_GEMM_EPI_GELU) y = gelu_tanh(y);
-          if (EPI == LTX_GEMM_EPI_SIGMOID2 || (EPI == LTX_GEMM_EPI_BIAS && gn + e >= p.sig_from))
-            y = 2.0f * round_bf(1.0f / (1.0f + expf(-y)));
-          v[e] = (bf16)y;
-        }
-        *reinterpret_cast<bf16x4*>(E + (i * 32 + frag_r) * EPI_ROWB + nl * 2) = v;
-      }
-    }
+  wait_vmcnt<0>();  // the re-read stages land before the epilogue reuses LDS
+  if (tid < BN) {
+    col_lds[tid] = col_bias;
+    col_lds[BN + tid] = col_gate;
   }
-  __syncthreads();
+  __syncthreads();  // all waves done with the stage buffers; columns visible
 
-  // ---- epilogue phase 2: coalesced 16-byte stores (+ gated residual) ----
+  // ---- epilogue: registers -> bf16 tile in LDS (per wave), then coalesced
+  // 16-byte row stores.  Phase-2 lane mapping: 16-byte chunk ch of rows
+  // it * ROWS_PER_IT + rsub of the wave tile.
   constexpr int CHUNKS = WN / 8;  // 16-byte chunks per wave-tile row
   constexpr int ROWS_PER_IT = 64 / CHUNKS;
+  constexpr int ITS = WM / ROWS_PER_IT;
   const int ch = lane % CHUNKS;
   const int rsub = lane / CHUNKS;
-  const int gn = n0 + wn * WN + ch * 8;
-  float g8[8];
-  if (EPI == LTX_GEMM_EPI_RESIDUAL || EPI == LTX_GEMM_EPI_RESIDUAL_ROUND) {
+  const int gn2 = n0 + wn * WN + ch * 8;
+  const bool col_ok = gn2 < p.N;  // N % 8 == 0: a chunk is all in or all out
+  // Residual rows are fetched before phase 1 so their latency overlaps it
+  // (rows past M re-read row M-1, columns past N read column 0; neither is
+  // stored).  The residual may alias C: every residual element of this tile
+  // is read before any of its outputs is written.
+  bf16x8 res[RESID ? ITS : 1];
+  if constexpr (RESID) {
+    const int gnc = col_ok ? gn2 : 0;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) g8[e] = gn + e < p.N ? p.gate[gn + e] : 0.0f;
+    for (int it = 0; it < ITS; ++it) {
+      int gm = m0 + wm * WM + it * ROWS_PER_IT + rsub;
+      gm = gm < p.M ? gm : p.M - 1;
+      res[it] = *reinterpret_cast<const bf16x8*>(p.R + (int64_t)gm * p.ldr + gnc);
+    }
   }
-  for (int rr = 0; rr < WM; rr += ROWS_PER_IT) {
-    const int ml = rr + rsub;
+
+  // phase 1: acc[i][j] reg 4g+e holds C[m][n] with m = i*32 + lane%32 and
+  // n = j*32 + 8g + 4*(lane/32) + e (wave-local coordinates).  Whether any
+  // column of this wave tile takes the head-gate sigmoid is wave-uniform, so
+  // the common case runs without it.
+  char* E = lds + wave * EPI_WAVE;
+  auto phase1 = [&](auto sig_tag) {
+    constexpr bool SIG = decltype(sig_tag)::value;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int nl = j * 32 + 8 * g + 4 * frag_c;
+        const int gn = n0 + wn * WN + nl;
+        const f32x4 bias4 = *reinterpret_cast<const f32x4*>(col_lds + wn * WN + nl);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          float y[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            y[e] = acc[i][j][4 * g + e] + bias4[e];
+            if (EPI == LTX_GEMM_EPI_GELU) y[e] = gelu_tanh(round_bf(y[e]));
+            if (EPI == LTX_GEMM_EPI_SIGMOID2) y[e] = sigmoid2_bf(round_bf(y[e]));
+            if (SIG && gn + e >= p.sig_from) y[e] = sigmoid2_bf(round_bf(y[e]));
+          }
+          bf16x4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = (bf16)y[e];
+          *reinterpret_cast<bf16x4*>(E + (i * 32 + frag_r) * EPI_ROWB + nl * 2) = v;
+        }
+      }
+    }
+  };
+  if (EPI == LTX_GEMM_EPI_BIAS && n0 + wn * WN + WN > p.sig_from)
+    phase1(std::true_type{});
+  else
+    phase1(std::false_type{});
+  __syncthreads();
+
+  // phase 2: coalesced 16-byte stores (+ gated residual)
+  float g8[8];
+  if constexpr (RESID) {
+    const f32x4 ga = *reinterpret_cast<const f32x4*>(col_lds + BN + wn * WN + ch * 8);
+    const f32x4 gb = *reinterpret_cast<const f32x4*>(col_lds + BN + wn * WN + ch * 8 + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      g8[e] = ga[e];
+      g8[4 + e] = gb[e];
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < ITS; ++it) {
+    const int ml = it * ROWS_PER_IT + rsub;
     const int gm = m0 + wm * WM + ml;
-    if (gm >= p.M || gn >= p.N) continue;
     bf16x8 v = *reinterpret_cast<const bf16x8*>(E + ml * EPI_ROWB + ch * 16);
-    if (EPI == LTX_GEMM_EPI_RESIDUAL || EPI == LTX_GEMM_EPI_RESIDUAL_ROUND) {
-      const bf16x8 res = *reinterpret_cast<const bf16x8*>(p.R + (int64_t)gm * p.ldr + gn);
+    if constexpr (RESID) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float y = (float)v[e];
         float o;
         if (EPI == LTX_GEMM_EPI_RESIDUAL)
-          o = fmaf(g8[e], y, (float)res[e]);
+          o = fmaf(g8[e], y, (float)res[it][e]);
         else
-          o = round_bf(y * g8[e]) + (float)res[e];
+          o = round_bf(y * g8[e]) + (float)res[it][e];
         v[e] = (bf16)o;
       }
     }
-    *reinterpret_cast<bf16x8*>(p.C + (int64_t)gm * p.ldc + gn) = v;
+    if (gm < p.M && col_ok) *reinterpret_cast<bf16x8*>(p.C + (int64_t)gm * p.ldc + gn2) = v;
   }
 }
 
-template <int BM, int BN, int BKIND, int EPI, int SWZ = 0>
+template <int BM, int BN, int BK, int STAGES, int BKIND, int EPI, int SWZ = 0, int LOADER = LOAD_DMA>
 static void launch_tile(GemmArgs p, hipStream_t s) {
   p.tiles_m = (p.M + BM - 1) / BM;
   p.tiles_n = (p.N + BN - 1) / BN;
-  gemm_kernel<BM, BN, BKIND, EPI, SWZ><<<p.tiles_m * p.tiles_n, kGemmThreads, 0, s>>>(p);
+  gemm_kernel<BM, BN, BK, STAGES, BKIND, EPI, SWZ, LOADER><<<p.tiles_m * p.tiles_n, kGemmThreads, 0, s>>>(p);
 }
 
+// Tile shapes (all K step 64, two LDS stages): 256x256 and 128x128 with the
+// register-staged loader (1 and 2; 128x128 runs two workgroups per CU), and
+// 256x256 with the LDS-DMA loader (3).
 template <int BKIND, int EPI>
 static void launch_epi(const GemmArgs& p, int tile, hipStream_t s) {
   if (tile == 0) {
@@ -447,20 +585,18 @@ static void launch_epi(const GemmArgs& p, int tile, hipStream_t s) {
     tile = big >= 160 ? 1 : 2;
   }
   if (tile == 1)
-    launch_tile<256, 256, BKIND, EPI>(p, s);
+    launch_tile<256, 256, 64, 2, BKIND, EPI, 0, LOAD_REG>(p, s);
   else if (tile == 2)
-    launch_tile<128, 128, BKIND, EPI>(p, s);
-  else if (tile == 3)
-    launch_tile<256, 256, BKIND, EPI, 1>(p, s);
+    launch_tile<128, 128, 64, 2, BKIND, EPI, 0, LOAD_REG>(p, s);
   else
-    launch_tile<128, 128, BKIND, EPI, 1>(p, s);
+    launch_tile<256, 256, 64, 2, BKIND, EPI, 0, LOAD_DMA>(p, s);
 }
 
 template <int BKIND>
 static int launch_kind(const GemmArgs& p, int epilogue, hipStream_t s) {
   const int epi = epilogue & 0xff;
   const int tile = (epilogue >> 8) & 0xf;
-  if (tile > 4) return LTX_ERR_INVALID_ARG;
+  if (tile > 3) return LTX_ERR_INVALID_ARG;
   switch (epi) {
     case LTX_GEMM_EPI_BIAS: launch_epi<BKIND, LTX_GEMM_EPI_BIAS>(p, tile, s); break;
     case LTX_GEMM_EPI_GELU: launch_epi<BKIND, LTX_GEMM_EPI_GELU>(p, tile, s); break;

@@ -27,8 +27,16 @@ constexpr int kWave = 64;
 
 __device__ __forceinline__ float bf2f(bf16 v) { return (float)v; }
 __device__ __forceinline__ bf16 f2bf(float v) { return (bf16)v; }
-// Round an fp32 value to the nearest bf16 and return it widened again.
-__device__ __forceinline__ float round_bf(float v) { return (float)(bf16)v; }
+// Round an fp32 value to the nearest bf16 (RNE) and return it widened again.
+// The empty asm hides where `v` comes from: without it LLVM narrows a product
+// of two bf16-exact operands, round_bf(a * b), to a bf16 multiply whose
+// promoted form then fuses with a following add into one fma -- dropping
+// exactly the intermediate rounding the reference performs.  It emits no
+// instruction, so the compiler still sees (and guards) every real one.
+__device__ __forceinline__ float round_bf(float v) {
+  asm("" : "+v"(v));
+  return (float)(bf16)v;
+}
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -62,6 +62,7 @@ GEMM_EPI_RESIDUAL_ROUND = 3
 GEMM_EPI_SIGMOID2 = 4
 GEMM_TILE_256 = 1 << 8
 GEMM_TILE_128 = 2 << 8
+GEMM_TILE_256_DMA = 3 << 8
 
 _LIB: ctypes.CDLL | None = None
 
