@@ -255,6 +255,23 @@ int ltx_flash_attn_bf16(const void* Q, int64_t q_rs, const void* K, int64_t k_rs
                         const void* gate, int64_t gate_rs, int64_t Tq, int64_t Tk,
                         int64_t H, int64_t head_dim, float scale, void* stream);
 
+/* Split-KV form of ltx_flash_attn_bf16 for few queries over many keys (the
+ * audio-query V2A cross-attention: 68-121 queries x 3456-6144 video keys):
+ * the keys are cut into `splits` ranges processed by separate workgroups,
+ * whose partial (O, max, sum) go to `workspace` and are merged by a second
+ * kernel; same result contract as ltx_flash_attn_bf16 (the merge reorders the
+ * fp32 sums only).  workspace: device memory of at least
+ * ltx_attn_splitkv_workspace_bytes(Tq, H, head_dim, splits) bytes, 16-byte
+ * aligned, owned by the caller; concurrent calls need separate workspaces.
+ * 1 <= splits <= 256.  Same reference call site as ltx_flash_attn_bf16.
+ */
+int64_t ltx_attn_splitkv_workspace_bytes(int64_t Tq, int64_t H, int64_t head_dim, int64_t splits);
+int ltx_flash_attn_splitkv_bf16(const void* Q, int64_t q_rs, const void* K, int64_t k_rs,
+                                const void* Vt, int64_t tk_pad, void* O, int64_t o_rs,
+                                const void* gate, int64_t gate_rs, int64_t Tq, int64_t Tk,
+                                int64_t H, int64_t head_dim, float scale, int64_t splits,
+                                void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

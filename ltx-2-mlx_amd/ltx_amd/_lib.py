@@ -46,6 +46,8 @@ SIGNATURES: dict[str, list] = {
     "ltx_dequantize_w8_bf16": [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp],
     "ltx_attn_transpose_v_bf16": [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp],
     "ltx_flash_attn_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _vp],
+    "ltx_flash_attn_splitkv_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64,
+                                    _f32, _i64, _vp, _i64, _vp],
     "ltx_broadcast_add_f32": [_vp, _vp, _vp, _i64, _i64, _vp],
 }
 
@@ -83,6 +85,8 @@ def lib() -> ctypes.CDLL:
             fn.restype = ctypes.c_int
         handle.ltx_attn_vt_padded_len.argtypes = [_i64]
         handle.ltx_attn_vt_padded_len.restype = _i64
+        handle.ltx_attn_splitkv_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64]
+        handle.ltx_attn_splitkv_workspace_bytes.restype = _i64
         handle.ltx_status_string.argtypes = [ctypes.c_int]
         handle.ltx_status_string.restype = ctypes.c_char_p
         _LIB = handle

@@ -38,14 +38,31 @@ def transpose_v(v: torch.Tensor, heads: int, out: torch.Tensor | None = None) ->
     return out
 
 
+# Workgroup counts below which the key range is split over workgroups: a
+# full-size tile holds 256 queries, a split tile 128.
+_FULL_Q, _SPLIT_Q, _MIN_WG, _TARGET_WG = 256, 128, 128, 512
+
+
+def kv_splits(tq: int, tk: int, heads: int) -> int:
+    """Number of key ranges for split-KV attention (1 = single pass)."""
+    if (tq + _FULL_Q - 1) // _FULL_Q * heads >= _MIN_WG:
+        return 1
+    blocks = (tk + 63) // 64
+    base = (tq + _SPLIT_Q - 1) // _SPLIT_Q * heads
+    return max(1, min(blocks // 2, _TARGET_WG // base, 64))
+
+
 def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor | None, heads: int, *,
                     vt: torch.Tensor | None = None, gate: torch.Tensor | None = None,
-                    out: torch.Tensor | None = None, scale: float | None = None) -> torch.Tensor:
+                    out: torch.Tensor | None = None, scale: float | None = None,
+                    splits: int | None = None) -> torch.Tensor:
     """softmax(q k^T * scale) v per head, optionally times a per-head gate.
 
     q (Tq, H*dh), k/v (Tk, H*dh) bf16 row views; ``vt`` may carry V already
     transposed by :func:`transpose_v`.  gate: bf16 (Tq, H) or None.  Returns
-    (Tq, H*dh) bf16 (written into ``out`` when given).
+    (Tq, H*dh) bf16 (written into ``out`` when given).  ``splits`` forces the
+    number of key ranges (default :func:`kv_splits`); more than one runs the
+    split-KV kernel pair with a workspace from the torch allocator.
     """
     d = q.shape[-1]
     dh = d // heads
@@ -70,6 +87,15 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor | None, he
             raise TypeError("gate must be bf16")
         gate = gv
         gptr = gv.data_ptr()
+    if splits is None:
+        splits = kv_splits(tq, tk, heads)
+    if splits > 1:
+        nbytes = _lib.lib().ltx_attn_splitkv_workspace_bytes(tq, heads, dh, splits)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+        _lib.call("ltx_flash_attn_splitkv_bf16", _lib.ptr(qv), qs, _lib.ptr(kv), ks, _lib.ptr(vt), tkp,
+                  ov.data_ptr(), os_, gptr, gs, tq, tk, heads, dh, float(scale), splits, ws.data_ptr(), nbytes,
+                  _lib.stream_of(q), detail=f"Tq={tq} Tk={tk} H={heads} dh={dh} splits={splits}")
+        return out
     _lib.call("ltx_flash_attn_bf16", _lib.ptr(qv), qs, _lib.ptr(kv), ks, _lib.ptr(vt), tkp, ov.data_ptr(), os_,
               gptr, gs, tq, tk, heads, dh, float(scale), _lib.stream_of(q),
               detail=f"Tq={tq} Tk={tk} H={heads} dh={dh}")

@@ -33,7 +33,8 @@ def test_library_exports_every_declared_symbol():
     missing = [s for s in declared_symbols() if not hasattr(lib, s)]
     assert not missing, missing
     # every declared symbol is bound with a signature in the ctypes layer
-    bound = set(_lib.SIGNATURES) | {"ltx_status_string", "ltx_attn_vt_padded_len"}
+    bound = set(_lib.SIGNATURES) | {"ltx_status_string", "ltx_attn_vt_padded_len",
+                                     "ltx_attn_splitkv_workspace_bytes"}
     assert set(declared_symbols()) <= bound, set(declared_symbols()) - bound
 
 
