@@ -95,9 +95,11 @@ __device__ __forceinline__ float sigmoid2_bf(float y) {
 }
 
 __device__ __forceinline__ float e8m0_to_f32(uint32_t s) {
-  if (s == 0xffu) return __uint_as_float(0x7fc00000u);
-  if (s == 0u) return __uint_as_float(0x00400000u);  // 2^-127
-  return __uint_as_float(s << 23);
+  // 2^(s-127): s << 23 is the float for 1 <= s <= 254; s = 0 (2^-127) and
+  // s = 255 (NaN) set the top mantissa bit as well.  Branch-free: s differs
+  // per lane.
+  const uint32_t special = (s == 0u || s == 0xffu) ? 0x00400000u : 0u;
+  return __uint_as_float((s << 23) | special);
 }
 
 __device__ __forceinline__ void tile_coords(int bid, int nblocks, int tiles_m, int tiles_n, int& tm,
@@ -141,15 +143,19 @@ struct GemmCfg {
   static constexpr int WM = BM / 2, WN = BN / 2;    // wave tile (2 x 2 waves)
   static constexpr int TM = WM / 32, TN = WN / 32;  // 32x32 MFMA tiles per wave
   static constexpr bool B8 = BKIND != B_BF16;
+  // 8-bit weights stay 8-bit in LDS with the DMA loader (dequantised per
+  // fragment); the register loader dequantises them once, on the way to LDS.
+  static constexpr bool B_RAW = B8 && LOADER == LOAD_DMA;
   static constexpr int KSTEPS = BK / 16;             // MFMA k-steps per stage
   static constexpr int A_ROWB = BK * 2;              // bytes per LDS row
-  static constexpr int B_ROWB = B8 ? BK : BK * 2;
+  static constexpr int B_ROWB = B_RAW ? BK : BK * 2;
+  static constexpr int B_GROWB = B8 ? BK : BK * 2;   // global bytes per weight row per stage
   static constexpr int A_BYTES = BM * A_ROWB, B_BYTES = BN * B_ROWB;
   static constexpr int STAGE = A_BYTES + B_BYTES;
   static constexpr int STAGES = STAGES_;
-  // per-lane DMA instructions per stage (each wave instruction moves 1 KiB)
+  // per-lane 16-byte loads per stage (each wave instruction moves 1 KiB)
   static constexpr int A_DMA = A_BYTES / 1024 / 4;
-  static constexpr int B_DMA = B_BYTES / 1024 / 4;
+  static constexpr int B_DMA = BN * B_GROWB / 1024 / 4;
   static constexpr int L = A_DMA + B_DMA;
   static constexpr int EPI_ROWB = WN * 2 + 16;  // padded epilogue row
   static constexpr int EPI_WAVE = WM * EPI_ROWB;
@@ -157,7 +163,7 @@ struct GemmCfg {
   static constexpr int LDS_BYTES = (STAGES * STAGE > EPI_BYTES) ? STAGES * STAGE : EPI_BYTES;
   static_assert(BK == 32 || BK == 64, "K step");
   static_assert(!B8 || BK == 64, "8-bit weights use 64-byte rows");
-  static_assert(BKIND != B_MXFP8 || STAGES == 2, "MXFP8 scales ride one stage ahead");
+  static_assert(!B_RAW || BKIND != B_MXFP8 || STAGES == 2, "MXFP8 scales ride one stage ahead");
   static_assert(LOADER == LOAD_DMA || STAGES == 2, "register staging is the third stage");
   static constexpr int COL_BYTES = 2 * BN * 4;  // epilogue bias + gate columns
   static_assert(LDS_BYTES + COL_BYTES <= 160 * 1024, "LDS");
@@ -178,7 +184,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
   using Cfg = GemmCfg<BM, BN, BK, STAGES_, BKIND, EPI, SWZ, LOADER>;
   constexpr bool REG = LOADER == LOAD_REG;
   constexpr int WM = Cfg::WM, WN = Cfg::WN, TM = Cfg::TM, TN = Cfg::TN;
-  constexpr bool B8 = Cfg::B8;
+  constexpr bool B8 = Cfg::B8, B_RAW = Cfg::B_RAW;
+  constexpr bool B_CONV = B8 && !B_RAW;  // 8-bit weights dequantised by the loader
   constexpr int STAGES = Cfg::STAGES, KSTEPS = Cfg::KSTEPS;
   constexpr int STAGE = Cfg::STAGE;
   constexpr int A_BYTES = Cfg::A_BYTES;
@@ -223,13 +230,30 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
     a_src[i] = (const char*)(p.A + (int64_t)gm * p.lda) + chunk * 16;
   }
   const char* b_src[B_DMA];
+  int b_dst[B_CONV ? B_DMA : 1];            // loader dequant: LDS byte offset of the row
+  int b_c16[B_CONV ? B_DMA : 1];            // ... and the 16-code chunk of it
+  const uint8_t* b_scr[B_CONV ? B_DMA : 1];  // MXFP8 scale row
+  float b_s8[B_CONV ? B_DMA : 1];           // int8 row scale
 #pragma unroll
   for (int i = 0; i < B_DMA; ++i) {
-    const int r = (1024 / B_ROWB) * (4 * i + wave) + lane / B_LPR;
-    const int chunk = (lane % B_LPR) ^ chunk_xor<B_ROWB, SWZ>(r);
-    int gn = n0 + r;
-    gn = gn < p.N ? gn : p.N - 1;
-    b_src[i] = (const char*)p.B + (int64_t)gn * p.ldb * (B8 ? 1 : 2) + chunk * 16;
+    if constexpr (!B_CONV) {
+      const int r = (1024 / B_ROWB) * (4 * i + wave) + lane / B_LPR;
+      const int chunk = (lane % B_LPR) ^ chunk_xor<B_ROWB, SWZ>(r);
+      int gn = n0 + r;
+      gn = gn < p.N ? gn : p.N - 1;
+      b_src[i] = (const char*)p.B + (int64_t)gn * p.ldb * (B8 ? 1 : 2) + chunk * 16;
+    } else {
+      // 64-byte code rows, 16 per wave instruction: lane -> row +lane/4,
+      // codes 16*(lane%4) .. +16 (no swizzle: it applies to the bf16 writes)
+      const int r = 16 * (4 * i + wave) + (lane >> 2);
+      int gn = n0 + r;
+      gn = gn < p.N ? gn : p.N - 1;
+      b_c16[i] = lane & 3;
+      b_dst[i] = r * B_ROWB;
+      b_src[i] = (const char*)p.B + (int64_t)gn * p.ldb + b_c16[i] * 16;
+      if (BKIND == B_MXFP8) b_scr[i] = (const uint8_t*)p.bscale + (int64_t)gn * p.ld_scale + (b_c16[i] >> 1);
+      if (BKIND == B_INT8) b_s8[i] = ((const float*)p.bscale)[gn];
+    }
   }
 
   // Per-lane weight rows of the B fragments and their scales.
@@ -241,8 +265,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
   for (int j = 0; j < TN; ++j) {
     int gn = n0 + wn * WN + j * 32 + frag_r;
     gn = gn < p.N ? gn : p.N - 1;
-    if (BKIND == B_INT8) s_i8[j] = ((const float*)p.bscale)[gn];
-    if (BKIND == B_MXFP8) sc_row[j] = (const uint8_t*)p.bscale + (int64_t)gn * p.ld_scale;
+    if (B_RAW && BKIND == B_INT8) s_i8[j] = ((const float*)p.bscale)[gn];
+    if (B_RAW && BKIND == B_MXFP8) sc_row[j] = (const uint8_t*)p.bscale + (int64_t)gn * p.ld_scale;
   }
   // MXFP8 scales of one stage: 2 E8M0 bytes (k blocks 0/1 of the 64) per row.
   uint32_t sc_cur[TN], sc_next[TN];
@@ -261,19 +285,59 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
     }
   };
   // Register-staged loader: load d of stage kt into rg[d], and its LDS write.
+  // 8-bit weight loads carry 16 codes (and, for MXFP8, the E8M0 scale of
+  // their 32-block), written to LDS as 16 dequantised bf16 in two chunks.
   typedef __attribute__((address_space(1))) const u32x4* g16_t;
+  typedef __attribute__((address_space(1))) const uint8_t* g1_t;
   u32x4 rg[REG ? L : 1];
+  uint32_t rsc[(REG && BKIND == B_MXFP8) ? B_DMA : 1];
   auto gload = [&](int d, int kt) {
     if constexpr (REG) {
-      if (d < A_DMA) rg[d] = *(g16_t)(a_src[d] + (int64_t)kt * (BK * 2));
-      else rg[d] = *(g16_t)(b_src[d - A_DMA] + (int64_t)kt * (B8 ? BK : BK * 2));
+      if (d < A_DMA) {
+        rg[d] = *(g16_t)(a_src[d] + (int64_t)kt * (BK * 2));
+      } else {
+        rg[d] = *(g16_t)(b_src[d - A_DMA] + (int64_t)kt * (B8 ? BK : BK * 2));
+        if constexpr (BKIND == B_MXFP8) rsc[d - A_DMA] = *(g1_t)(b_scr[d - A_DMA] + kt * (BK / 32));
+      }
     }
   };
   auto lwrite = [&](int d, int buf) {
     if constexpr (REG) {
       char* As = lds + buf * STAGE;
-      char* dst = d < A_DMA ? As + (4 * d + wave) * 1024 : As + A_BYTES + (4 * (d - A_DMA) + wave) * 1024;
-      *reinterpret_cast<u32x4*>(dst + lane * 16) = rg[d];
+      if (!B_CONV || d < A_DMA) {
+        char* dst = d < A_DMA ? As + (4 * d + wave) * 1024 : As + A_BYTES + (4 * (d - A_DMA) + wave) * 1024;
+        *reinterpret_cast<u32x4*>(dst + lane * 16) = rg[d];
+      } else {
+        const int i = d - A_DMA;
+        const u32x4 w = rg[d];
+        uint32_t o[8];
+        if constexpr (BKIND == B_MXFP8) {
+          const float sc = e8m0_to_f32(rsc[i]);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            o[2 * q] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[q], sc, false));
+            o[2 * q + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[q], sc, true));
+          }
+        } else {
+          const float sc = b_s8[i], nb = -128.0f * sc;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t u = w[q] ^ 0x80808080u;
+            bf16x2 p0, p1;
+            p0[0] = (bf16)fmaf((float)(u & 0xffu), sc, nb);
+            p0[1] = (bf16)fmaf((float)((u >> 8) & 0xffu), sc, nb);
+            p1[0] = (bf16)fmaf((float)((u >> 16) & 0xffu), sc, nb);
+            p1[1] = (bf16)fmaf((float)(u >> 24), sc, nb);
+            o[2 * q] = __builtin_bit_cast(uint32_t, p0);
+            o[2 * q + 1] = __builtin_bit_cast(uint32_t, p1);
+          }
+        }
+        const int r = b_dst[i] / B_ROWB;
+        char* row = As + A_BYTES + b_dst[i];
+        const int x = chunk_xor<B_ROWB, SWZ>(r);
+        *reinterpret_cast<u32x4*>(row + ((2 * b_c16[i]) ^ x) * 16) = u32x4{o[0], o[1], o[2], o[3]};
+        *reinterpret_cast<u32x4*>(row + ((2 * b_c16[i] + 1) ^ x) * 16) = u32x4{o[4], o[5], o[6], o[7]};
+      }
     }
   };
   auto load_scales = [&](int kt) {
@@ -283,7 +347,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
   // Stage kt+1 landed while the (STAGES-2) younger stages stay in flight.
   auto wait_next_stage = [&]() {
     if constexpr (REG) return;  // the compiler tracks register loads itself
-    else if constexpr (BKIND == B_MXFP8) wait_vmcnt<0>();  // scale loads share the counter
+    else if constexpr (B_RAW && BKIND == B_MXFP8) wait_vmcnt<0>();  // scale loads share the counter
     else wait_vmcnt<(STAGES - 2) * L>();
   };
 
@@ -303,69 +367,76 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
   const int a_swz = chunk_xor<A_ROWB, SWZ>(frag_r);  // same for rows i*32+frag_r
   const int b_swz = chunk_xor<B_ROWB, SWZ>(frag_r);
 
-  // Fragment reads of k-step kk of the stage in buffer `buf` (8-bit weights
-  // dequantised here with the scales in sc_cur).
-  auto read_frags = [&](int buf, int kk, bf16x8* fa, bf16x8* fb) {
+  // Fragment reads of k-step kk of the stage in buffer `buf`.  8-bit weights
+  // are read as their raw codes and dequantised only as their MFMAs issue
+  // (conv), so no MFMA waits for a conversion that waits for LDS.
+  using BFrag = std::conditional_t<B_RAW, u32x2, bf16x8>;
+  auto read_frags = [&](int buf, int kk, bf16x8* fa, BFrag* fb) {
     const char* As = lds + buf * STAGE;
     const char* Bs = As + A_BYTES;
     const int ca = ((kk * 2 + frag_c) ^ a_swz) * 16;
 #pragma unroll
     for (int i = 0; i < TM; ++i) fa[i] = *reinterpret_cast<const bf16x8*>(As + a_off[i] + ca);
-    if (!B8) {
+    if constexpr (!B_RAW) {
+      const int cbf = ((kk * 2 + frag_c) ^ b_swz) * 16;
 #pragma unroll
-      for (int j = 0; j < TN; ++j) fb[j] = *reinterpret_cast<const bf16x8*>(Bs + b_off[j] + ca);
+      for (int j = 0; j < TN; ++j) fb[j] = *reinterpret_cast<const bf16x8*>(Bs + b_off[j] + cbf);
     } else {
       const int c8 = kk * 2 + frag_c;  // 8-byte chunk of the 64-byte row
       const int cb = ((c8 >> 1) ^ b_swz) * 16 + (c8 & 1) * 8;
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const u32x2 raw = *reinterpret_cast<const u32x2*>(Bs + b_off[j] + cb);
-        uint32_t o[4];
-        if (BKIND == B_INT8) {
-          const float s = s_i8[j], nb = -128.0f * s;
+      for (int j = 0; j < TN; ++j) fb[j] = *reinterpret_cast<const u32x2*>(Bs + b_off[j] + cb);
+    }
+  };
+  // B fragment j of k-step kk as bf16 (MXFP8 scales of the current stage in
+  // sc_cur; int8 per-row scales in s_i8).
+  auto conv = [&](const BFrag* fb, int j, int kk) -> bf16x8 {
+    if constexpr (!B_RAW) {
+      return fb[j];
+    } else {
+      const u32x2 raw = fb[j];
+      uint32_t o[4];
+      if constexpr (BKIND == B_INT8) {
+        const float sc = s_i8[j], nb = -128.0f * sc;
 #pragma unroll
-          for (int d = 0; d < 2; ++d) {
-            const uint32_t u = raw[d] ^ 0x80808080u;
-            bf16x2 p0, p1;
-            p0[0] = (bf16)fmaf((float)(u & 0xffu), s, nb);
-            p0[1] = (bf16)fmaf((float)((u >> 8) & 0xffu), s, nb);
-            p1[0] = (bf16)fmaf((float)((u >> 16) & 0xffu), s, nb);
-            p1[1] = (bf16)fmaf((float)(u >> 24), s, nb);
-            o[2 * d] = __builtin_bit_cast(uint32_t, p0);
-            o[2 * d + 1] = __builtin_bit_cast(uint32_t, p1);
-          }
-        } else {
-          const float sc = e8m0_to_f32((sc_cur[j] >> (8 * (kk >> 1))) & 0xffu);
-#pragma unroll
-          for (int d = 0; d < 2; ++d) {
-            o[2 * d] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[d], sc, false));
-            o[2 * d + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[d], sc, true));
-          }
+        for (int d = 0; d < 2; ++d) {
+          const uint32_t u = raw[d] ^ 0x80808080u;
+          bf16x2 p0, p1;
+          p0[0] = (bf16)fmaf((float)(u & 0xffu), sc, nb);
+          p0[1] = (bf16)fmaf((float)((u >> 8) & 0xffu), sc, nb);
+          p1[0] = (bf16)fmaf((float)((u >> 16) & 0xffu), sc, nb);
+          p1[1] = (bf16)fmaf((float)(u >> 24), sc, nb);
+          o[2 * d] = __builtin_bit_cast(uint32_t, p0);
+          o[2 * d + 1] = __builtin_bit_cast(uint32_t, p1);
         }
-        fb[j] = __builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]});
+      } else {
+        const float sc = e8m0_to_f32((sc_cur[j] >> (8 * (kk >> 1))) & 0xffu);
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+          o[2 * d] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[d], sc, false));
+          o[2 * d + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[d], sc, true));
+        }
+      }
+      return __builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]});
+    }
+  };
+  // MFMAs of k-step kk, weight-fragment-major, with memory instructions spread
+  // between them: op(m) issues what belongs after MFMA m.  Issuing loads or
+  // LDS writes this way never idles the matrix pipe, and the dequantisation
+  // of weight fragment j+1 runs under the MFMAs of fragment j.
+  auto mfmas_with = [&](const bf16x8* fa, const BFrag* fb, int kk, auto&& op) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const bf16x8 b = conv(fb, j, kk);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, fa[i], acc[i][j], 0, 0, 0);
+        op(j * TM + i);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   };
-  auto mfmas = [&](const bf16x8* fa, const bf16x8* fb) {
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
-  };
-  // MFMAs of one k-step with memory instructions spread between them:
-  // op(m) issues what belongs after MFMA m.  Issuing loads or LDS writes this
-  // way never idles the matrix pipe.
-  auto mfmas_with = [&](const bf16x8* fa, const bf16x8* fb, auto&& op) {
-    constexpr int NM = TM * TN;
-#pragma unroll
-    for (int m = 0; m < NM; ++m) {
-      const int i = m / TN, j = m % TN;
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
-      op(m);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
+  auto mfmas = [&](const bf16x8* fa, const BFrag* fb, int kk) { mfmas_with(fa, fb, kk, [](int) {}); };
   // the L loads of stage kt_src, spread over the NM MFMAs of one k-step
   auto loads_at = [&](int kt_src, int buf) {
     return [&, kt_src, buf](int m) {
@@ -382,7 +453,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
   // next k-step are read while the MFMAs of the current one run, including
   // across the stage boundary, whose barrier sits between the fragment reads
   // of the last k-step and its MFMAs.
-  bf16x8 fa[2][TM], fb[2][TN];
+  bf16x8 fa[2][TM];
+  BFrag fb[2][TN];
   if constexpr (REG) {
 #pragma unroll
     for (int d = 0; d < L; ++d) gload(d, 0);
@@ -396,7 +468,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
 #pragma unroll
       for (int d = 0; d < L; ++d) dma_op(d, st < KT ? st : KT - 1, st);
   }
-  if (BKIND == B_MXFP8) {
+  if (B_RAW && BKIND == B_MXFP8) {
     load_scales(0);
     wait_vmcnt<0>();
 #pragma unroll
@@ -424,7 +496,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (REG) {
         constexpr int NM = TM * TN, SLOTS = (KSTEPS - 1) * NM;
-        mfmas_with(fa[kk & 1], fb[kk & 1], [&](int m) {
+        mfmas_with(fa[kk & 1], fb[kk & 1], kk, [&](int m) {
 #pragma unroll
           for (int d = 0; d < L; ++d)
             if ((d * SLOTS) / L == kk * NM + m && write) {
@@ -433,7 +505,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
             }
         });
       } else {
-        mfmas(fa[kk & 1], fb[kk & 1]);
+        mfmas(fa[kk & 1], fb[kk & 1], kk);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -445,25 +517,25 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
     leading_ksteps(buf, nbuf, true, kt + 2 < KT ? kt + 2 : KT - 1);
     wait_next_stage();
     __syncthreads();  // stage kt+1 visible to all waves; stage kt's buffer free
-    if (BKIND == B_MXFP8) {
-#pragma unroll
-      for (int j = 0; j < TN; ++j) sc_cur[j] = sc_next[j];
-    }
     read_frags(nbuf, 0, fa[0], fb[0]);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (REG) {
-      mfmas(fa[LASTF], fb[LASTF]);
+      mfmas(fa[LASTF], fb[LASTF], KSTEPS - 1);
     } else {  // DMA of stage kt+STAGES into the freed buffer
       const int kt_src = kt + STAGES < KT ? kt + STAGES : KT - 1;
-      mfmas_with(fa[LASTF], fb[LASTF], loads_at(kt_src, buf));
+      mfmas_with(fa[LASTF], fb[LASTF], KSTEPS - 1, loads_at(kt_src, buf));
     }
-    if (BKIND == B_MXFP8) load_scales(kt + 2 < KT ? kt + 2 : KT - 1);
+    if (B_RAW && BKIND == B_MXFP8) {  // the next stage's scales (the last k-step used this one's)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) sc_cur[j] = sc_next[j];
+      load_scales(kt + 2 < KT ? kt + 2 : KT - 1);
+    }
     buf = nbuf;
   }
   leading_ksteps(buf, buf, false, 0);
   wait_lgkmcnt0();
   __builtin_amdgcn_sched_barrier(0);
-  mfmas(fa[LASTF], fb[LASTF]);
+  mfmas(fa[LASTF], fb[LASTF], KSTEPS - 1);
   __builtin_amdgcn_sched_barrier(0);
   wait_vmcnt<0>();  // the re-read stages land before the epilogue reuses LDS
   if (tid < BN) {
