@@ -62,6 +62,9 @@ class LTXModel:
         self.timestep_scale_multiplier = timestep_scale_multiplier
         self.av_ca_timestep_scale_multiplier = av_ca_timestep_scale_multiplier
         self.weight_format = weight_format
+        # audio stream work on its own HIP stream, overlapping the video stream
+        self.concurrent_audio = True
+        self._audio_stream: torch.cuda.Stream | None = None
         self.video_dim = num_attention_heads * attention_head_dim
         self.audio_dim = AUDIO_HEADS * AUDIO_HEAD_DIM
         self.video_config = TransformerConfig(self.video_dim, num_attention_heads, attention_head_dim,
@@ -187,11 +190,22 @@ class LTXModel:
                       self._ada_a.data_ptr(), self.num_layers, ADA_ROWS * self.audio_dim, stream)
             audio = TransformerArgs(x=ax, context=audio_context, timesteps=self._temb_a[:9],
                                     positional_embeddings=ape, cross_positional_embeddings=axpe)
-        # blocks
+        # blocks; the audio stream's work overlaps the video stream's on a
+        # second HIP stream (forked once here, joined before the heads)
+        side = None
+        if run_audio and self.concurrent_audio:
+            if self._audio_stream is None:
+                self._audio_stream = torch.cuda.Stream(device=vx.device)  # default priority
+            side = self._audio_stream
         for i, block in enumerate(self.transformer_blocks):
             block.ada_rows_video = self._ada_v[i]
             block.ada_rows_audio = self._ada_a[i] if run_audio else None
+            block.audio_stream = side
+            block.audio_fork = i == 0
             video, audio = block(video, audio, profile_events=profile_events)
+        if side is not None:
+            torch.cuda.current_stream().wait_stream(side)
+            audio.x.record_stream(torch.cuda.current_stream())
         # output heads
         v_out = self._output(video.x, self.scale_shift_table, self._emb_v, self.proj_out)
         a_out = None

@@ -28,10 +28,18 @@ The AdaLN modulation rows of a block are ``table + timestep embedding``
 The 48-block scheduler computes all blocks' rows in one launch per step and
 hands each block its slice (``ada_rows``); a block used on its own computes
 its rows from its tables and the args' timestep fields.
+
+With ``audio_stream`` set (the 48-block model sets it) and both streams
+running, the audio stream's work (steps 3, the audio half of 4, and its FF) is
+issued on that second HIP stream: the 68-token audio GEMMs and attentions use
+a few CUs each and overlap with the video work.  The streams meet once per
+block, at A2V / V2A: each direction waits for the other stream's modulated
+inputs only (events), so the data flow and every rounding are unchanged.
 """
 
 from __future__ import annotations
 
+import contextlib
 import os
 import time
 from collections.abc import Callable
@@ -149,6 +157,8 @@ class BasicAVTransformerBlock:
         # per-step modulation rows injected by the scheduler (see module doc)
         self.ada_rows_video: torch.Tensor | None = None
         self.ada_rows_audio: torch.Tensor | None = None
+        self.audio_stream: torch.cuda.Stream | None = None
+        self.audio_fork = True  # the audio stream waits for the caller's stream first
         self._adaln_flags = 0 if _FUSED_ADALN_ENABLED else _lib.ADALN_ROUND_NORM
 
     # -- parameters ---------------------------------------------------------
@@ -235,6 +245,21 @@ class BasicAVTransformerBlock:
         ada_v = self._ada(video, self.video_tables, self.ada_rows_video) if run_vx or need_av else None
         ada_a = self._ada(audio, self.audio_tables, self.ada_rows_audio) if run_ax or need_av else None
 
+        # Audio work on the second stream when both streams run.  Tensors that
+        # cross streams are recorded on the consuming stream so the caching
+        # allocator keeps them until that stream is done with them.
+        side = self.audio_stream if (self.audio_stream is not None and run_vx and run_ax) else None
+        main = torch.cuda.current_stream() if side is not None else None
+
+        def on_audio():
+            return torch.cuda.stream(side) if side is not None else contextlib.nullcontext()
+
+        if side is not None:
+            if self.audio_fork:  # audio input and modulation rows come from the caller's stream
+                side.wait_stream(main)
+            a2.record_stream(side)
+            ada_a.record_stream(side)
+
         if run_vx:
             pe = _tables(video.positional_embeddings)
             if not skip("skip_video_self_attn"):
@@ -252,20 +277,23 @@ class BasicAVTransformerBlock:
             mark("video text-attn")
 
         if run_ax:
-            pe = _tables(audio.positional_embeddings)
-            if not skip("skip_audio_self_attn"):
-                h = adaln(a2, ada_a[ROW_SCALE_MSA], ada_a[ROW_SHIFT_MSA], eps, flags)
-                o = self.audio_attn1.core(h, pe=pe)
-                a2 = residual_gemm(o, self.audio_attn1.to_out, a2, a_owned, ada_a[ROW_GATE_MSA], gemm.EPI_RESIDUAL)
+            with on_audio():
+                pe = _tables(audio.positional_embeddings)
+                if not skip("skip_audio_self_attn"):
+                    h = adaln(a2, ada_a[ROW_SCALE_MSA], ada_a[ROW_SHIFT_MSA], eps, flags)
+                    o = self.audio_attn1.core(h, pe=pe)
+                    a2 = residual_gemm(o, self.audio_attn1.to_out, a2, a_owned, ada_a[ROW_GATE_MSA],
+                                       gemm.EPI_RESIDUAL)
+                    a_owned = True
+                    mark("audio self-attn")
+                ctx = audio.context[0] if audio.context.dim() == 3 else audio.context
+                a = adaln(a2, ada_a[ROW_SCALE_Q], ada_a[ROW_SHIFT_Q], eps, rn)
+                c = adaln(ctx, ada_a[ROW_SCALE_KV], ada_a[ROW_SHIFT_KV], eps, _lib.ADALN_NO_NORM)
+                o = self.audio_attn2.core(a, c)
+                a2 = residual_gemm(o, self.audio_attn2.to_out, a2, a_owned, ada_a[ROW_GATE_Q],
+                                   gemm.EPI_RESIDUAL_ROUND)
                 a_owned = True
-                mark("audio self-attn")
-            ctx = audio.context[0] if audio.context.dim() == 3 else audio.context
-            a = adaln(a2, ada_a[ROW_SCALE_Q], ada_a[ROW_SHIFT_Q], eps, rn)
-            c = adaln(ctx, ada_a[ROW_SCALE_KV], ada_a[ROW_SHIFT_KV], eps, _lib.ADALN_NO_NORM)
-            o = self.audio_attn2.core(a, c)
-            a2 = residual_gemm(o, self.audio_attn2.to_out, a2, a_owned, ada_a[ROW_GATE_Q], gemm.EPI_RESIDUAL_ROUND)
-            a_owned = True
-            mark("audio text-attn")
+                mark("audio text-attn")
 
         if run_a2v or run_v2a:
             vpe = _tables(video.cross_positional_embeddings)
@@ -273,8 +301,14 @@ class BasicAVTransformerBlock:
             # modulated inputs of both directions from the pre-A2V streams
             vs_a2v = adaln(v2, ada_v[ROW_SCALE_A2V], ada_v[ROW_SHIFT_A2V], eps, rn)
             vs_v2a = adaln(v2, ada_v[ROW_SCALE_V2A], ada_v[ROW_SHIFT_V2A], eps, rn)
-            as_a2v = adaln(a2, ada_a[ROW_SCALE_A2V], ada_a[ROW_SHIFT_A2V], eps, rn)
-            as_v2a = adaln(a2, ada_a[ROW_SCALE_V2A], ada_a[ROW_SHIFT_V2A], eps, rn)
+            ev_v = main.record_event() if side is not None else None
+            with on_audio():
+                as_a2v = adaln(a2, ada_a[ROW_SCALE_A2V], ada_a[ROW_SHIFT_A2V], eps, rn)
+                as_v2a = adaln(a2, ada_a[ROW_SCALE_V2A], ada_a[ROW_SHIFT_V2A], eps, rn)
+            if side is not None:
+                main.wait_event(side.record_event())
+                as_a2v.record_stream(main)
+                vs_v2a.record_stream(side)
             if run_a2v and not skip("skip_a2v_cross_attn"):
                 o = self.audio_to_video_attn.core(vs_a2v, as_a2v, pe=vpe, k_pe=ape)
                 v2 = residual_gemm(o, self.audio_to_video_attn.to_out, v2, v_owned, ada_v[ROW_GATE_AV],
@@ -282,11 +316,14 @@ class BasicAVTransformerBlock:
                 v_owned = True
                 mark("audio->video attn")
             if run_v2a and not skip("skip_v2a_cross_attn"):
-                o = self.video_to_audio_attn.core(as_v2a, vs_v2a, pe=ape, k_pe=vpe)
-                a2 = residual_gemm(o, self.video_to_audio_attn.to_out, a2, a_owned, ada_a[ROW_GATE_AV],
-                                   gemm.EPI_RESIDUAL)
-                a_owned = True
-                mark("video->audio attn")
+                with on_audio():
+                    if side is not None:
+                        side.wait_event(ev_v)
+                    o = self.video_to_audio_attn.core(as_v2a, vs_v2a, pe=ape, k_pe=vpe)
+                    a2 = residual_gemm(o, self.video_to_audio_attn.to_out, a2, a_owned, ada_a[ROW_GATE_AV],
+                                       gemm.EPI_RESIDUAL)
+                    a_owned = True
+                    mark("video->audio attn")
 
         if run_vx:
             h = adaln(v2, ada_v[ROW_SCALE_MLP], ada_v[ROW_SHIFT_MLP], eps, flags)
@@ -294,10 +331,12 @@ class BasicAVTransformerBlock:
             v2 = residual_gemm(f, self.ff.project_out, v2, v_owned, ada_v[ROW_GATE_MLP], gemm.EPI_RESIDUAL)
             mark("video ff")
         if run_ax:
-            h = adaln(a2, ada_a[ROW_SCALE_MLP], ada_a[ROW_SHIFT_MLP], eps, flags)
-            f = self.audio_ff.hidden(h)
-            a2 = residual_gemm(f, self.audio_ff.project_out, a2, a_owned, ada_a[ROW_GATE_MLP], gemm.EPI_RESIDUAL)
-            mark("audio ff")
+            with on_audio():
+                h = adaln(a2, ada_a[ROW_SCALE_MLP], ada_a[ROW_SHIFT_MLP], eps, flags)
+                f = self.audio_ff.hidden(h)
+                a2 = residual_gemm(f, self.audio_ff.project_out, a2, a_owned, ada_a[ROW_GATE_MLP],
+                                   gemm.EPI_RESIDUAL)
+                mark("audio ff")
 
         def pack(args, x2, x_in, owned):
             if args is None or not owned:
