@@ -1,7 +1,9 @@
 """Benchmark: ms per distilled audio+video DiT denoise step on one MI355X.
 
 Workload (default): the LTX-2.3 22B-shape transformer, 48 blocks resident in
-HBM with random-init bf16 weights ~N(0, 0.02), one denoise step at
+HBM with random-init weights ~N(0, 0.02) stored as MXFP8 (E4M3 codes + E8M0
+scale per 32 along K; --weights bf16|int8 for the other formats), one
+denoise step at
 768x512x65 -> 3456 video tokens (latent 9x16x24), 68 audio tokens and 256
 text tokens per modality, eight distilled sigmas cycled.  A "step" is one
 full transformer forward (preprocess, 48 blocks, output heads) plus the fused
@@ -11,7 +13,11 @@ Prints ONE JSON line.  Besides ms/step and tokens/s it carries:
   roofline      the dominant kernel (video FF up-projection GEMM, M=3456,
                 K=4096, N=16384, GELU epilogue): algorithmic flops per launch /
                 its average launch time from stream events around every such
-                launch in a timed region of eager steps;
+                launch in eager steps run right after the timed region (the
+                timed region replays HIP graphs, which take no events);
+                ``traffic`` = HBM bytes per launch from the rocprofv3
+                FETCH_SIZE / WRITE_SIZE summary committed in profiles/ for
+                this kernel and weight format (null when none matches);
   fused_ops     HBM GB/s of adaln_norm_fused / gated_add_fused at the
                 reference's test shape (T=14640, C=4096) over a >512 MB buffer
                 rotation (no Infinity-Cache reuse);
@@ -48,12 +54,38 @@ def parse_args(argv=None):
     ap.add_argument("--frames", type=int, default=65)
     ap.add_argument("--audio-tokens", type=int, default=None)
     ap.add_argument("--text-tokens", type=int, default=256)
-    ap.add_argument("--weights", choices=["bf16", "int8", "mxfp8"], default="bf16")
+    ap.add_argument("--weights", choices=["bf16", "int8", "mxfp8"], default="mxfp8")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of HIP graph replay")
     ap.add_argument("--kernel-steps", type=int, default=2, help="eager steps for the dominant-kernel timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-fused-bench", action="store_true")
+    ap.add_argument("--counter-workload", choices=["ff-up", "copy"], default=None,
+                    help="run only a short workload for rocprofv3 --pmc passes and exit: the video FF "
+                         "up-projection GEMM (4 launches, --weights format) or a 1 GiB device copy (3 "
+                         "launches, the FETCH_SIZE / WRITE_SIZE calibration)")
     return ap.parse_args(argv)
+
+
+def counter_workload(kind: str, weights: str) -> None:
+    import torch
+
+    from ltx_amd.kernels import gemm
+
+    if kind == "copy":
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+    else:
+        g = torch.Generator(device="cuda").manual_seed(0)
+        x = torch.randn((3456, 4096), generator=g, device="cuda").bfloat16()
+        w = (torch.randn((16384, 4096), generator=g, device="cuda") * 0.02).bfloat16()
+        wt = gemm.make_weight(w, torch.zeros(16384, device="cuda"), kind=weights)
+        out = torch.empty((3456, 16384), dtype=torch.bfloat16, device="cuda")
+        for _ in range(4):
+            gemm.linear(x, wt, epilogue=gemm.EPI_GELU, out=out)
+    torch.cuda.synchronize()
+    print(f"counter workload {kind} ({weights}) done", flush=True)
 
 
 def step_flops(tv: int, ta: int, s: int, layers: int) -> float:
@@ -73,6 +105,20 @@ def step_flops(tv: int, ta: int, s: int, layers: int) -> float:
     if ta:
         a += 4 * ta * ta * ad + 4 * ta * s * ad + 4 * tv * ta * ad * 2
     return layers * (g + a) + 2 * tv * 128 * vd * 2 + 2 * ta * 128 * ad * 2
+
+
+def measured_traffic(kernel: str, weights: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter
+    summary (profiles/gemm_ff_up_hbm_traffic.json), or None."""
+    path = ROOT / "profiles" / "gemm_ff_up_hbm_traffic.json"
+    try:
+        rec = json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+    for r in rec.get("launches", []):
+        if r.get("kernel") == kernel and r.get("weights") == weights:
+            return r.get("hbm_bytes")
+    return None
 
 
 def fused_op_bandwidth(torch):
@@ -161,6 +207,9 @@ def main(argv=None):
         print(json.dumps({"error": "this build measures one GPU; the denoise step does not shard across GPUs "
                                    "here (see DESIGN.md for the sharding design)", "n_gpus": args.gpus}))
         return 2
+    if args.counter_workload:
+        counter_workload(args.counter_workload, args.weights)
+        return 0
     import torch
 
     from ltx_amd.components.patchifiers import audio_latent_frames, video_latent_grid
@@ -232,9 +281,10 @@ def main(argv=None):
     k_ms = sum(durs) / len(durs)
     k_flop = 2.0 * tv * 4096 * 16384
     achieved = k_flop / (k_ms * 1e-3) / 1e12
-    roofline = {"bound": "mfma", "kernel": "gemm_kernel<256,256,bf16,GELU> (video FF up, M=%d K=4096 N=16384)" % tv,
+    kname = f"gemm_kernel<256,256,{args.weights},GELU>"
+    roofline = {"bound": "mfma", "kernel": f"{kname} (video FF up, M={tv} K=4096 N=16384; bf16 MFMA)",
                 "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic(kname, args.weights),
                 "launch_us": round(k_ms * 1e3, 1), "launches_timed": len(durs),
                 "algorithmic_flop_per_launch": k_flop}
     flops = step_flops(tv, ta, s, args.layers)
