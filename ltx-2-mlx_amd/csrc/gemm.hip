@@ -388,6 +388,22 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
       for (int j = 0; j < TN; ++j) fb[j] = *reinterpret_cast<const u32x2*>(Bs + b_off[j] + cb);
     }
   };
+  // fragment f of k-step kk: A fragments 0..TM-1, then B fragments
+  auto read_frag = [&](int buf, int kk, int f, bf16x8* fa, BFrag* fb) {
+    const char* As = lds + buf * STAGE;
+    const char* Bs = As + A_BYTES;
+    if (f < TM) {
+      const int ca = ((kk * 2 + frag_c) ^ a_swz) * 16;
+      fa[f] = *reinterpret_cast<const bf16x8*>(As + a_off[f] + ca);
+    } else if constexpr (!B_RAW) {
+      const int cbf = ((kk * 2 + frag_c) ^ b_swz) * 16;
+      fb[f - TM] = *reinterpret_cast<const bf16x8*>(Bs + b_off[f - TM] + cbf);
+    } else {
+      const int c8 = kk * 2 + frag_c;
+      const int cb = ((c8 >> 1) ^ b_swz) * 16 + (c8 & 1) * 8;
+      fb[f - TM] = *reinterpret_cast<const u32x2*>(Bs + b_off[f - TM] + cb);
+    }
+  };
   // B fragment j of k-step kk as bf16 (MXFP8 scales of the current stage in
   // sc_cur; int8 per-row scales in s_i8).
   auto conv = [&](const BFrag* fb, int j, int kk) -> bf16x8 {
@@ -485,18 +501,19 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
   // kk.  The fragments of kk were issued one MFMA block earlier; waiting for
   // them before issuing the next reads keeps at most one group (TM+TN <= 8
   // reads) in flight, which the 4-bit LDS counter can track exactly.
-  // With the register loader, the LDS writes of the next stage (into wbuf),
-  // each followed by the global load of the stage after it into the same
-  // registers (kt_load), are spread evenly over these k-steps' MFMAs.
+  // With the register loader, the fragment reads of k-step kk+1 go one after
+  // each of the first TM+TN MFMAs of kk, and the LDS writes of the next stage
+  // (into wbuf), each followed by the global load of the stage after it into
+  // the same registers (kt_load), are spread evenly over these k-steps' MFMAs:
+  // no burst of LDS traffic queues up behind the other waves'.
   auto leading_ksteps = [&](int buf, int wbuf, bool write, int kt_load) {
 #pragma unroll
     for (int kk = 0; kk < KSTEPS - 1; ++kk) {
       wait_lgkmcnt0();
-      read_frags(buf, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
-      __builtin_amdgcn_sched_barrier(0);
       if constexpr (REG) {
         constexpr int NM = TM * TN, SLOTS = (KSTEPS - 1) * NM;
         mfmas_with(fa[kk & 1], fb[kk & 1], kk, [&](int m) {
+          if (m < TM + TN) read_frag(buf, kk + 1, m, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
 #pragma unroll
           for (int d = 0; d < L; ++d)
             if ((d * SLOTS) / L == kk * NM + m && write) {
@@ -505,6 +522,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
             }
         });
       } else {
+        read_frags(buf, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
         mfmas(fa[kk & 1], fb[kk & 1], kk);
       }
       __builtin_amdgcn_sched_barrier(0);
