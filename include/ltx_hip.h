@@ -178,7 +178,8 @@ int ltx_broadcast_add_f32(const float* table, const float* vec, float* out, int6
  *   MXFP8: w = bf16(e4m3(q) * 2^(e - 127))
  * bias: fp32 (N) or NULL.  C: bf16 (M, N) row stride ldc.
  * Requirements: K % 64 == 0, N % 8 == 0, 16-byte aligned pointers and row
- * strides.  `epilogue` is one of LTX_GEMM_EPI_* optionally OR-ed with a tile
+ * strides; MXFP8 scales 4-byte aligned with ld_scale % 4 == 0.  `epilogue` is
+ * one of LTX_GEMM_EPI_* optionally OR-ed with a tile
  * override (LTX_GEMM_TILE_256 / LTX_GEMM_TILE_128; default: by problem size).
  * With LTX_GEMM_EPI_BIAS, output columns n >= sigmoid_from get the head-gate
  * epilogue of LTX_GEMM_EPI_SIGMOID2 instead (pass N for none): the per-head

@@ -251,7 +251,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
       b_c16[i] = lane & 3;
       b_dst[i] = r * B_ROWB;
       b_src[i] = (const char*)p.B + (int64_t)gn * p.ldb + b_c16[i] * 16;
-      if (BKIND == B_MXFP8) b_scr[i] = (const uint8_t*)p.bscale + (int64_t)gn * p.ld_scale + (b_c16[i] >> 1);
+      if (BKIND == B_MXFP8) b_scr[i] = (const uint8_t*)p.bscale + (int64_t)gn * p.ld_scale;
       if (BKIND == B_INT8) b_s8[i] = ((const float*)p.bscale)[gn];
     }
   }
@@ -288,16 +288,22 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
   // 8-bit weight loads carry 16 codes (and, for MXFP8, the E8M0 scale of
   // their 32-block), written to LDS as 16 dequantised bf16 in two chunks.
   typedef __attribute__((address_space(1))) const u32x4* g16_t;
-  typedef __attribute__((address_space(1))) const uint8_t* g1_t;
+  typedef __attribute__((address_space(1))) const uint32_t* g4_t;
   u32x4 rg[REG ? L : 1];
-  uint32_t rsc[(REG && BKIND == B_MXFP8) ? B_DMA : 1];
+  // MXFP8: the aligned 4-byte scale word holding this load's E8M0 byte, and
+  // the byte's bit offset in it (ld_scale % 4 == 0)
+  uint32_t rsc[(REG && BKIND == B_MXFP8) ? B_DMA : 1], rsh[(REG && BKIND == B_MXFP8) ? B_DMA : 1];
   auto gload = [&](int d, int kt) {
     if constexpr (REG) {
       if (d < A_DMA) {
         rg[d] = *(g16_t)(a_src[d] + (int64_t)kt * (BK * 2));
       } else {
         rg[d] = *(g16_t)(b_src[d - A_DMA] + (int64_t)kt * (B8 ? BK : BK * 2));
-        if constexpr (BKIND == B_MXFP8) rsc[d - A_DMA] = *(g1_t)(b_scr[d - A_DMA] + kt * (BK / 32));
+        if constexpr (BKIND == B_MXFP8) {
+          const int byte = kt * (BK / 32) + (b_c16[d - A_DMA] >> 1);
+          rsc[d - A_DMA] = *(g4_t)(b_scr[d - A_DMA] + (byte & ~3));
+          rsh[d - A_DMA] = 8 * (byte & 3);
+        }
       }
     }
   };
@@ -312,7 +318,12 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
         const u32x4 w = rg[d];
         uint32_t o[8];
         if constexpr (BKIND == B_MXFP8) {
-          const float sc = e8m0_to_f32(rsc[i]);
+          // The loaded word goes straight into the empty asm, which pins the
+          // byte extraction and decode here: hoisted to the top of the loop
+          // they made every iteration wait for the previous stage's loads.
+          uint32_t e = rsc[i];
+          asm volatile("" : "+v"(e));
+          const float sc = e8m0_to_f32((e >> rsh[i]) & 0xffu);
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             o[2 * q] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[q], sc, false));
@@ -782,6 +793,7 @@ extern "C" int ltx_gemm_mxfp8_bf16(const void* A, int64_t lda, const uint8_t* Wq
   int st = gemm_check(A, lda, Wq, ldw, C, ldc, M, N, K, epilogue, residual, ldr, gate, 1);
   if (st != LTX_OK) return st;
   if (!w_scale || ld_scale < K / 32) return LTX_ERR_INVALID_ARG;
+  if (ld_scale % 4 || ((uintptr_t)w_scale & 3u)) return LTX_ERR_ALIGNMENT;  // scale words
   if (M == 0 || N == 0) return LTX_OK;
   if (K == 0) return LTX_ERR_UNSUPPORTED;
   GemmArgs p = make_args(A, lda, Wq, ldw, w_scale, ld_scale, bias, C, ldc, M, N, K, residual, ldr,
