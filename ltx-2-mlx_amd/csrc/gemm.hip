@@ -458,6 +458,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, fa[i], acc[i][j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);  // the MFMA issues first; op runs under it
         op(j * TM + i);
         __builtin_amdgcn_sched_barrier(0);
       }
