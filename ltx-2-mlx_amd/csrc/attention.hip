@@ -17,17 +17,25 @@
 //   are contiguous (see vt_position).
 //
 // Kernel structure: one workgroup = 8 waves = 256 queries of one head; each
-// wave owns 32 queries, two waves share a SIMD, so one wave's softmax (VALU,
-// transcendental) overlaps the other's matrix work.  Scores are computed
+// wave owns 32 queries and two waves share a SIMD.  Scores are computed
 // transposed, S^T = K Q^T, with v_mfma_f32_32x32x16_bf16: each lane then
 // holds one query's scores in registers, so the row max / row sum are
-// lane-local plus one cross-half shuffle, and P^T feeds the P.V MFMA straight
-// from registers (O^T += Vt . P^T).  K and Vt stream through LDS in 64-key
-// stages by direct global->LDS DMA, double buffered.  The running max is
-// raised only when a block's max exceeds it by more than 2^8 (P then stays
-// <= 256, exact in fp32 and bf16-relative as any other P), so the O^T
-// rescale runs in the first blocks and then almost never.  Workgroups of one
-// head are numbered contiguously per XCD so its K/V stay in that XCD's L2.
+// lane-local plus one cross-half exchange (v_permlane32_swap), and P^T feeds
+// the P.V MFMA straight from registers (O^T += Vt . P^T).  K and Vt stream
+// through LDS in 64-key stages by direct global->LDS DMA, double buffered.
+// Key blocks are software-pipelined inside each wave, because VALU work only
+// overlaps the issuing wave's own MFMAs: the softmax of block b is cut into
+// one piece per MFMA slot (row max, running-max update, then exp2 / row sum
+// / bf16 pack) spread over the P.V MFMAs of block b-1 and the S^T MFMAs of
+// block b+1.  The stage barrier sits after a wave's last Vt read of a P.V
+// half, so the K fragments of the next block are read behind the remaining
+// MFMAs.  The running max is raised only when a block's max exceeds it by
+// more than 2^8 (P then stays <= 256, exact in fp32 and bf16-relative as any
+// other P), so the O^T rescale runs in the first blocks and then almost
+// never.  Workgroups of one head are numbered contiguously per XCD so its
+// K/V stay in that XCD's L2.
+#include <type_traits>
+
 #include "ltx_common.h"
 
 namespace ltx {
@@ -79,8 +87,29 @@ struct SplitOut {
   int splits;
 };
 
+// Softmax schedule of one key block over the MFMA slots of the pipeline:
+// slots 0..NP-1 are the P.V half that follows the block's S^T (row max in
+// slots < F, running-max update in slot F, exps after it), slots NP.. are the
+// next S^T half (remaining exps).  Element e = 16*sb + r of the block's S^T.
+template <int NP, int NQ, int DTILES>
+struct AttnSched {
+  static constexpr int F = NP / 2 - 1;
+  static constexpr int NE = NP + NQ - F - 1;  // slots that carry exps
+  static constexpr int exp_slot(int e) { return F + 1 + e * NE / 32; }
+  static constexpr int max_slot(int e) { return e * F / 32; }
+  // element e is written into P^T fragment e/8, which the previous block's
+  // P.V reads in half-2 slots [(e/8)*DTILES, (e/8+1)*DTILES)
+  static constexpr bool valid() {
+    for (int e = 0; e < 32; ++e)
+      if (exp_slot(e) < NP && exp_slot(e) < (e / 8 + 1) * DTILES) return false;
+    for (int e = 0; e < 32; e += 2)
+      if (exp_slot(e) > exp_slot(e + 1)) return false;
+    return F >= 1 && exp_slot(31) < NP + NQ;
+  }
+};
+
 template <int DH, bool GATED, int WAVES, bool SPLIT>
-__global__ __launch_bounds__(64 * WAVES, 1) void flash_attn_kernel(
+__global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
     const bf16* __restrict__ Q, int64_t q_rs, const bf16* __restrict__ K, int64_t k_rs,
     const bf16* __restrict__ Vt, int64_t tk_pad, bf16* __restrict__ O, int64_t o_rs,
     const bf16* __restrict__ G, int64_t g_rs, int Tq, int Tk, int H, float scale_log2, SplitOut so) {
@@ -88,8 +117,16 @@ __global__ __launch_bounds__(64 * WAVES, 1) void flash_attn_kernel(
   constexpr int kAttnQ = Cfg::QT;
   constexpr int DSTEPS = Cfg::DSTEPS, DTILES = Cfg::DTILES;
   constexpr int K_ROWB = Cfg::K_ROWB, K_BYTES = Cfg::K_BYTES, V_ROWB = Cfg::V_ROWB;
-  constexpr int STAGE = Cfg::STAGE, K_DMA = Cfg::K_DMA, V_DMA = Cfg::V_DMA;
-  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
+  constexpr int V_BYTES = Cfg::V_BYTES, K_DMA = Cfg::K_DMA, V_DMA = Cfg::V_DMA;
+  constexpr int NQ = 2 * DSTEPS;  // MFMAs of S^T = K Q^T per key block (one per slot)
+  constexpr int NP = 4 * DTILES;  // MFMAs of O^T += Vt P^T per key block
+  constexpr int EPS = 32 / NQ;    // softmax elements per S^T slot
+  constexpr int PF = 4;           // fragment reads in flight ahead of their MFMA
+  static_assert(NQ >= PF && NP >= PF && 32 % NQ == 0, "slot schedule");
+  // K ring (2 x K_BYTES) followed by the Vt ring (2 x V_BYTES)
+  __shared__ __attribute__((aligned(1024))) char lds[2 * (K_BYTES + V_BYTES)];
+  char* const Ks0 = lds;
+  char* const Vs0 = lds + 2 * K_BYTES;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hh = lane >> 5, l32 = lane & 31;
@@ -120,7 +157,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void flash_attn_kernel(
   }
 
   // ---- DMA sources.  Wave instruction i fills the 1 KiB LDS block
-  // kAttnWaves*i + wave.  K: 1024/K_ROWB rows per block.
+  // WAVES*i + wave.  K: 1024/K_ROWB rows per block.
   constexpr int K_ROWS_PER = 1024 / K_ROWB;      // 4 (dh 128) or 8 (dh 64)
   constexpr int K_CH = K_ROWB / 16;               // 16-byte chunks per row
   const char* k_src[K_DMA];
@@ -143,121 +180,249 @@ __global__ __launch_bounds__(64 * WAVES, 1) void flash_attn_kernel(
   }
 
   const int nblocks_all = (Tk + kAttnKB - 1) / kAttnKB;
-  // key blocks [kb0, kb1) of this workgroup
+  // key blocks [kb0, kb0 + nb) of this workgroup
   const int per_split = (nblocks_all + nsplit - 1) / nsplit;
   const int kb0 = split * per_split;
   const int kb1 = (kb0 + per_split) < nblocks_all ? (kb0 + per_split) : nblocks_all;
-  auto issue = [&](int kb, int buf) {
-    char* Ks = lds + buf * STAGE;
-    char* Vs = Ks + K_BYTES;
+  const int nb = kb1 > kb0 ? kb1 - kb0 : 0;
+  // K row k_row[i] of key block 0; a block advances every row by k_step bytes
+  const char* k_blk0[K_DMA];
 #pragma unroll
-    for (int i = 0; i < K_DMA; ++i) {
-      int key = kb * kAttnKB + k_row[i];
-      key = key < Tk ? key : Tk - 1;
-      adma16(k_src[i] + (int64_t)key * k_rs * 2, Ks + (WAVES * i + wave) * 1024);
+  for (int i = 0; i < K_DMA; ++i) k_blk0[i] = k_src[i] + (int64_t)k_row[i] * k_rs * 2;
+  const int64_t k_step = (int64_t)kAttnKB * k_rs * 2;
+  auto issue_k = [&](int kb, int buf) {
+    char* Ks = Ks0 + buf * K_BYTES;
+    if ((kb + 1) * kAttnKB <= Tk) {
+#pragma unroll
+      for (int i = 0; i < K_DMA; ++i) adma16(k_blk0[i] + kb * k_step, Ks + (WAVES * i + wave) * 1024);
+    } else {  // last, partial block: rows past Tk repeat row Tk-1 (their scores are masked)
+#pragma unroll
+      for (int i = 0; i < K_DMA; ++i) {
+        int key = kb * kAttnKB + k_row[i];
+        key = key < Tk ? key : Tk - 1;
+        adma16(k_src[i] + (int64_t)key * k_rs * 2, Ks + (WAVES * i + wave) * 1024);
+      }
     }
+  };
+  auto issue_v = [&](int kb, int buf) {
+    char* Vs = Vs0 + buf * V_BYTES;
 #pragma unroll
     for (int i = 0; i < V_DMA; ++i)
       adma16(v_src[i] + (int64_t)kb * kAttnKB * 2, Vs + (WAVES * i + wave) * 1024);
   };
+
+  // Loop-invariant fragment-read offsets; ring buffer, 32-row sub-block and
+  // O^T tile enter as immediates.  K row sb*32+l32, 16-byte chunk 2*ds+hh;
+  // Vt row t*32+l32, chunk 2*j+hh for P.V step j = 2*sb + st.
+  const int k_swz = (K_CH == 16) ? (l32 & 15) : ((l32 >> 1) & 7);
+  const int v_swz = (l32 >> 1) & 7;
+  int k_addr[DSTEPS], v_addr[4];
+#pragma unroll
+  for (int ds = 0; ds < DSTEPS; ++ds) k_addr[ds] = l32 * K_ROWB + (((2 * ds + hh) ^ k_swz) * 16);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v_addr[j] = l32 * V_ROWB + (((2 * j + hh) ^ v_swz) * 16);
 
   f32x16 acc[DTILES];
 #pragma unroll
   for (int t = 0; t < DTILES; ++t)
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[t][e] = 0.0f;
-  float m_run = -INFINITY, l_run = 0.0f;
+  f32x16 s[2][2];        // S^T of two consecutive key blocks (ping-pong by block parity)
+  uint32_t pw[4][4];     // P^T fragments (bf16 pairs) of one block
+  bf16x8 vf[4][DTILES];  // Vt fragments in flight
+  bf16x8 kf[DSTEPS][2];  // K fragments in flight
+  float pe[32];          // exps of a block (an even element waits for its pair)
+  float m_run = -INFINITY, l_run = 0.0f, neg_m = INFINITY, alpha_pend = 1.0f;
+  float rs = 0.0f;       // row sum of the block whose exps are in flight
 
-  // fragment-read offsets
-  int k_off[2];
+  // Software pipeline.  Iteration b = [half 1: S^T MFMAs of block b] then
+  // [half 2: P.V MFMAs of block b-1].  Per 32-query wave a 64-key block costs
+  // NQ + NP MFMAs and ~110 VALU instructions (max, scale fma, exp2, sum, bf16
+  // pack); VALU work overlaps only the issuing wave's own MFMAs, so the
+  // softmax of block b is spread one piece per MFMA slot over half 2 of
+  // iteration b (row max, then the max update, then the first exps) and half 1
+  // of iteration b+1 (the remaining exps).  A P^T fragment of block b is
+  // written only after the last P.V MFMA of block b-1 that reads it.
+  using Sch = AttnSched<NP, NQ, DTILES>;
+  static_assert(Sch::valid(), "softmax slot schedule");
+  auto half_sum = [](float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  };
+  auto half_max = [](float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  };
+  // exps of the block in s[X] that fall in slot G (counted from its half 2)
+  auto do_exps = [&](auto xc, int G) {
+    constexpr int X = decltype(xc)::value;
 #pragma unroll
-  for (int sb = 0; sb < 2; ++sb) k_off[sb] = (sb * 32 + l32) * K_ROWB;
-  const int k_swz = (K_CH == 16) ? (l32 & 15) : ((l32 >> 1) & 7);  // rows sb*32+l32 share it
-  int v_off[DTILES];
-#pragma unroll
-  for (int t = 0; t < DTILES; ++t) v_off[t] = (t * 32 + l32) * V_ROWB;
-  const int v_swz = (l32 >> 1) & 7;
-
-  if (kb0 < kb1) issue(kb0, 0);
-  for (int kb = kb0; kb < kb1; ++kb) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (kb + 1 < kb1) issue(kb + 1, (kb + 1 - kb0) & 1);
-    const char* Ks = lds + ((kb - kb0) & 1) * STAGE;
-    const char* Vs = Ks + K_BYTES;
-
-    // ---- S^T = K Q^T for two 32-key sub-blocks
-    f32x16 s[2];
-#pragma unroll
-    for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) s[sb][e] = 0.0f;
-#pragma unroll
-    for (int ds = 0; ds < DSTEPS; ++ds) {
-      const int c = ((ds * 2 + hh) ^ k_swz) * 16;
-      bf16x8 kf[2];
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb) kf[sb] = *reinterpret_cast<const bf16x8*>(Ks + k_off[sb] + c);
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb) s[sb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[sb], qf[ds], s[sb], 0, 0, 0);
+    for (int e = 0; e < 32; ++e) {
+      if (Sch::exp_slot(e) == G) {
+        // hardware exp2: P below 2^-126 of the running max flushes to zero
+        pe[e] = __builtin_amdgcn_exp2f(fmaf(s[X][e >> 4][e & 15], scale_log2, neg_m));
+        rs += pe[e];
+        if (e & 1) {
+          uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){pe[e - 1], pe[e]}, bf16x2));
+          // keep the pack and the sum in this slot (pure arithmetic would
+          // otherwise be sunk to its first use, past the MFMAs)
+          asm volatile("" : "+v"(w));
+          pw[e >> 3][(e & 7) >> 1] = w;
+        }
+      }
     }
-
-    // ---- online softmax (log2 domain); the lane owns one query
+    asm volatile("" : "+v"(rs));
+  };
+  auto read_k = [&](int buf, int k) {  // K fragment of S^T slot k
+    kf[k >> 1][k & 1] =
+        *reinterpret_cast<const bf16x8*>(Ks0 + buf * K_BYTES + (k & 1) * 32 * K_ROWB + k_addr[k >> 1]);
+  };
+  // Half 1 of iteration b (parity P): S^T of block b from K buffer P into
+  // s[P] (its first PF K fragments already in flight); remaining exps of
+  // block b-1 (s[1-P]); first Vt reads of half 2.
+  auto half1 = [&](auto pc, auto qkc, auto expc) {
+    constexpr int P = decltype(pc)::value;
+    constexpr bool QK = decltype(qkc)::value, EXP = decltype(expc)::value;
+    const char* Vb = Vs0 + (1 - P) * V_BYTES;
+    if (QK) {
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s[P][sb][e] = 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) {
+      const int ds = k >> 1, sb = k & 1;
+      if (QK) s[P][sb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ds][sb], qf[ds], s[P][sb], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (EXP) do_exps(std::integral_constant<int, 1 - P>(), NP + k);
+      const int kn = k + PF;
+      if (QK && kn < NQ) {
+        read_k(P, kn);
+      } else if (EXP && kn >= NQ) {
+        const int n = kn - NQ;  // first PF Vt fragments of half 2
+        vf[n / DTILES][n % DTILES] =
+            *reinterpret_cast<const bf16x8*>(Vb + (n % DTILES) * 32 * V_ROWB + v_addr[n / DTILES]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (EXP) {
+      l_run += half_sum(rs);
+      rs = 0.0f;
+    }
+  };
+  // keys past Tk in the last block score -inf
+  auto mask_tail = [&](auto pc, int kb) {
+    constexpr int P = decltype(pc)::value;
     if ((kb + 1) * kAttnKB > Tk) {
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = kb * kAttnKB + sb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-          if (key >= Tk) s[sb][r] = -INFINITY;
+          if (key >= Tk) s[P][sb][r] = -INFINITY;
         }
     }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[sb][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_log2;
-    float alpha = 1.0f;
-    if (mx > m_run + kLazyMax) {
-      alpha = __builtin_amdgcn_exp2f(m_run - mx);  // 0 on the first block (m_run = -inf)
-      m_run = mx;
-    }
-    if (__any(alpha != 1.0f)) {
-      l_run *= alpha;
+  };
+  auto sync_stage = [&]() {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  };
+  // Half 2 of iteration b (parity P): P.V of block b-1 from Vt buffer 1-P;
+  // row max of block b (s[P]), the running-max update, first exps of block b.
+  // The running max (log2 domain) is raised only when a block's max exceeds
+  // it by more than 2^kLazyMax; O^T is rescaled just before the next P.V.
+  // Stage sync (NEW only), once this wave has issued its last Vt read of the
+  // half: K_{b+1} and Vt_b become resident, every wave is done with K_b and
+  // Vt_{b-1}, whose buffers then receive K_{b+2} and Vt_{b+1}; the remaining
+  // slots read the first K fragments of block b+1.
+  auto half2 = [&](auto pc, auto pvc, auto newc, int b) {
+    constexpr int P = decltype(pc)::value;
+    constexpr bool PV = decltype(pvc)::value, NEW = decltype(newc)::value;
+    const char* Vb = Vs0 + (1 - P) * V_BYTES;
+    const int kb = kb0 + b;
+    if (PV && __any(alpha_pend != 1.0f)) {
 #pragma unroll
       for (int t = 0; t < DTILES; ++t)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) acc[t][e] *= alpha;
+        for (int e = 0; e < 16; ++e) acc[t][e] *= alpha_pend;
     }
-    float rs = 0.0f;
+    if (NEW) mask_tail(pc, kb);
+    float mx = -INFINITY;
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        // hardware exp2: P below 2^-126 of the running max flushes to zero
-        const float pr = __builtin_amdgcn_exp2f(fmaf(s[sb][r], scale_log2, -m_run));
-        s[sb][r] = pr;
-        rs += pr;
+    for (int n = 0; n < NP; ++n) {
+      const int j = n / DTILES, t = n % DTILES;
+      if (PV) {
+        const bf16x8 pj = __builtin_bit_cast(bf16x8, (u32x4){pw[j][0], pw[j][1], pw[j][2], pw[j][3]});
+        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[j][t], pj, acc[t], 0, 0, 0);
       }
-    l_run += rs + __shfl_xor(rs, 32, 64);
-
-    // ---- O^T += Vt . P^T  (P^T fragment of step (sb, st) = S regs 8st..8st+7)
+      __builtin_amdgcn_sched_barrier(0);
+      const int nn = n + PF;
+      if (PV && nn < NP)
+        vf[nn / DTILES][nn % DTILES] =
+            *reinterpret_cast<const bf16x8*>(Vb + (nn % DTILES) * 32 * V_ROWB + v_addr[nn / DTILES]);
+      if (NEW && nn == NP) {
+        __builtin_amdgcn_sched_barrier(0);
+        sync_stage();
+        if (b + 2 < nb) issue_k(kb + 2, P);
+        if (b + 1 < nb) issue_v(kb + 1, 1 - P);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (NEW && nn >= NP && b + 1 < nb) read_k(1 - P, nn - NP);
+      if (NEW) {
+        if (n < Sch::F) {
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-#pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        bf16x8 pf;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) pf[e] = (bf16)s[sb][8 * st + e];
-        const int chunk = sb * 4 + st * 2 + hh;  // 16-byte chunk of the 64-key row
-#pragma unroll
-        for (int t = 0; t < DTILES; ++t) {
-          const bf16x8 vf = *reinterpret_cast<const bf16x8*>(Vs + v_off[t] + ((chunk ^ v_swz) * 16));
-          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, acc[t], 0, 0, 0);
+          for (int e = 0; e < 32; ++e)
+            if (Sch::max_slot(e) == n) mx = fmaxf(mx, s[P][e >> 4][e & 15]);
+          asm volatile("" : "+v"(mx));
+        } else if (n == Sch::F) {
+          mx = half_max(mx) * scale_log2;
+          float alpha = 1.0f;
+          if (mx > m_run + kLazyMax) {
+            alpha = __builtin_amdgcn_exp2f(m_run - mx);  // 0 on the first block (m_run = -inf)
+            m_run = mx;
+          }
+          l_run *= alpha;
+          alpha_pend = alpha;
+          neg_m = -m_run;
+        } else {
+          do_exps(pc, n);
         }
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using BT = std::integral_constant<bool, true>;
+  using BF = std::integral_constant<bool, false>;
+  // iteration b in [1, nb) with parity P = b & 1
+  auto body = [&](auto pc, int b) {
+    half1(pc, BT(), BT());
+    half2(pc, BT(), BT(), b);
+  };
+
+  if (nb > 0) {
+    issue_k(kb0, 0);
+    sync_stage();
+    if (nb > 1) issue_k(kb0 + 1, 1);
+    issue_v(kb0, 0);
+#pragma unroll
+    for (int k = 0; k < PF; ++k) read_k(0, k);
+    half1(I0(), BT(), BF());
+    half2(I0(), BF(), BT(), 0);
+    int b = 1;
+    for (; b + 1 < nb; b += 2) {
+      body(I1(), b);
+      body(I0(), b + 1);
+    }
+    if (b < nb) body(I1(), b);
+    // drain (iteration nb): last exps and P.V of block nb-1
+    auto drain = [&](auto pc) {
+      half1(pc, BF(), BT());
+      half2(pc, BT(), BF(), 0);
+    };
+    if (nb & 1) drain(I1()); else drain(I0());
   }
 
   const int q = q0 + l32;
