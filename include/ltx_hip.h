@@ -234,6 +234,18 @@ int ltx_quantize_w8_bf16(const void* W, int64_t ldw, int64_t N, int64_t K, int8_
 int ltx_dequantize_w8_bf16(const int8_t* q, int64_t ldq, const float* scale, int64_t N,
                            int64_t K, void* out, int64_t ldo, void* stream);
 
+/* FP8 checkpoint tensor dequantisation -- the numeric step of
+ * loader/transformer_cache.py:658-708 (_iter_fp8_checkpoint_weights):
+ *   out[i] = OUT(from_fp8(codes[i]) * weight_scale)
+ * with the E4M3 decode exact (0x7F / 0xFF NaN), the product in fp32 and one
+ * round-to-nearest-even into OUT = bf16 (out_dtype 0) or fp32 (out_dtype 1).
+ * scale: device pointer to the tensor's fp32 weight_scale, or NULL for an
+ * unscaled tensor (exact decode).  codes and out 16-byte aligned, n elements
+ * (any n >= 0), flat.  E5M2 is not decoded (the reference rejects it too).
+ */
+int ltx_dequantize_fp8_e4m3(const uint8_t* codes, int64_t n, const float* scale, void* out,
+                            int out_dtype, void* stream);
+
 /* ---- attention ---------------------------------------------------------------
  * Flash attention with the per-head output gate fused (replaces
  * attention.py:283-302 -> kernels/steel_attention.py:251-280 and the gate of

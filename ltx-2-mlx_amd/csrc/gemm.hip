@@ -307,47 +307,65 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
       }
     }
   };
-  auto lwrite = [&](int d, int buf) {
+  // LDS write of load d, in NPART pieces (part = 0 .. NPART-1) issued in
+  // consecutive MFMA slots: an 8-bit weight load is dequantised a quarter at
+  // a time (its ~16 VALU instructions in one slot would idle the matrix pipe
+  // for two MFMAs), the last piece writes the 16 bf16 to LDS.
+  float b_sc[B_CONV ? B_DMA : 1];      // dequantisation scale of the load in flight
+  uint32_t b_o[B_CONV ? B_DMA : 1][8];  // its bf16 pairs
+  auto lwrite = [&](int d, int buf, int part, int nparts) {
     if constexpr (REG) {
       char* As = lds + buf * STAGE;
       if (!B_CONV || d < A_DMA) {
+        if (part != nparts - 1) return;
         char* dst = d < A_DMA ? As + (4 * d + wave) * 1024 : As + A_BYTES + (4 * (d - A_DMA) + wave) * 1024;
         *reinterpret_cast<u32x4*>(dst + lane * 16) = rg[d];
       } else {
         const int i = d - A_DMA;
         const u32x4 w = rg[d];
-        uint32_t o[8];
-        if constexpr (BKIND == B_MXFP8) {
-          // The loaded word goes straight into the empty asm, which pins the
-          // byte extraction and decode here: hoisted to the top of the loop
-          // they made every iteration wait for the previous stage's loads.
-          uint32_t e = rsc[i];
-          asm volatile("" : "+v"(e));
-          const float sc = e8m0_to_f32((e >> rsh[i]) & 0xffu);
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            o[2 * q] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[q], sc, false));
-            o[2 * q + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[q], sc, true));
+        if (part == 0) {
+          if constexpr (BKIND == B_MXFP8) {
+            // The loaded word goes straight into the empty asm, which pins the
+            // byte extraction and decode here: hoisted to the top of the loop
+            // they made every iteration wait for the previous stage's loads.
+            uint32_t e = rsc[i];
+            asm volatile("" : "+v"(e));
+            b_sc[i] = e8m0_to_f32((e >> rsh[i]) & 0xffu);
+          } else {
+            b_sc[i] = b_s8[i];
           }
-        } else {
-          const float sc = b_s8[i], nb = -128.0f * sc;
+        }
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < 4; ++q) {
+          if (q * nparts / 4 != part) continue;
+          const float sc = b_sc[i];
+          if constexpr (BKIND == B_MXFP8) {
+            b_o[i][2 * q] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[q], sc, false));
+            b_o[i][2 * q + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[q], sc, true));
+          } else {
+            const float nb = -128.0f * sc;
             const uint32_t u = w[q] ^ 0x80808080u;
             bf16x2 p0, p1;
             p0[0] = (bf16)fmaf((float)(u & 0xffu), sc, nb);
             p0[1] = (bf16)fmaf((float)((u >> 8) & 0xffu), sc, nb);
             p1[0] = (bf16)fmaf((float)((u >> 16) & 0xffu), sc, nb);
             p1[1] = (bf16)fmaf((float)(u >> 24), sc, nb);
-            o[2 * q] = __builtin_bit_cast(uint32_t, p0);
-            o[2 * q + 1] = __builtin_bit_cast(uint32_t, p1);
+            b_o[i][2 * q] = __builtin_bit_cast(uint32_t, p0);
+            b_o[i][2 * q + 1] = __builtin_bit_cast(uint32_t, p1);
           }
+          // keep this piece in its slot (pure arithmetic would otherwise be
+          // sunk to the LDS write)
+          asm volatile("" : "+v"(b_o[i][2 * q]), "+v"(b_o[i][2 * q + 1]));
         }
-        const int r = b_dst[i] / B_ROWB;
-        char* row = As + A_BYTES + b_dst[i];
-        const int x = chunk_xor<B_ROWB, SWZ>(r);
-        *reinterpret_cast<u32x4*>(row + ((2 * b_c16[i]) ^ x) * 16) = u32x4{o[0], o[1], o[2], o[3]};
-        *reinterpret_cast<u32x4*>(row + ((2 * b_c16[i] + 1) ^ x) * 16) = u32x4{o[4], o[5], o[6], o[7]};
+        if (part == nparts - 1) {
+          const int r = b_dst[i] / B_ROWB;
+          char* row = As + A_BYTES + b_dst[i];
+          const int x = chunk_xor<B_ROWB, SWZ>(r);
+          *reinterpret_cast<u32x4*>(row + ((2 * b_c16[i]) ^ x) * 16) =
+              u32x4{b_o[i][0], b_o[i][1], b_o[i][2], b_o[i][3]};
+          *reinterpret_cast<u32x4*>(row + ((2 * b_c16[i] + 1) ^ x) * 16) =
+              u32x4{b_o[i][4], b_o[i][5], b_o[i][6], b_o[i][7]};
+        }
       }
     }
   };
@@ -487,7 +505,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
 #pragma unroll
     for (int d = 0; d < L; ++d) gload(d, 0);
 #pragma unroll
-    for (int d = 0; d < L; ++d) lwrite(d, 0);
+    for (int d = 0; d < L; ++d) lwrite(d, 0, 0, 1);
 #pragma unroll
     for (int d = 0; d < L; ++d) gload(d, KT > 1 ? 1 : 0);
   } else {
@@ -524,14 +542,21 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
       wait_lgkmcnt0();
       if constexpr (REG) {
         constexpr int NM = TM * TN, SLOTS = (KSTEPS - 1) * NM;
+        // slots of a dequantising (8-bit weight) load: up to 4, within its share
+        constexpr int BPARTS = (SLOTS / L) < 4 ? (SLOTS / L) : 4;
+        static_assert(!B_CONV || BPARTS >= 1, "slots per load");
         mfmas_with(fa[kk & 1], fb[kk & 1], kk, [&](int m) {
           if (m < TM + TN) read_frag(buf, kk + 1, m, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
 #pragma unroll
-          for (int d = 0; d < L; ++d)
-            if ((d * SLOTS) / L == kk * NM + m && write) {
-              lwrite(d, wbuf);
-              gload(d, kt_load);
-            }
+          for (int d = 0; d < L; ++d) {
+            const int np = (B_CONV && d >= A_DMA) ? BPARTS : 1;
+#pragma unroll
+            for (int part = 0; part < np; ++part)
+              if ((d * SLOTS) / L + part == kk * NM + m && write) {
+                lwrite(d, wbuf, part, np);
+                if (part == np - 1) gload(d, kt_load);
+              }
+          }
         });
       } else {
         read_frags(buf, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);

@@ -8,9 +8,14 @@
 //     X = floor(log2(max|w|)) - 8 (8 = E4M3 emax), clamped to [-127, 127],
 //     scale byte = X + 127, code = E4M3(w / 2^X) rounded to nearest-even and
 //     saturated to +-448.  An all-zero block gets X = -127.
+// FP8 checkpoints (loader/transformer_cache.py:658-708): E4M3 codes with an
+//   optional per-tensor fp32 weight_scale, dequantised at load time as
+//   from_fp8(w) * scale in fp32 and rounded once to the cache dtype.
 // int8 W8A16 (per output channel, symmetric):
 //     s[n] = max_k |w[n,k]| / 127 (fp32), q = clamp(rint(w / s), -127, 127);
 //     a zero row has s = 0 and q = 0.  Decode: w' = bf16(fp32(q) * s).
+#include <type_traits>
+
 #include "ltx_common.h"
 
 namespace ltx {
@@ -148,6 +153,54 @@ __global__ void w8_dequantize_kernel(const int8_t* __restrict__ q, int64_t ldq,
   *reinterpret_cast<bf16x8*>(out + n * ldo + c * 8) = o;
 }
 
+// E4M3 code -> float, exact: (-1)^s 2^(e-7) (1 + m/8), subnormals (e = 0)
+// m 2^-9, 0x7F / 0xFF NaN, no infinities.  The subnormals are formed from
+// the integer m rather than an fp32 denormal, so the decode does not depend on
+// the denormal mode.
+__device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
+  const uint32_t e = (c >> 3) & 0xFu, m = c & 7u;
+  const float mag = e == 0u ? (float)m * 0.001953125f : __uint_as_float(((e + 120u) << 23) | (m << 20));
+  const float v = (c & 0x7Fu) == 0x7Fu ? __builtin_nanf("") : mag;
+  return (c & 0x80u) ? -v : v;
+}
+
+// FP8 checkpoint dequantisation: out[i] = OUT(e4m3(codes[i]) * scale) with the
+// product in fp32 (scale = 1 without a weight_scale: exact).  16 codes per
+// thread; the tail (n % 16) one code per thread.
+template <typename OUT>
+__global__ __launch_bounds__(256) void fp8_dequant_kernel(const uint8_t* __restrict__ codes, int64_t n,
+                                                          const float* __restrict__ scale,
+                                                          OUT* __restrict__ out) {
+  const float sc = scale ? *scale : 1.0f;
+  const int64_t groups = n / 16;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < groups) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(codes + t * 16);
+    float v[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) v[4 * q + b] = e4m3_to_f32((w[q] >> (8 * b)) & 0xFFu) * sc;
+    if constexpr (std::is_same_v<OUT, bf16>) {
+      bf16x8 o0, o1;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        o0[e] = (bf16)v[e];
+        o1[e] = (bf16)v[8 + e];
+      }
+      *reinterpret_cast<bf16x8*>(out + t * 16) = o0;
+      *reinterpret_cast<bf16x8*>(out + t * 16 + 8) = o1;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        *reinterpret_cast<f32x4*>(out + t * 16 + 4 * e) = f32x4{v[4 * e], v[4 * e + 1], v[4 * e + 2], v[4 * e + 3]};
+    }
+  } else if (t < groups + n % 16) {
+    const int64_t i = groups * 16 + (t - groups);
+    out[i] = (OUT)(e4m3_to_f32(codes[i]) * sc);
+  }
+}
+
 }  // namespace ltx
 
 using namespace ltx;
@@ -204,5 +257,22 @@ extern "C" int ltx_dequantize_w8_bf16(const int8_t* q, int64_t ldq, const float*
   if (total == 0) return LTX_OK;
   w8_dequantize_kernel<<<(int)((total + 255) / 256), 256, 0, (hipStream_t)stream>>>(
       q, ldq, scale, N, K, (bf16*)out, ldo);
+  return ltx_launch_status();
+}
+
+// FP8 E4M3 checkpoint tensor -> bf16 (out_dtype 0) or fp32 (out_dtype 1).
+extern "C" int ltx_dequantize_fp8_e4m3(const uint8_t* codes, int64_t n, const float* scale, void* out,
+                                       int out_dtype, void* stream) {
+  if (!codes || !out || n < 0) return LTX_ERR_INVALID_ARG;
+  if (out_dtype != 0 && out_dtype != 1) return LTX_ERR_UNSUPPORTED;
+  if (!a16(codes) || !a16(out) || ((uintptr_t)scale & 3u)) return LTX_ERR_ALIGNMENT;
+  const int64_t threads = n / 16 + n % 16;
+  if (threads == 0) return LTX_OK;
+  if ((threads + 255) / 256 > INT32_MAX) return LTX_ERR_UNSUPPORTED;
+  const int blocks = (int)((threads + 255) / 256);
+  if (out_dtype == 0)
+    fp8_dequant_kernel<bf16><<<blocks, 256, 0, (hipStream_t)stream>>>(codes, n, scale, (bf16*)out);
+  else
+    fp8_dequant_kernel<float><<<blocks, 256, 0, (hipStream_t)stream>>>(codes, n, scale, (float*)out);
   return ltx_launch_status();
 }

@@ -44,6 +44,7 @@ SIGNATURES: dict[str, list] = {
     "ltx_dequantize_mxfp8_bf16": [_vp, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _vp],
     "ltx_quantize_w8_bf16": [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp],
     "ltx_dequantize_w8_bf16": [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp],
+    "ltx_dequantize_fp8_e4m3": [_vp, _i64, _vp, _vp, _int, _vp],
     "ltx_attn_transpose_v_bf16": [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp],
     "ltx_flash_attn_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _vp],
     "ltx_flash_attn_splitkv_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64,

@@ -14,6 +14,10 @@
   its invariants (scale range, round trip of representable blocks).
 * int8 per-channel W8A16: defined by the build (the reference has no int8
   path); closed form, pinned by brute-force minimisation.
+* FP8 checkpoint dequantisation (loader/transformer_cache.py:691-705):
+  ``from_fp8(w) * weight_scale`` in fp32, rounded once; pinned against torch's
+  float8_e4m3fn -> float32 product -> bfloat16 casts and the reference's known
+  answer (0x38 with weight_scale 2.0 -> 2.0).
 """
 
 from __future__ import annotations
@@ -36,6 +40,16 @@ def e4m3_decode_table() -> np.ndarray:
 
 
 _TABLE = e4m3_decode_table()
+
+
+def fp8_checkpoint_dequant(codes, scale=None, out: str = "bf16") -> np.ndarray:
+    """``out(from_fp8(codes) * scale)``, product in fp32 (exact decode without
+    a scale); ``out`` "bf16" (RNE, as float32 values) or "f32"."""
+    v = _TABLE[np.asarray(codes, dtype=np.uint8)]
+    if scale is not None:
+        with np.errstate(over="ignore"):  # IEEE overflow to +-inf is the defined result
+            v = (v * np.float32(scale)).astype(np.float32)
+    return bf16r(v) if out == "bf16" else v
 _POS = _TABLE[:0x7F].astype(np.float64)  # codes 0x00..0x7E, ascending
 
 

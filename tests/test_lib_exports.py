@@ -64,3 +64,9 @@ def test_argument_validation_without_gpu():
     assert lib.ltx_flash_attn_bf16(16, 4096, 16, 4096, 16, 64, 16, 4096, None, 0, 4, 4, 32, 96, 0.1, None) == -2
     # zero rows is a no-op success
     assert lib.ltx_adaln_norm_fused_bf16(16, 4096, 16, 16, 16, 4096, 0, 4096, 1e-6, 0, None) == 0
+    # FP8 checkpoint dequant: null codes -> invalid, fp16 output -> unsupported,
+    # misaligned codes -> alignment, zero elements -> no-op success
+    assert lib.ltx_dequantize_fp8_e4m3(None, 16, None, 16, 0, None) == -1
+    assert lib.ltx_dequantize_fp8_e4m3(16, 16, None, 16, 2, None) == -2
+    assert lib.ltx_dequantize_fp8_e4m3(17, 16, None, 16, 0, None) == -4
+    assert lib.ltx_dequantize_fp8_e4m3(16, 0, None, 16, 0, None) == 0
