@@ -40,7 +40,9 @@
 //     and gate columns come from LDS and residual rows are fetched before the
 //     tile is staged, so the epilogue never waits on memory per element.
 //   * blockIdx -> tile: consecutive tiles go to the same XCD (the hardware
-//     round-robins workgroups over the 8 XCDs), grouped 8 tile-rows at a time.
+//     round-robins workgroups over the 8 XCDs), grouped 4 tile-rows at a
+//     time: the 32 concurrent tiles of an XCD form 4 x 8, the fewest distinct
+//     activation and weight bytes per K step.
 #include <type_traits>
 
 #include "ltx_common.h"
@@ -71,7 +73,7 @@ struct GemmArgs {
 };
 
 constexpr int kGemmThreads = 256;
-constexpr int kGroupM = 8;
+constexpr int kGroupM = 4;
 constexpr int kNumXcd = 8;
 
 // GELU with the tanh approximation (feed_forward.py:8-14).  tanh(u) is
@@ -322,6 +324,12 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
         *reinterpret_cast<u32x4*>(dst + lane * 16) = rg[d];
       } else {
         const int i = d - A_DMA;
+        if (part == 0 && (b_dst[i] / B_ROWB) & 1) {
+          // odd rows convert their upper 8 codes first, so their first LDS
+          // write fills the chunks the even row above leaves free
+          const u32x4 v = rg[d];
+          rg[d] = u32x4{v[2], v[3], v[0], v[1]};
+        }
         const u32x4 w = rg[d];
         if (part == 0) {
           if constexpr (BKIND == B_MXFP8) {
@@ -358,12 +366,15 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
           asm volatile("" : "+v"(b_o[i][2 * q]), "+v"(b_o[i][2 * q + 1]));
         }
         if (part == nparts - 1) {
-          const int r = b_dst[i] / B_ROWB;
+          // rows 2m and 2m+1 share their chunk swizzle: the even row writes
+          // its even chunks first, the odd row its odd chunks, so each write
+          // instruction covers every chunk position of the two rows once
+          const int r = b_dst[i] / B_ROWB, odd = r & 1;
           char* row = As + A_BYTES + b_dst[i];
           const int x = chunk_xor<B_ROWB, SWZ>(r);
-          *reinterpret_cast<u32x4*>(row + ((2 * b_c16[i]) ^ x) * 16) =
+          *reinterpret_cast<u32x4*>(row + ((2 * b_c16[i] + odd) ^ x) * 16) =
               u32x4{b_o[i][0], b_o[i][1], b_o[i][2], b_o[i][3]};
-          *reinterpret_cast<u32x4*>(row + ((2 * b_c16[i] + 1) ^ x) * 16) =
+          *reinterpret_cast<u32x4*>(row + ((2 * b_c16[i] + 1 - odd) ^ x) * 16) =
               u32x4{b_o[i][4], b_o[i][5], b_o[i][6], b_o[i][7]};
         }
       }
@@ -550,9 +561,10 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
 #pragma unroll
           for (int d = 0; d < L; ++d) {
             const int np = (B_CONV && d >= A_DMA) ? BPARTS : 1;
+            const int slot0 = (d * SLOTS) / L;
 #pragma unroll
             for (int part = 0; part < np; ++part)
-              if ((d * SLOTS) / L + part == kk * NM + m && write) {
+              if (slot0 + part == kk * NM + m && write) {
                 lwrite(d, wbuf, part, np);
                 if (part == np - 1) gload(d, kt_load);
               }
