@@ -62,7 +62,7 @@ def parse_args(argv=None):
     ap.add_argument("--kernel-steps", type=int, default=2, help="eager steps for the dominant-kernel timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-fused-bench", action="store_true")
-    ap.add_argument("--counter-workload", choices=["ff-up", "copy"], default=None,
+    ap.add_argument("--counter-workload", choices=["ff-up", "ff-up-vs-library", "copy"], default=None,
                     help="run only a short workload for rocprofv3 --pmc passes and exit: the video FF "
                          "up-projection GEMM (4 launches, --weights format) or a 1 GiB device copy (3 "
                          "launches, the FETCH_SIZE / WRITE_SIZE calibration)")
@@ -79,6 +79,18 @@ def counter_workload(kind: str, weights: str) -> None:
         dst = torch.empty_like(src)
         for _ in range(3):
             dst.copy_(src)
+    elif kind == "ff-up-vs-library":
+        # the FF up-projection shape through the vendor library (hipBLASLt,
+        # plain bf16 linear) and through this library's bf16 and MXFP8 GEMMs
+        g = torch.Generator(device="cuda").manual_seed(0)
+        x = torch.randn((3456, 4096), generator=g, device="cuda").bfloat16()
+        w = (torch.randn((16384, 4096), generator=g, device="cuda") * 0.02).bfloat16()
+        b = torch.zeros(16384, device="cuda")
+        wb, wm = gemm.make_weight(w, b, kind="bf16"), gemm.make_weight(w, b, kind="mxfp8")
+        for _ in range(3):
+            torch.nn.functional.linear(x, w)
+            gemm.linear(x, wb, tile=gemm.TILE_256)
+            gemm.linear(x, wm, tile=gemm.TILE_256)
     else:
         g = torch.Generator(device="cuda").manual_seed(0)
         x = torch.randn((3456, 4096), generator=g, device="cuda").bfloat16()
