@@ -195,6 +195,13 @@ int ltx_broadcast_add_f32(const float* table, const float* vec, float* out, int6
 #define LTX_GEMM_TILE_256 (1 << 8)
 #define LTX_GEMM_TILE_128 (2 << 8)
 #define LTX_GEMM_TILE_256_DMA (3 << 8) /* 256x256, LDS-DMA loader */
+/* OR-ed into `epilogue`: the bias is added to the bf16-rounded product,
+ * acc' = bf16(acc) + bias, before the epilogue's own steps -- the
+ * quantised-linear form `quantized_matmul(x, w) + bias` of nn.QuantizedLinear
+ * (loader/transformer_cache.py:177-193), which rounds the product to the
+ * activation dtype before the bias add.  Without it the bias is added to the
+ * fp32 accumulator (mx.addmm, one rounding). */
+#define LTX_GEMM_ROUND_THEN_BIAS (1 << 12)
 
 int ltx_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, const float* bias,
                   void* C, int64_t ldc, int64_t M, int64_t N, int64_t K, int epilogue,

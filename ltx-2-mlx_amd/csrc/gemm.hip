@@ -68,6 +68,7 @@ struct GemmArgs {
   int64_t ldr;
   const float* gate;   // fp32 (N)
   int sig_from;        // columns n >= sig_from get the 2*sigmoid head-gate epilogue
+  int round_then_bias; // bias added to the bf16-rounded product (quantised-linear form)
   int M, N, K;
   int tiles_m, tiles_n;
 };
@@ -642,6 +643,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
   // column of this wave tile takes the head-gate sigmoid is wave-uniform, so
   // the common case runs without it.
   char* E = lds + wave * EPI_WAVE;
+  const bool rtb = p.round_then_bias != 0;
   auto phase1 = [&](auto sig_tag) {
     constexpr bool SIG = decltype(sig_tag)::value;
 #pragma unroll
@@ -656,7 +658,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
           float y[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            y[e] = acc[i][j][4 * g + e] + bias4[e];
+            const float a = acc[i][j][4 * g + e];
+            y[e] = (rtb ? round_bf(a) : a) + bias4[e];
             if (EPI == LTX_GEMM_EPI_GELU) y[e] = gelu_tanh(round_bf(y[e]));
             if (EPI == LTX_GEMM_EPI_SIGMOID2) y[e] = sigmoid2_bf(round_bf(y[e]));
             if (SIG && gn + e >= p.sig_from) y[e] = sigmoid2_bf(round_bf(y[e]));
@@ -737,12 +740,14 @@ static int launch_kind(const GemmArgs& p, int epilogue, hipStream_t s) {
   const int epi = epilogue & 0xff;
   const int tile = (epilogue >> 8) & 0xf;
   if (tile > 3) return LTX_ERR_INVALID_ARG;
+  GemmArgs q = p;
+  q.round_then_bias = (epilogue & LTX_GEMM_ROUND_THEN_BIAS) != 0;
   switch (epi) {
-    case LTX_GEMM_EPI_BIAS: launch_epi<BKIND, LTX_GEMM_EPI_BIAS>(p, tile, s); break;
-    case LTX_GEMM_EPI_GELU: launch_epi<BKIND, LTX_GEMM_EPI_GELU>(p, tile, s); break;
-    case LTX_GEMM_EPI_RESIDUAL: launch_epi<BKIND, LTX_GEMM_EPI_RESIDUAL>(p, tile, s); break;
-    case LTX_GEMM_EPI_RESIDUAL_ROUND: launch_epi<BKIND, LTX_GEMM_EPI_RESIDUAL_ROUND>(p, tile, s); break;
-    case LTX_GEMM_EPI_SIGMOID2: launch_epi<BKIND, LTX_GEMM_EPI_SIGMOID2>(p, tile, s); break;
+    case LTX_GEMM_EPI_BIAS: launch_epi<BKIND, LTX_GEMM_EPI_BIAS>(q, tile, s); break;
+    case LTX_GEMM_EPI_GELU: launch_epi<BKIND, LTX_GEMM_EPI_GELU>(q, tile, s); break;
+    case LTX_GEMM_EPI_RESIDUAL: launch_epi<BKIND, LTX_GEMM_EPI_RESIDUAL>(q, tile, s); break;
+    case LTX_GEMM_EPI_RESIDUAL_ROUND: launch_epi<BKIND, LTX_GEMM_EPI_RESIDUAL_ROUND>(q, tile, s); break;
+    case LTX_GEMM_EPI_SIGMOID2: launch_epi<BKIND, LTX_GEMM_EPI_SIGMOID2>(q, tile, s); break;
     default: return LTX_ERR_INVALID_ARG;
   }
   return ltx_launch_status();
@@ -760,6 +765,7 @@ static int gemm_check(const void* A, int64_t lda, const void* B, int64_t ldb, vo
   if (!A || !B || !C || M < 0 || N < 0 || K < 0) return LTX_ERR_INVALID_ARG;
   if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 2) return LTX_ERR_UNSUPPORTED;
   const int epi = epilogue & 0xff;
+  if (epilogue & ~(0xfff | LTX_GEMM_ROUND_THEN_BIAS)) return LTX_ERR_INVALID_ARG;
   if ((epi == LTX_GEMM_EPI_RESIDUAL || epi == LTX_GEMM_EPI_RESIDUAL_ROUND) && (!R || !gate || ldr < N))
     return LTX_ERR_INVALID_ARG;
   if (K % 64 != 0 || N % 8 != 0) return LTX_ERR_UNSUPPORTED;
@@ -788,6 +794,7 @@ static GemmArgs make_args(const void* A, int64_t lda, const void* B, int64_t ldb
   p.ldr = ldr;
   p.gate = gate;
   p.sig_from = (int)(sigmoid_from < N ? (sigmoid_from < 0 ? 0 : sigmoid_from) : N);
+  p.round_then_bias = 0;
   p.M = (int)M;
   p.N = (int)N;
   p.K = (int)K;

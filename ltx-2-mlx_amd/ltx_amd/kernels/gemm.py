@@ -46,12 +46,22 @@ class LinearWeight:
     ``w`` is (N, K) in nn.Linear layout: bf16, int8 codes, or E4M3 codes
     (uint8).  ``scale`` is fp32 (N) for int8 and E8M0 uint8 (N, K/32) for
     mxfp8.  ``bias`` is fp32 (N) or None.
+
+    ``qlinear`` selects the reference module whose arithmetic the GEMM
+    reproduces: False for ``nn.Linear`` (``mx.addmm``: bias added to the fp32
+    accumulator, one rounding), True for ``nn.QuantizedLinear`` /
+    ``_PretransposedQuantizedLinear`` (loader/transformer_cache.py:177-193:
+    ``quantized_matmul(x, w) + bias``, the product rounded to bf16 before the
+    bias add).  MXFP8 weights are the reference's quantised linears, so
+    ``make_weight(kind="mxfp8")`` sets it; a quantised cache weight decoded
+    to bf16 keeps it.
     """
 
     kind: str
     w: torch.Tensor
     scale: torch.Tensor | None = None
     bias: torch.Tensor | None = None
+    qlinear: bool = False
 
     @property
     def out_features(self) -> int:
@@ -100,7 +110,7 @@ def make_weight(w: torch.Tensor, bias: torch.Tensor | None = None, kind: str = "
     if kind == "bf16":
         return LinearWeight("bf16", w.contiguous(), None, b)
     q, s = _quantize(kind, w)
-    return LinearWeight(kind, q, s, b)
+    return LinearWeight(kind, q, s, b, qlinear=kind == "mxfp8")
 
 
 def dequantize(weight: LinearWeight) -> torch.Tensor:
@@ -156,6 +166,8 @@ def linear(x: torch.Tensor, weight: LinearWeight, *, epilogue: int = EPI_BIAS,
         gate = g.contiguous()
         gptr = gate.data_ptr()
     flags = epilogue | (tile << 8)
+    if weight.qlinear and weight.bias is not None:
+        flags |= _lib.GEMM_ROUND_THEN_BIAS
     sig = n if sigmoid_from is None else int(sigmoid_from)
     bias = weight.bias
     bptr = None if bias is None else bias.data_ptr()

@@ -154,15 +154,25 @@ def iter_fp8_checkpoint_weights(weights_path: str | Path, value_dtype: torch.dty
         stored = _load_tensor(mm, data_start, entry, device)
         if key in fp8_keys:
             scale_key = f"{key}_scale"
+            scale = None
             if scale_key in weight_scale_keys:
-                scale = _load_tensor(mm, data_start, header[scale_key], device).to(torch.float32)
-                if scale.numel() == 1:
-                    inter = torch.float32 if value_dtype != torch.bfloat16 else torch.bfloat16
-                    value = dequantize_fp8_e4m3(stored, scale, inter)
-                else:  # broadcast scale: exact decode, then the fp32 product
-                    value = dequantize_fp8_e4m3(stored, None, torch.float32) * scale
-                stored = _cast_for_cache(value, value_dtype, key)
-            else:  # plain E4M3 (|w| <= 448) decodes exactly into every value dtype
-                inter = torch.bfloat16 if value_dtype == torch.bfloat16 else torch.float32
-                stored = dequantize_fp8_e4m3(stored, None, inter).to(value_dtype)
+                scale = _load_tensor(mm, data_start, header[scale_key], device)
+            stored = dequantize_checkpoint_tensor(stored, scale, value_dtype, key)
         yield key, stored
+
+
+def dequantize_checkpoint_tensor(codes: torch.Tensor, scale: torch.Tensor | None, value_dtype: torch.dtype,
+                                 key: str = "") -> torch.Tensor:
+    """One FP8 checkpoint tensor in ``value_dtype`` (transformer_cache.py:691-705):
+    ``from_fp8(codes) * weight_scale`` in fp32 rounded once, or the exact
+    decode without a scale (|w| <= 448 fits every value dtype)."""
+    if scale is None:
+        inter = torch.bfloat16 if value_dtype == torch.bfloat16 else torch.float32
+        return dequantize_fp8_e4m3(codes, None, inter).to(value_dtype)
+    scale = scale.to(device=codes.device, dtype=torch.float32)
+    if scale.numel() == 1:
+        inter = torch.float32 if value_dtype != torch.bfloat16 else torch.bfloat16
+        value = dequantize_fp8_e4m3(codes, scale, inter)
+    else:  # broadcast scale: exact decode, then the fp32 product
+        value = dequantize_fp8_e4m3(codes, None, torch.float32) * scale
+    return _cast_for_cache(value, value_dtype, key)

@@ -49,13 +49,16 @@ class Modality:
 
 
 class LTXModel:
-    """Random-init LTX-2.3 AV transformer (model.py:497-1486)."""
+    """LTX-2.3 AV transformer (model.py:497-1486): random-init weights, or
+    ``init="empty"`` storage filled by ``loader.load_transformer_cache`` /
+    ``loader.load_transformer_weights``."""
 
     def __init__(self, num_layers: int = 48, *, num_attention_heads: int = 32, attention_head_dim: int = 128,
                  in_channels: int = 128, out_channels: int = 128, cross_attention_dim: int = 4096,
                  norm_eps: float = 1e-6, timestep_scale_multiplier: float = 1000.0,
                  av_ca_timestep_scale_multiplier: float = 1000.0, weight_format: str = "bf16",
-                 device: str | torch.device = "cuda", seed: int = 0, audio: bool = True):
+                 device: str | torch.device = "cuda", seed: int = 0, audio: bool = True, init: str = "random",
+                 audio_attention_heads: int = AUDIO_HEADS, audio_attention_head_dim: int = AUDIO_HEAD_DIM):
         self.device = torch.device(device)
         self.num_layers = num_layers
         self.norm_eps = norm_eps
@@ -66,32 +69,42 @@ class LTXModel:
         self.concurrent_audio = True
         self._audio_stream: torch.cuda.Stream | None = None
         self.video_dim = num_attention_heads * attention_head_dim
-        self.audio_dim = AUDIO_HEADS * AUDIO_HEAD_DIM
+        self.audio_dim = audio_attention_heads * audio_attention_head_dim
         self.video_config = TransformerConfig(self.video_dim, num_attention_heads, attention_head_dim,
                                               cross_attention_dim, True, True)
-        self.audio_config = (TransformerConfig(self.audio_dim, AUDIO_HEADS, AUDIO_HEAD_DIM, self.audio_dim, True, True)
+        self.audio_config = (TransformerConfig(self.audio_dim, audio_attention_heads, audio_attention_head_dim,
+                                               self.audio_dim, True, True)
                              if audio else None)
+        if init not in ("random", "empty"):
+            raise ValueError(f"init must be 'random' or 'empty', got {init!r}")
         gen = torch.Generator(device=self.device)
         gen.manual_seed(seed)
         dev = self.device
         vd, ad = self.video_dim, self.audio_dim
+        lin = dict(gen=gen, device=dev, weight_format="bf16", init=init)
+        mlp = dict(device=dev, generator=gen, init=init)
+
+        def table(d):
+            if init == "empty":
+                return torch.zeros((2, d), device=dev)
+            return (torch.randn((2, d), generator=gen, device=dev) * 0.02).contiguous()
 
         # preprocess / output heads (bf16 weights; small, kept unquantised)
-        self.patchify_proj = linear_weight(vd, in_channels, gen=gen, device=dev, weight_format="bf16")
-        self.adaln_single = AdaLayerNormSingle(vd, 9, device=dev, generator=gen)
-        self.prompt_adaln_single = AdaLayerNormSingle(vd, 2, device=dev, generator=gen)
-        self.av_ca_video_scale_shift_adaln_single = AdaLayerNormSingle(vd, 4, device=dev, generator=gen)
-        self.av_ca_a2v_gate_adaln_single = AdaLayerNormSingle(vd, 1, device=dev, generator=gen)
-        self.scale_shift_table = (torch.randn((2, vd), generator=gen, device=dev) * 0.02).contiguous()
-        self.proj_out = linear_weight(out_channels, vd, gen=gen, device=dev, weight_format="bf16")
+        self.patchify_proj = linear_weight(vd, in_channels, **lin)
+        self.adaln_single = AdaLayerNormSingle(vd, 9, **mlp)
+        self.prompt_adaln_single = AdaLayerNormSingle(vd, 2, **mlp)
+        self.av_ca_video_scale_shift_adaln_single = AdaLayerNormSingle(vd, 4, **mlp)
+        self.av_ca_a2v_gate_adaln_single = AdaLayerNormSingle(vd, 1, **mlp)
+        self.scale_shift_table = table(vd)
+        self.proj_out = linear_weight(out_channels, vd, **lin)
         if audio:
-            self.audio_patchify_proj = linear_weight(ad, AUDIO_IN_CHANNELS, gen=gen, device=dev, weight_format="bf16")
-            self.audio_adaln_single = AdaLayerNormSingle(ad, 9, device=dev, generator=gen)
-            self.audio_prompt_adaln_single = AdaLayerNormSingle(ad, 2, device=dev, generator=gen)
-            self.av_ca_audio_scale_shift_adaln_single = AdaLayerNormSingle(ad, 4, device=dev, generator=gen)
-            self.av_ca_v2a_gate_adaln_single = AdaLayerNormSingle(ad, 1, device=dev, generator=gen)
-            self.audio_scale_shift_table = (torch.randn((2, ad), generator=gen, device=dev) * 0.02).contiguous()
-            self.audio_proj_out = linear_weight(out_channels, ad, gen=gen, device=dev, weight_format="bf16")
+            self.audio_patchify_proj = linear_weight(ad, AUDIO_IN_CHANNELS, **lin)
+            self.audio_adaln_single = AdaLayerNormSingle(ad, 9, **mlp)
+            self.audio_prompt_adaln_single = AdaLayerNormSingle(ad, 2, **mlp)
+            self.av_ca_audio_scale_shift_adaln_single = AdaLayerNormSingle(ad, 4, **mlp)
+            self.av_ca_v2a_gate_adaln_single = AdaLayerNormSingle(ad, 1, **mlp)
+            self.audio_scale_shift_table = table(ad)
+            self.audio_proj_out = linear_weight(out_channels, ad, **lin)
 
         # all blocks' modulation tables packed for the one-launch row update
         self.video_tables = torch.empty((num_layers, ADA_ROWS, vd), dtype=torch.float32, device=dev)
@@ -101,7 +114,7 @@ class LTXModel:
         for i in range(num_layers):
             w = build_block(self.video_config, self.audio_config, device=dev, weight_format=weight_format,
                             generator=gen, norm_eps=norm_eps, video_tables=self.video_tables[i],
-                            audio_tables=None if self.audio_tables is None else self.audio_tables[i])
+                            audio_tables=None if self.audio_tables is None else self.audio_tables[i], init=init)
             self.transformer_blocks.append(BasicAVTransformerBlock(i, self.video_config, self.audio_config,
                                                                    norm_eps=norm_eps, weights=w))
         # per-step buffers

@@ -18,10 +18,12 @@ SINUSOID_DIM = 256
 
 class AdaLayerNormSingle:
     def __init__(self, dim: int, num_embeddings: int, *, device="cuda", generator: torch.Generator | None = None,
-                 std: float = 0.02):
+                 std: float = 0.02, init: str = "random"):
         g = generator
 
         def rnd(shape):
+            if init == "empty":  # storage for a checkpoint loader
+                return torch.empty(shape, dtype=torch.bfloat16, device=device)
             return (torch.randn(shape, generator=g, device=device, dtype=torch.float32) * std).to(torch.bfloat16)
 
         self.dim = dim

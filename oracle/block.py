@@ -5,7 +5,9 @@ attention.py:528-603, feed_forward.py:64-112, model.py:285-497, :1312-1342,
 :1489-1542 and diffusion_steps.py:58-69, with every bf16 rounding of the
 reference (``bf`` marks them).  Weights are plain per-projection tensors
 (to_q, to_k, to_v, to_gate_logits, to_out, ...), decoded to their bf16
-values, as in the reference's modules.
+values, as in the reference's modules; ``<name>_qlinear`` marks a projection
+that the reference runs as a quantised linear (bias added after the bf16
+rounding of the product).
 
 AdaLN follows the reference's dispatch default (transformer.py:85-110): the
 compiled inline form ``(rms_norm(x) * (1 + scale) + shift).astype(bf16)``
@@ -47,12 +49,20 @@ def adaln(x, scale, shift, eps=EPS, fused=False):
     return bf(rms_norm_bf(x, eps) * (1 + scale) + shift)
 
 
-def linear(x, w, b=None):
-    """nn.Linear / mx.addmm on bf16: fp32 accumulation, bf16 output."""
+def linear(x, w, b=None, qlinear=False):
+    """nn.Linear / mx.addmm on bf16: fp32 accumulation, bf16 output.  With
+    ``qlinear`` nn.QuantizedLinear's form (loader/transformer_cache.py:
+    177-193): the product is rounded to bf16 before the bias add."""
     y = x @ w.T
+    if qlinear:
+        y = bf(y)
     if b is not None:
         y = y + b
     return bf(y)
+
+
+def _proj(w: dict, name: str, x):
+    return linear(x, w[name], w[name + "_b"], w.get(name + "_qlinear", False))
 
 
 def gelu_tanh(x):
@@ -84,10 +94,10 @@ def sdpa(q, k, v, heads):
 def attention(w: dict, x, context=None, pe=None, k_pe=None, heads=32, eps=EPS):
     """Attention.__call__ (attention.py:528-603)."""
     context = x if context is None else context
-    g = bf(2.0 * bf(torch.sigmoid(linear(x, w["to_gate_logits"], w["to_gate_logits_b"]))))
-    v = linear(context, w["to_v"], w["to_v_b"])
-    q = linear(x, w["to_q"], w["to_q_b"])
-    k = linear(context, w["to_k"], w["to_k_b"])
+    g = bf(2.0 * bf(torch.sigmoid(_proj(w, "to_gate_logits", x))))
+    v = _proj(w, "to_v", context)
+    q = _proj(w, "to_q", x)
+    k = _proj(w, "to_k", context)
     q = bf(q * rms_inv(q, eps) * w["q_norm"])
     k = bf(k * rms_inv(k, eps) * w["k_norm"])
     if pe is not None:
@@ -97,12 +107,12 @@ def attention(w: dict, x, context=None, pe=None, k_pe=None, heads=32, eps=EPS):
     o = sdpa(q, k, v, heads)
     t, d = o.shape
     o = bf(o.view(t, heads, d // heads) * g[:, :, None]).reshape(t, d)
-    return linear(o, w["to_out"], w["to_out_b"])
+    return _proj(w, "to_out", o)
 
 
 def feed_forward(w: dict, x):
-    h = bf(gelu_tanh(linear(x, w["w1"], w["b1"])))
-    return linear(h, w["w2"], w["b2"])
+    h = bf(gelu_tanh(linear(x, w["w1"], w["b1"], w.get("w1_qlinear", False))))
+    return linear(h, w["w2"], w["b2"], w.get("w2_qlinear", False))
 
 
 def block(W: dict, vx, ax, v_ada, a_ada, vctx, actx, vpe, vxpe, ape, axpe, *, fused_adaln=False, eps=EPS):

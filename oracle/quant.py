@@ -115,17 +115,24 @@ def gelu_tanh(x):
     return 0.5 * x * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (x + 0.044715 * x ** 3)))
 
 
-def linear(x, W, b=None, *, epilogue: str = "bias", residual=None, gate=None, exact: bool = False):
+def linear(x, W, b=None, *, epilogue: str = "bias", residual=None, gate=None, exact: bool = False,
+           round_then_bias: bool = False):
     """Oracle of the projection GEMM + epilogue (nn.Linear / mx.addmm,
     attention.py:425-437, feed_forward.py:91-112): the product of the bf16
     values accumulated in fp32 (the reference's accumulator; ``exact=True``
-    uses float64), then the epilogue's rounding points."""
+    uses float64), then the epilogue's rounding points.
+
+    ``round_then_bias`` is nn.QuantizedLinear's form
+    (loader/transformer_cache.py:177-193): ``quantized_matmul`` returns the
+    bf16 product and the bias is added to it in bf16, ``bf16(bf16(x W^T) + b)``."""
     import torch
 
     dt = torch.float64 if exact else torch.float32
     xt = torch.from_numpy(np.asarray(x, np.float32)).to(dt)
     wt = torch.from_numpy(np.asarray(W, np.float32)).to(dt)
     y = (xt @ wt.T).double().numpy()
+    if round_then_bias:
+        y = bf16r(y.astype(np.float32)).astype(np.float64)
     if b is not None:
         y = y + np.asarray(b, np.float64)
     y = bf16r(y.astype(np.float32)).astype(np.float64)

@@ -33,13 +33,18 @@ def attention_weights(a) -> dict:
         w["to_k"], w["to_k_b"] = pkv[:inner], bkv[:inner]
         w["to_v"], w["to_v_b"] = pkv[inner:], bkv[inner:]
     w["to_out"], w["to_out_b"] = _dec(a.to_out), _bias(a.to_out, a.to_out.out_features)
+    for n in ("to_q", "to_k", "to_v", "to_gate_logits"):
+        w[n + "_qlinear"] = (a.proj_q if n in ("to_q", "to_gate_logits") or a.self_attention
+                             else a.proj_kv).qlinear
+    w["to_out_qlinear"] = a.to_out.qlinear
     w["q_norm"], w["k_norm"] = a.q_norm.float().cpu(), a.k_norm.float().cpu()
     return w
 
 
 def ff_weights(f) -> dict:
     return {"w1": _dec(f.project_in), "b1": _bias(f.project_in, f.inner_dim),
-            "w2": _dec(f.project_out), "b2": _bias(f.project_out, f.dim_out)}
+            "w2": _dec(f.project_out), "b2": _bias(f.project_out, f.dim_out),
+            "w1_qlinear": f.project_in.qlinear, "w2_qlinear": f.project_out.qlinear}
 
 
 def block_weights(b) -> dict:

@@ -130,25 +130,29 @@ def test_gemm_block_shapes(kind, K, N):
     wt = gemm.make_weight(_t(W), _t(b, torch.float32), kind=kind)
     out = gemm.linear(_t(x), wt)
     torch.cuda.synchronize()
-    ref = oq.linear(x, _decoded(kind, W), b)
+    ref = oq.linear(x, _decoded(kind, W), b, round_then_bias=kind == "mxfp8")
     _check(bf16_from_torch(out), ref)
 
 
-@pytest.mark.parametrize("epi", ["gelu", "sigmoid2", "residual", "residual_round"])
+@pytest.mark.parametrize("epi", ["bias", "gelu", "sigmoid2", "residual", "residual_round"])
 @pytest.mark.parametrize("tile", [1, 2, 3])
-def test_gemm_epilogues(epi, tile):
+@pytest.mark.parametrize("kind", ["bf16", "mxfp8"])
+def test_gemm_epilogues(epi, tile, kind):
+    """Every epilogue, with a non-zero bias: single rounding for bf16 weights
+    (mx.addmm), bias after the bf16 product for MXFP8 (nn.QuantizedLinear)."""
     from ltx_amd.kernels import gemm
 
-    codes = {"gelu": gemm.EPI_GELU, "sigmoid2": gemm.EPI_SIGMOID2, "residual": gemm.EPI_RESIDUAL,
-             "residual_round": gemm.EPI_RESIDUAL_ROUND}
+    codes = {"bias": gemm.EPI_BIAS, "gelu": gemm.EPI_GELU, "sigmoid2": gemm.EPI_SIGMOID2,
+             "residual": gemm.EPI_RESIDUAL, "residual_round": gemm.EPI_RESIDUAL_ROUND}
     rng = np.random.default_rng(3)
     M, K, N = 700, 1024, 1536
     x = _bf(rng, (M, K))
     W = _bf(rng, (N, K), 0.05)
-    b = rng.standard_normal(N).astype(np.float32) * 0.1
+    b = bf16r(rng.standard_normal(N).astype(np.float32) * 0.1)
     res = _bf(rng, (M, N))
     g = rng.standard_normal(N).astype(np.float32) * 0.5
-    wt = gemm.make_weight(_t(W), _t(b, torch.float32))
+    wt = gemm.make_weight(_t(W), _t(b, torch.float32), kind=kind)
+    assert wt.qlinear == (kind == "mxfp8")
     rt, gt = _t(res), _t(g, torch.float32)
     if epi.startswith("residual"):  # in place on the residual stream
         out = gemm.linear(_t(x), wt, epilogue=codes[epi], out=rt, residual=rt, gate=gt, tile=tile)
@@ -156,8 +160,13 @@ def test_gemm_epilogues(epi, tile):
     else:
         out = gemm.linear(_t(x), wt, epilogue=codes[epi], tile=tile)
     torch.cuda.synchronize()
-    ref = oq.linear(x, W, b, epilogue=epi, residual=res, gate=g)
+    ref = oq.linear(x, _decoded(kind, W), b, epilogue=epi, residual=res, gate=g,
+                    round_then_bias=kind == "mxfp8")
     _check(bf16_from_torch(out), ref, min_exact=0.85)
+    if kind == "mxfp8" and epi != "sigmoid2":  # the other rounding form is measurably further away
+        alt = oq.linear(x, _decoded(kind, W), b, epilogue=epi, residual=res, gate=g)
+        assert (ulp_diff_bf16(bf16_from_torch(out), ref) == 0).mean() > \
+            (ulp_diff_bf16(bf16_from_torch(out), alt) == 0).mean()
 
 
 @pytest.mark.parametrize("M,K,N", [(1, 4096, 4096), (68, 2048, 2048), (68, 2048, 6144), (256, 4096, 8192),

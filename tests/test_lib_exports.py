@@ -70,3 +70,8 @@ def test_argument_validation_without_gpu():
     assert lib.ltx_dequantize_fp8_e4m3(16, 16, None, 16, 2, None) == -2
     assert lib.ltx_dequantize_fp8_e4m3(17, 16, None, 16, 0, None) == -4
     assert lib.ltx_dequantize_fp8_e4m3(16, 0, None, 16, 0, None) == 0
+    # GEMM flags: the quantised-linear bias form is accepted (M = 0: no launch),
+    # an unknown flag bit is rejected
+    assert lib.ltx_gemm_bf16(16, 64, 16, 64, None, 16, 64, 0, 64, 64, _lib.GEMM_ROUND_THEN_BIAS, None, 0, None,
+                             64, None) == 0
+    assert lib.ltx_gemm_bf16(16, 64, 16, 64, None, 16, 64, 0, 64, 64, 1 << 13, None, 0, None, 64, None) == -1

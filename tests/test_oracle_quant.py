@@ -115,3 +115,19 @@ def test_linear_oracle_against_float64_loops(rng, epi):
             elif epi == "residual_round":
                 y = float(res[i, j]) + float(bf16r(np.float32(float(g[j]) * y)))
             assert out[i, j] == bf16r(np.float32(y)), (i, j)
+
+
+def test_linear_oracle_quantized_linear_form_matches_torch_bf16_add(rng):
+    """nn.QuantizedLinear's ``quantized_matmul(x, w) + bias``: the product is a
+    bf16 tensor and the bias add is a bf16 add (transformer_cache.py:177-193).
+    torch's bfloat16 add rounds the same way, so it checks the form."""
+    x = bf16r(rng.standard_normal((16, 64)).astype(np.float32))
+    W = bf16r(rng.standard_normal((40, 64)).astype(np.float32) * 0.1)
+    b = bf16r(rng.standard_normal(40).astype(np.float32))
+    out = oq.linear(x, W, b, exact=True, round_then_bias=True)
+    prod = torch.from_numpy(x).double() @ torch.from_numpy(W).double().T
+    ref = (prod.float().bfloat16() + torch.from_numpy(b).bfloat16()).float().numpy()
+    np.testing.assert_array_equal(out, ref)
+    # and it differs from the single-rounding addmm form somewhere
+    single = oq.linear(x, W, b, exact=True)
+    assert (single != out).any()
