@@ -253,6 +253,53 @@ int ltx_dequantize_w8_bf16(const int8_t* q, int64_t ldq, const float* scale, int
 int ltx_dequantize_fp8_e4m3(const uint8_t* codes, int64_t n, const float* scale, void* out,
                             int out_dtype, void* stream);
 
+/* ---- guided sampling ----------------------------------------------------------
+ * The elementwise math around the transformer passes of the guided loops
+ * (pipelines/av_pipeline.py:625-757, two_stage.py:306-388).  Every operation
+ * is one IEEE fp32 operation in the reference's order; scalars are the fp32
+ * values of the reference's python floats (MLX casts weak scalars to fp32).
+ *
+ * ltx_x0_from_velocity_f32  <- X0Model.denoise (model/transformer/model.py:1519-1525)
+ *   out = latent - sigma * velocity            (bf16 latent / velocity, fp32 out)
+ * ltx_guidance_f32          <- CFGGuider / CFGStarRescalingGuider / STGGuider .guide
+ *                              and .delta, MultiModalGuider.calculate
+ *                              (components/guiders.py:10-172)
+ *   u0  = coef0 ? coef0[0] * term0 : term0
+ *   out = base + c0*(base - u0) + c1*(base - term1) + c2*(base - term2)
+ *         (terms added left to right, absent (NULL) terms skipped), then
+ *         * factor[0] if factor is given;  LTX_GUIDE_DELTA_ONLY: out = c0*(base - u0).
+ *   CFG guide: base=cond, term0=uncond, c0=scale-1; CFG-star: coef0 from the
+ *   projection statistic; STG: base=guided, term0=perturbed, c0=scale;
+ *   MultiModalGuider: base=cond, terms (uncond, perturbed, modality).
+ * ltx_guidance_stats_f32    <- projection_coef (guiders.py:175-190) and the
+ *                              MultiModalGuider std rescale (:155-161); one
+ *                              workgroup, fp64 accumulation of fp32 products:
+ *   LTX_GUIDE_STATS_PROJECTION: out[0] = sum(a*b) / (sum(b*b) + 1e-8)
+ *   LTX_GUIDE_STATS_STD_RATIO:  out[0] = rescale * std(a)/std(b) + one_minus_rescale,
+ *                               std(x) = sqrt(var(x) + 1e-8)
+ * ltx_ge_correct_f32        <- GE velocity correction (av_pipeline.py:722-728), in place:
+ *   cur = (latent - denoised) / sigma; if prev_valid:
+ *   denoised = latent - (gamma*(cur - prev) + prev) * sigma;  prev = cur
+ * ltx_euler_step_bf16       <- EulerDiffusionStep.step (components/diffusion_steps.py:19-69)
+ *   out = bf16(denoised + ratio * (sample - denoised)), ratio = fp32(sigma_next / sigma)
+ * fp32 arrays 16-byte aligned (scalars 4-byte), n elements, flat.
+ */
+#define LTX_GUIDE_DELTA_ONLY 1
+#define LTX_GUIDE_STATS_PROJECTION 1
+#define LTX_GUIDE_STATS_STD_RATIO 2
+
+int ltx_x0_from_velocity_f32(const void* latent, const void* velocity, float sigma, float* out,
+                             int64_t n, void* stream);
+int ltx_guidance_f32(const float* base, const float* term0, const float* term1, const float* term2,
+                     float c0, float c1, float c2, const float* coef0, const float* factor,
+                     float* out, int64_t n, int flags, void* stream);
+int ltx_guidance_stats_f32(const float* a, const float* b, int64_t n, int mode, float rescale,
+                           float one_minus_rescale, float* out, void* stream);
+int ltx_ge_correct_f32(const void* latent, float* denoised, float* prev_velocity, int prev_valid,
+                       float sigma, float gamma, int64_t n, void* stream);
+int ltx_euler_step_bf16(const void* sample, const float* denoised, float ratio, void* out, int64_t n,
+                        void* stream);
+
 /* ---- attention ---------------------------------------------------------------
  * Flash attention with the per-head output gate fused (replaces
  * attention.py:283-302 -> kernels/steel_attention.py:251-280 and the gate of

@@ -50,6 +50,11 @@ SIGNATURES: dict[str, list] = {
     "ltx_flash_attn_splitkv_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64,
                                     _f32, _i64, _vp, _i64, _vp],
     "ltx_broadcast_add_f32": [_vp, _vp, _vp, _i64, _i64, _vp],
+    "ltx_x0_from_velocity_f32": [_vp, _vp, _f32, _vp, _i64, _vp],
+    "ltx_guidance_f32": [_vp, _vp, _vp, _vp, _f32, _f32, _f32, _vp, _vp, _vp, _i64, _int, _vp],
+    "ltx_guidance_stats_f32": [_vp, _vp, _i64, _int, _f32, _f32, _vp, _vp],
+    "ltx_ge_correct_f32": [_vp, _vp, _vp, _int, _f32, _f32, _i64, _vp],
+    "ltx_euler_step_bf16": [_vp, _vp, _f32, _vp, _i64, _vp],
 }
 
 # Flag values (include/ltx_hip.h)

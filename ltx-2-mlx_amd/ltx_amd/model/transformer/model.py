@@ -179,11 +179,15 @@ class LTXModel:
     def velocity(self, video_latent: torch.Tensor, video_context: torch.Tensor, sigma_dev: torch.Tensor,
                  pes: tuple, audio_latent: torch.Tensor | None = None,
                  audio_context: torch.Tensor | None = None,
-                 profile_events: list | None = None) -> tuple[torch.Tensor, torch.Tensor | None]:
+                 profile_events: list | None = None,
+                 perturbations=None) -> tuple[torch.Tensor, torch.Tensor | None]:
         """One transformer forward -> (video velocity (T, 128), audio velocity).
 
         Latents are 2-D (T, 128) bf16; contexts (S, D) bf16; ``sigma_dev`` is
-        the fp32 device scalar of this step's sigma.
+        the fp32 device scalar of this step's sigma.  ``perturbations`` (a
+        ``BatchedPerturbationConfig``) skips attention sub-layers per block, the
+        STG / modality-isolated passes (model.py:1044-1310 hands it to every
+        block).
         """
         vpe, vxpe, ape, axpe = pes
         run_audio = self.audio_config is not None and audio_latent is not None and audio_latent.shape[0] > 0
@@ -215,7 +219,7 @@ class LTXModel:
             block.ada_rows_audio = self._ada_a[i] if run_audio else None
             block.audio_stream = side
             block.audio_fork = i == 0
-            video, audio = block(video, audio, profile_events=profile_events)
+            video, audio = block(video, audio, perturbations=perturbations, profile_events=profile_events)
         if side is not None:
             torch.cuda.current_stream().wait_stream(side)
             audio.x.record_stream(torch.cuda.current_stream())

@@ -51,6 +51,7 @@ from ... import _lib
 from ...kernels import fused_ops, gemm
 from .attention import Attention
 from .feed_forward import FeedForward
+from ...components.perturbations import BatchedPerturbationConfig  # noqa: F401  (the block's perturbation type)
 from .rope import LTXRopeType
 
 # Dispatch shims (transformer.py:85-110): with LTX_FUSED_ADALN=1 the block's
@@ -344,21 +345,6 @@ class BasicAVTransformerBlock:
             return args.replace(x=x2[None] if x_in.dim() == 3 else x2)
 
         return pack(video, v2, vx, v_owned), pack(audio, a2, ax, a_owned)
-
-
-class BatchedPerturbationConfig:
-    """Minimal STG perturbation set: ``all_in_batch(kind, block_idx)``
-    (components/perturbations.py); kinds are the reference's names
-    ``skip_video_self_attn``, ``skip_audio_self_attn``,
-    ``skip_a2v_cross_attn`` and ``skip_v2a_cross_attn``."""
-
-    def __init__(self, skips: dict[str, set[int] | None]):
-        self.skips = skips
-
-    def all_in_batch(self, kind, block_idx: int) -> bool:
-        key = getattr(kind, "value", kind)
-        blocks = self.skips.get(key, set())
-        return blocks is None or block_idx in blocks
 
 
 ProfileHook = Callable[[str], None]

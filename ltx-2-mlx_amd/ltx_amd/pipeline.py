@@ -1,12 +1,23 @@
-"""Distilled audio+video denoise loop on the resident transformer.
+"""Audio+video denoise loops on the resident transformer.
 
-Restates ``AVPipeline._denoise_loop_simple_av`` (pipelines/av_pipeline.py:
-899-1146) for the text-to-video+audio path: uniform denoise masks (scalar
-timestep), no CFG, eight Euler steps over ``DISTILLED_SIGMA_VALUES``.  The
-sigma schedule lives on the device for the whole loop, RoPE tables are built
-once per stage, and a step enqueues its kernels without host synchronisation
-(the reference's one per-step barrier, av_pipeline.py:1113, is left to the
-caller).
+* ``denoise`` / ``denoise_step`` restate ``AVPipeline._denoise_loop_simple_av``
+  (pipelines/av_pipeline.py:899-1146) for the text-to-video+audio path:
+  uniform denoise masks (scalar timestep), no CFG, eight Euler steps over
+  ``DISTILLED_SIGMA_VALUES``.
+* ``denoise_cfg_av`` restates ``_denoise_loop_cfg_av`` (av_pipeline.py:
+  625-757): per step the positive pass, the negative-prompt pass when either
+  modality's CFG guider is enabled, and the STG pass (perturbed video
+  self-attention) while the step is within the STG cutoff; video and audio
+  guided separately, optional GE velocity correction, Euler.
+* ``denoise_multimodal_av`` restates the multi-modal guided loop of
+  pipelines/two_stage.py:306-388: conditioned, unconditioned and
+  modality-isolated passes combined by ``MultiModalGuider``.
+
+The sigma schedule lives on the device for the whole loop, RoPE tables are
+built once per stage, and a step enqueues its kernels without host
+synchronisation (the reference's one per-step barrier, av_pipeline.py:1113,
+is left to the caller).  The uniform denoise mask makes the reference's
+``maybe_post_process_latent`` the identity (pipelines/common.py:299-318).
 """
 
 from __future__ import annotations
@@ -14,6 +25,7 @@ from __future__ import annotations
 import numpy as np
 import torch
 
+from . import _lib
 from .components.diffusion_steps import EulerDiffusionStep
 from .components.patchifiers import audio_latent_frames, video_latent_grid
 from .components.schedulers import DISTILLED_SIGMA_VALUES
@@ -42,8 +54,15 @@ class DenoiseState:
         self.audio_context = torch.randn((text_tokens, model.audio_dim), generator=gen, device=dev).to(torch.bfloat16)
         self.video_positions = video_positions(f, h, w, fps)
         self.audio_positions = audio_positions(self.audio_tokens) if self.audio_tokens else None
-        self.sigmas = [float(s) for s in sigmas]
+        self.sigmas = [float(np.float32(s)) for s in sigmas]
         self.sigmas_dev = torch.tensor(self.sigmas, dtype=torch.float32, device=dev)
+        # negative-prompt contexts of the guided loops (synthetic, own stream of draws)
+        neg = torch.Generator(device=dev)
+        neg.manual_seed(seed + 0x5EED)
+        self.negative_video_context = torch.randn((text_tokens, model.video_dim), generator=neg,
+                                                  device=dev).to(torch.bfloat16)
+        self.negative_audio_context = torch.randn((text_tokens, model.audio_dim), generator=neg,
+                                                  device=dev).to(torch.bfloat16)
 
 
 def denoise_step(model: LTXModel, state: DenoiseState, step: int, pes=None,
@@ -68,6 +87,98 @@ def denoise(model: LTXModel, state: DenoiseState, callback=None) -> DenoiseState
     stepper = EulerDiffusionStep()
     for step in range(len(state.sigmas) - 1):
         denoise_step(model, state, step, pes, stepper)
+        if callback is not None:
+            callback(step, state)
+    return state
+
+
+def _velocities(model: LTXModel, state: DenoiseState, sig, pes, video_context, audio_context, perturbations=None):
+    audio = state.audio_tokens > 0
+    return model.velocity(state.video_latent, video_context, sig, pes,
+                          state.audio_latent if audio else None, audio_context if audio else None,
+                          perturbations=perturbations)
+
+
+def denoise_cfg_av(model: LTXModel, state: DenoiseState, *, video_guider, audio_guider, stg_guider=None,
+                   stg_perturbations=None, stg_cutoff: float = 1.0, ge_gamma: float = 0.0,
+                   callback=None) -> DenoiseState:
+    """Guided joint denoising with separate guidance per modality
+    (av_pipeline.py:625-757), in place on ``state``'s latents."""
+    from .components.diffusion_steps import to_denoised
+
+    pes = model.rope(state.video_positions, state.audio_positions)
+    stepper = EulerDiffusionStep()
+    num_steps = len(state.sigmas) - 1
+    need_cfg = video_guider.enabled() or audio_guider.enabled()
+    audio = state.audio_tokens > 0
+    prev_velocity = None
+    for step in range(num_steps):
+        sigma = state.sigmas[step]
+        sig = state.sigmas_dev[step:step + 1]
+        v_pos, a_pos = _velocities(model, state, sig, pes, state.video_context, state.audio_context)
+        video_d = to_denoised(state.video_latent, v_pos, sigma)
+        audio_d = to_denoised(state.audio_latent, a_pos, sigma) if audio else None
+        if need_cfg:
+            v_neg, a_neg = _velocities(model, state, sig, pes, state.negative_video_context,
+                                       state.negative_audio_context)
+            video_d = video_guider.guide(video_d, to_denoised(state.video_latent, v_neg, sigma))
+            if audio:
+                audio_d = audio_guider.guide(audio_d, to_denoised(state.audio_latent, a_neg, sigma))
+        stg_active = (stg_guider is not None and stg_guider.enabled() and stg_perturbations is not None
+                      and (step + 1) / num_steps <= stg_cutoff)
+        if stg_active:
+            v_ptb, _ = _velocities(model, state, sig, pes, state.video_context, state.audio_context,
+                                   perturbations=stg_perturbations)
+            video_d = stg_guider.guide(video_d, to_denoised(state.video_latent, v_ptb, sigma))
+        if ge_gamma > 0 and sigma > 0:
+            valid = prev_velocity is not None
+            if prev_velocity is None:
+                prev_velocity = torch.empty_like(video_d)
+            _lib.call("ltx_ge_correct_f32", _lib.ptr(state.video_latent), _lib.ptr(video_d), _lib.ptr(prev_velocity),
+                      int(valid), float(sigma), float(ge_gamma), video_d.numel(), _lib.stream_of(video_d))
+        stepper.step(state.video_latent, video_d, state.sigmas, step, out=state.video_latent)
+        if audio:
+            stepper.step(state.audio_latent, audio_d, state.sigmas, step, out=state.audio_latent)
+        if callback is not None:
+            callback(step, state)
+    return state
+
+
+def denoise_multimodal_av(model: LTXModel, state: DenoiseState, *, video_guider, audio_guider,
+                          callback=None) -> DenoiseState:
+    """Multi-modal guided joint denoising (pipelines/two_stage.py:306-388):
+    conditioned pass, unconditioned pass when either guider runs CFG,
+    modality-isolated pass (A2V and V2A skipped in every block) when either
+    runs modality guidance; ``MultiModalGuider.calculate`` per modality."""
+    from .components.diffusion_steps import to_denoised
+    from .components.perturbations import modality_isolation_config
+
+    pes = model.rope(state.video_positions, state.audio_positions)
+    stepper = EulerDiffusionStep()
+    audio = state.audio_tokens > 0
+    iso = modality_isolation_config()
+    for step in range(len(state.sigmas) - 1):
+        sigma = state.sigmas[step]
+        sig = state.sigmas_dev[step:step + 1]
+        x_v, x_a = state.video_latent, state.audio_latent
+
+        def den(v, a):
+            return to_denoised(x_v, v, sigma), (to_denoised(x_a, a, sigma) if audio else None)
+
+        cond_v, cond_a = den(*_velocities(model, state, sig, pes, state.video_context, state.audio_context))
+        uncond_v = uncond_a = 0.0
+        if video_guider.do_unconditional_generation() or audio_guider.do_unconditional_generation():
+            uncond_v, uncond_a = den(*_velocities(model, state, sig, pes, state.negative_video_context,
+                                                  state.negative_audio_context))
+        mod_v = mod_a = 0.0
+        if video_guider.do_isolated_modality_generation() or audio_guider.do_isolated_modality_generation():
+            mod_v, mod_a = den(*_velocities(model, state, sig, pes, state.video_context, state.audio_context,
+                                            perturbations=iso))
+        video_d = video_guider.calculate(cond_v, uncond_v, 0.0, mod_v)
+        stepper.step(x_v, video_d, state.sigmas, step, out=x_v)
+        if audio:
+            audio_d = audio_guider.calculate(cond_a, uncond_a, 0.0, mod_a)
+            stepper.step(x_a, audio_d, state.sigmas, step, out=x_a)
         if callback is not None:
             callback(step, state)
     return state

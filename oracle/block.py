@@ -115,34 +115,43 @@ def feed_forward(w: dict, x):
     return linear(h, w["w2"], w["b2"], w.get("w2_qlinear", False))
 
 
-def block(W: dict, vx, ax, v_ada, a_ada, vctx, actx, vpe, vxpe, ape, axpe, *, fused_adaln=False, eps=EPS):
+def block(W: dict, vx, ax, v_ada, a_ada, vctx, actx, vpe, vxpe, ape, axpe, *, fused_adaln=False, eps=EPS,
+          skips=frozenset()):
     """BasicAVTransformerBlock.__call__ (transformer.py:389-674) on 2-D
     streams; ``*_ada`` are the (16, D) modulation rows
-    [sst(9) | prompt(2) | av(5)] + timestep rows."""
+    [sst(9) | prompt(2) | av(5)] + timestep rows.  ``skips`` holds the
+    perturbation kinds applying to this block ("skip_video_self_attn",
+    "skip_audio_self_attn", "skip_a2v_cross_attn", "skip_v2a_cross_attn"):
+    the sub-layer's whole residual update is skipped (transformer.py:430-470,
+    :576-625)."""
     r = v_ada
     vh, ah = 32, 32
     if vx is not None:
-        h = adaln(vx, r[1], r[0], eps, fused_adaln)
-        vx = bf(vx + attention(W["attn1"], h, pe=vpe, heads=vh) * r[2])
+        if "skip_video_self_attn" not in skips:
+            h = adaln(vx, r[1], r[0], eps, fused_adaln)
+            vx = bf(vx + attention(W["attn1"], h, pe=vpe, heads=vh) * r[2])
         a = adaln(vx, r[7], r[6], eps)
         c = bf(vctx * (1 + r[10]) + r[9])
         vx = bf(vx + bf(attention(W["attn2"], a, c, heads=vh) * r[8]))
     if ax is not None:
         q = a_ada
-        h = adaln(ax, q[1], q[0], eps, fused_adaln)
-        ax = bf(ax + attention(W["audio_attn1"], h, pe=ape, heads=ah) * q[2])
+        if "skip_audio_self_attn" not in skips:
+            h = adaln(ax, q[1], q[0], eps, fused_adaln)
+            ax = bf(ax + attention(W["audio_attn1"], h, pe=ape, heads=ah) * q[2])
         a = adaln(ax, q[7], q[6], eps)
         c = bf(actx * (1 + q[10]) + q[9])
         ax = bf(ax + bf(attention(W["audio_attn2"], a, c, heads=ah) * q[8]))
     if vx is not None and ax is not None:
         vn, an = rms_norm_bf(vx, eps), rms_norm_bf(ax, eps)
         q = a_ada
-        vs = bf(vn * (1 + r[11]) + r[12])
-        as_ = bf(an * (1 + q[11]) + q[12])
-        vx = bf(vx + attention(W["audio_to_video_attn"], vs, as_, pe=vxpe, k_pe=axpe, heads=ah) * r[15])
-        as2 = bf(an * (1 + q[13]) + q[14])
-        vs2 = bf(vn * (1 + r[13]) + r[14])
-        ax = bf(ax + attention(W["video_to_audio_attn"], as2, vs2, pe=axpe, k_pe=vxpe, heads=ah) * q[15])
+        if "skip_a2v_cross_attn" not in skips:
+            vs = bf(vn * (1 + r[11]) + r[12])
+            as_ = bf(an * (1 + q[11]) + q[12])
+            vx = bf(vx + attention(W["audio_to_video_attn"], vs, as_, pe=vxpe, k_pe=axpe, heads=ah) * r[15])
+        if "skip_v2a_cross_attn" not in skips:
+            as2 = bf(an * (1 + q[13]) + q[14])
+            vs2 = bf(vn * (1 + r[13]) + r[14])
+            ax = bf(ax + attention(W["video_to_audio_attn"], as2, vs2, pe=axpe, k_pe=vxpe, heads=ah) * q[15])
     if vx is not None:
         h = adaln(vx, r[4], r[3], eps, fused_adaln)
         vx = bf(vx + feed_forward(W["ff"], h) * r[5])
@@ -192,10 +201,10 @@ def euler_x0(latent, velocity, sigma: float, sigma_next: float):
     return bf(x0 + ratio * (latent - x0))
 
 
-def model_step(MW: dict, vlat, alat, vctx, actx, sigma: float, sigma_next: float, pes, *, av_ca_mult=1000.0,
-               ts_mult=1000.0, eps=EPS):
-    """One distilled AV denoise step: LTXModel.__call__ (model.py:1344-1486)
-    + X0Model (:1489-1542) + Euler (diffusion_steps.py:58-69).
+def model_velocity(MW: dict, vlat, alat, vctx, actx, sigma: float, pes, *, av_ca_mult=1000.0, ts_mult=1000.0,
+                   eps=EPS, skips=None):
+    """LTXModel.__call__ (model.py:1344-1486): (video velocity, audio velocity)
+    bf16 values.  ``skips(block_index) -> set of perturbation kinds``.
 
     MW: {"patchify": (w, b), "audio_patchify": (w, b), "mlps_v": [4 mlp dicts],
     "mlps_a": [...], "tables_v": (L, 16, D), "tables_a": ..., "blocks": [block
@@ -218,11 +227,19 @@ def model_step(MW: dict, vlat, alat, vctx, actx, sigma: float, sigma_next: float
     for i, W in enumerate(MW["blocks"]):
         v_ada = MW["tables_v"][i] + tv
         a_ada = MW["tables_a"][i] + ta if ax is not None else None
-        vx, ax = block(W, vx, ax, v_ada, a_ada, vctx, actx, vpe, vxpe, ape, axpe, eps=eps)
+        vx, ax = block(W, vx, ax, v_ada, a_ada, vctx, actx, vpe, vxpe, ape, axpe, eps=eps,
+                       skips=frozenset() if skips is None else frozenset(skips(i)))
     vvel = output_head(vx, MW["sst_out_v"], emb_v, *MW["proj_out_v"], eps=eps)
+    avel = output_head(ax, MW["sst_out_a"], emb_a, *MW["proj_out_a"], eps=eps) if ax is not None else None
+    return vvel, avel
+
+
+def model_step(MW: dict, vlat, alat, vctx, actx, sigma: float, sigma_next: float, pes, *, av_ca_mult=1000.0,
+               ts_mult=1000.0, eps=EPS):
+    """One distilled AV denoise step: LTXModel.__call__ (model.py:1344-1486)
+    + X0Model (:1489-1542) + Euler (diffusion_steps.py:58-69)."""
+    vvel, avel = model_velocity(MW, vlat, alat, vctx, actx, sigma, pes, av_ca_mult=av_ca_mult, ts_mult=ts_mult,
+                                eps=eps)
     new_v = euler_x0(vlat, vvel, sigma, sigma_next)
-    new_a = None
-    if ax is not None:
-        avel = output_head(ax, MW["sst_out_a"], emb_a, *MW["proj_out_a"], eps=eps)
-        new_a = euler_x0(alat, avel, sigma, sigma_next)
+    new_a = euler_x0(alat, avel, sigma, sigma_next) if avel is not None else None
     return new_v, new_a

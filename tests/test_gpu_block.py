@@ -126,8 +126,8 @@ def test_av_block_quantised_weights(fmt):
 
 
 def test_block_contract_passthrough_and_skip():
-    from ltx_amd.model.transformer.transformer import (BasicAVTransformerBlock, BatchedPerturbationConfig,
-                                                        TransformerArgs)
+    from ltx_amd.components.perturbations import create_batched_stg_config
+    from ltx_amd.model.transformer.transformer import BasicAVTransformerBlock, TransformerArgs
 
     vcfg, acfg = _cfgs(True)
     blk = BasicAVTransformerBlock(5, vcfg, acfg)
@@ -143,8 +143,8 @@ def test_block_contract_passthrough_and_skip():
     assert ao is audio  # disabled modality passes through untouched
     # skipping every sub-layer that can be skipped leaves text CA + FF: the
     # output must differ from the input but equal a run with skips on both
-    pert = BatchedPerturbationConfig({"skip_video_self_attn": {5}})
+    pert = create_batched_stg_config(1, skip_video_self_attn=True, blocks=[5])
     vo2, _ = blk(video, None, perturbations=pert)
-    vo3, _ = blk(video, None, perturbations=BatchedPerturbationConfig({"skip_video_self_attn": {4}}))
+    vo3, _ = blk(video, None, perturbations=create_batched_stg_config(1, blocks=[4]))
     torch.cuda.synchronize()
     assert not torch.equal(vo2.x, vo3.x)
