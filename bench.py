@@ -22,6 +22,9 @@ Prints ONE JSON line.  Besides ms/step and tokens/s it carries:
                 reference's test shape (T=14640, C=4096) over a >512 MB buffer
                 rotation (no Infinity-Cache reuse), launches replayed from a
                 HIP graph (kernel time, not host dispatch);
+  guided_step   ms per step of the CFG/STG guided loop (three transformer
+                passes: positive, negative prompt, STG-perturbed; CFG-star and
+                STG guidance; Euler), eager launches;
   cpu_baseline  the oracle (CPU restatement of the reference block) timed on
                 this host for one AV block at the same shapes, x48.
 """
@@ -60,6 +63,8 @@ def parse_args(argv=None):
     ap.add_argument("--weights", choices=["bf16", "int8", "mxfp8"], default="mxfp8")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of HIP graph replay")
     ap.add_argument("--kernel-steps", type=int, default=2, help="eager steps for the dominant-kernel timing")
+    ap.add_argument("--guided-steps", type=int, default=3,
+                    help="also time this many CFG-star + STG guided steps (3 passes each, eager); 0 skips")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-fused-bench", action="store_true")
     ap.add_argument("--counter-workload", choices=["ff-up", "ff-up-vs-library", "copy"], default=None,
@@ -224,6 +229,38 @@ def cpu_baseline(tv: int, ta: int, s: int, layers: int, grid):
                       f"the reference's own MLX CPU backend is not installable here"}
 
 
+def guided_step_ms(model, args, ta: int, s: int) -> dict:
+    """ms per guided step of the CFG/STG loop (av_pipeline.py:625-757): the
+    positive, negative-prompt and STG-perturbed transformer passes, CFG-star
+    guidance (video 3.0, audio 7.0), STG (scale 1.0, video self-attention
+    skipped in every block), Euler; shifted LTX-2 sigma schedule; eager."""
+    import torch
+
+    from ltx_amd.components.guiders import CFGStarRescalingGuider, STGGuider
+    from ltx_amd.components.perturbations import create_batched_stg_config
+    from ltx_amd.components.schedulers import LTX2Scheduler
+    from ltx_amd.pipeline import DenoiseState, denoise_cfg_av
+
+    kw = dict(video_guider=CFGStarRescalingGuider(3.0), audio_guider=CFGStarRescalingGuider(7.0),
+              stg_guider=STGGuider(1.0), stg_perturbations=create_batched_stg_config(1, blocks=None))
+
+    def run(steps):
+        st = DenoiseState(model, args.height, args.width, args.frames, text_tokens=s, audio_frames=ta, seed=1,
+                          sigmas=LTX2Scheduler().execute(steps=steps))
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        denoise_cfg_av(model, st, **kw)
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
+    print(f"# guided loop: warmup + {args.guided_steps} steps", file=sys.stderr, flush=True)
+    run(1)
+    wall = run(args.guided_steps)
+    return {"ms_per_step": round(wall / args.guided_steps * 1e3, 3), "passes_per_step": 3,
+            "steps": args.guided_steps, "timing": "eager",
+            "loop": "denoise_cfg_av: CFG-star video 3.0 / audio 7.0 + STG 1.0 (all blocks), LTX2Scheduler sigmas"}
+
+
 def main(argv=None):
     args = parse_args(argv)
     if args.gpus != 1:
@@ -325,8 +362,11 @@ def main(argv=None):
         "gemm_mfma_pct": round(100 * achieved / PEAK_BF16_TFLOPS, 1),
         "roofline": roofline,
     }
-    if not args.no_fused_bench:
+    if not args.no_fused_bench or args.guided_steps > 0:
         del graphs
+    if args.guided_steps > 0:
+        out["guided_step"] = guided_step_ms(model, args, ta, s)
+    if not args.no_fused_bench:
         out["fused_ops"] = fused_op_bandwidth(torch)
     if not args.no_cpu_baseline:
         sys.path.insert(0, str(ROOT))

@@ -300,6 +300,16 @@ int ltx_ge_correct_f32(const void* latent, float* denoised, float* prev_velocity
 int ltx_euler_step_bf16(const void* sample, const float* denoised, float ratio, void* out, int64_t n,
                         void* stream);
 
+/* ---- latent layouts ------------------------------------------------------------
+ * Swap of the two outer axes of an (A, B, R) array, out[b, a, r] = in[a, b, r],
+ * for 2- or 4-byte elements; out must not alias in.  The reference's
+ * patchifiers at batch 1 (components/patchifiers.py:52-124, :327-374):
+ *   video patchify   (C, F*H*W, 1) -> (F*H*W, C, 1)   unpatchify: the inverse swap
+ *   audio patchify   (C, T, M)     -> (T, C, M)       unpatchify: the inverse swap
+ */
+int ltx_swap_axes(const void* in, int64_t A, int64_t B, int64_t R, int elem_bytes, void* out,
+                  void* stream);
+
 /* ---- attention ---------------------------------------------------------------
  * Flash attention with the per-head output gate fused (replaces
  * attention.py:283-302 -> kernels/steel_attention.py:251-280 and the gate of

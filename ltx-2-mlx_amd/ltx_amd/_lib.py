@@ -55,6 +55,7 @@ SIGNATURES: dict[str, list] = {
     "ltx_guidance_stats_f32": [_vp, _vp, _i64, _int, _f32, _f32, _vp, _vp],
     "ltx_ge_correct_f32": [_vp, _vp, _vp, _int, _f32, _f32, _i64, _vp],
     "ltx_euler_step_bf16": [_vp, _vp, _f32, _vp, _i64, _vp],
+    "ltx_swap_axes": [_vp, _i64, _i64, _i64, _int, _vp, _vp],
 }
 
 # Flag values (include/ltx_hip.h)

@@ -13,6 +13,11 @@
   pipelines/two_stage.py:306-388: conditioned, unconditioned and
   modality-isolated passes combined by ``MultiModalGuider``.
 
+``set_latents`` / ``get_latents`` convert between the VAE latent layouts and
+the token rows (the patchifiers); ``save_final_latents``,
+``save_distilled_two_stage_latents`` and ``load_stage1_latents`` read and
+write the reference's latent sidecars.
+
 The sigma schedule lives on the device for the whole loop, RoPE tables are
 built once per stage, and a step enqueues its kernels without host
 synchronisation (the reference's one per-step barrier, av_pipeline.py:1113,
@@ -41,6 +46,7 @@ class DenoiseState:
                  sigmas=DISTILLED_SIGMA_VALUES):
         dev = model.device
         f, h, w = video_latent_grid(height, width, frames)
+        self.grid = (f, h, w)
         self.video_tokens = f * h * w
         self.audio_tokens = audio_latent_frames(frames, fps) if audio_frames is None else audio_frames
         if model.audio_config is None:
@@ -63,6 +69,93 @@ class DenoiseState:
                                                   device=dev).to(torch.bfloat16)
         self.negative_audio_context = torch.randn((text_tokens, model.audio_dim), generator=neg,
                                                   device=dev).to(torch.bfloat16)
+
+
+def set_latents(state: DenoiseState, video_latent: torch.Tensor, audio_latent: torch.Tensor | None = None) -> None:
+    """Start ``state`` from given latents in the VAE layouts -- video (1, 128,
+    F, H, W), audio (1, 8, T, 16) -- patchified into the token rows (e.g. a
+    stage-1 result read with ``load_stage1_latents``)."""
+    from .components.patchifiers import AudioPatchifier, VideoLatentPatchifier
+
+    f, h, w = state.grid
+    if tuple(video_latent.shape[2:]) != (f, h, w) or video_latent.shape[1] != 128:
+        raise ValueError(f"video latent {tuple(video_latent.shape)} does not fit the grid {(f, h, w)}")
+    v = VideoLatentPatchifier(1).patchify(video_latent.to(state.video_latent.device, torch.bfloat16))
+    state.video_latent.copy_(v[0])
+    if audio_latent is not None:
+        if state.audio_tokens != audio_latent.shape[2]:
+            raise ValueError(f"audio latent {tuple(audio_latent.shape)} has {audio_latent.shape[2]} frames, "
+                             f"the state {state.audio_tokens}")
+        a = AudioPatchifier(1).patchify(audio_latent.to(state.audio_latent.device, torch.bfloat16))
+        state.audio_latent.copy_(a[0])
+
+
+def get_latents(state: DenoiseState) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """The state's latents unpatchified: video (1, 128, F, H, W), audio
+    (1, 8, T, 16) or None."""
+    from .components.patchifiers import (AUDIO_LATENT_CHANNELS, AUDIO_MEL_BINS, AudioPatchifier,
+                                         VideoLatentPatchifier)
+
+    f, h, w = state.grid
+    video = VideoLatentPatchifier(1).unpatchify(state.video_latent[None], (128, f, h, w))
+    audio = None
+    if state.audio_tokens:
+        audio = AudioPatchifier(1).unpatchify(state.audio_latent[None],
+                                              (AUDIO_LATENT_CHANNELS, state.audio_tokens, AUDIO_MEL_BINS))
+    return video, audio
+
+
+def save_final_latents(path: str, video_latent: torch.Tensor, audio_latent: torch.Tensor | None = None) -> str:
+    """``final_video_latent`` / ``final_audio_latent`` sidecar
+    (av_pipeline.py:233-253); returns the path written."""
+    from .sidecars import save_sidecar
+
+    arrays = {"final_video_latent": video_latent}
+    if audio_latent is not None:
+        arrays["final_audio_latent"] = audio_latent
+    return save_sidecar(path, arrays)
+
+
+def save_distilled_two_stage_latents(path: str, stage_1_video_latent: torch.Tensor,
+                                     stage_2_video_latent: torch.Tensor,
+                                     stage_1_audio_latent: torch.Tensor | None = None,
+                                     stage_2_audio_latent: torch.Tensor | None = None) -> str:
+    """Both distilled stages plus the final-latent keys (av_pipeline.py:255-290)."""
+    from .sidecars import save_sidecar
+
+    arrays = {"stage_1_video_latent": stage_1_video_latent, "stage_2_video_latent": stage_2_video_latent,
+              "final_video_latent": stage_2_video_latent}
+    if stage_1_audio_latent is not None:
+        arrays["stage_1_audio_latent"] = stage_1_audio_latent
+    if stage_2_audio_latent is not None:
+        arrays["stage_2_audio_latent"] = stage_2_audio_latent
+        arrays["final_audio_latent"] = stage_2_audio_latent
+    return save_sidecar(path, arrays, metadata={"pipeline": "distilled_two_stage"})
+
+
+def load_stage1_latents(path: str, device: str | torch.device = "cpu"):
+    """``(video, audio or None, metadata)`` of a two-stage sidecar
+    (scripts/stage2_harness.py:56-74)."""
+    from .sidecars import load_sidecar
+
+    arrays, file_metadata = load_sidecar(path, device=device)
+    if "stage_1_video_latent" not in arrays:
+        raise ValueError(f"{path} does not contain stage_1_video_latent. "
+                         "Use a distilled two-stage latent sidecar saved with --save-latents.")
+    video = arrays["stage_1_video_latent"]
+    audio = arrays.get("stage_1_audio_latent")
+    metadata = {"pipeline": file_metadata.get("pipeline"), "video_shape": tuple(video.shape),
+                "audio_shape": tuple(audio.shape) if audio is not None else None}
+    return video, audio, metadata
+
+
+def infer_dimensions_from_stage1(video_latent: torch.Tensor) -> tuple[int, int, int]:
+    """(height, width, frames) of the full-resolution output of a stage-1
+    latent (half resolution, scripts/stage2_harness.py:77-85)."""
+    if video_latent.dim() != 5:
+        raise ValueError(f"stage_1_video_latent must be 5D (B,C,F,H,W), got shape {tuple(video_latent.shape)}")
+    frames = (video_latent.shape[2] - 1) * 8 + 1
+    return video_latent.shape[3] * 64, video_latent.shape[4] * 64, frames
 
 
 def denoise_step(model: LTXModel, state: DenoiseState, step: int, pes=None,
