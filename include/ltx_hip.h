@@ -300,6 +300,22 @@ int ltx_ge_correct_f32(const void* latent, float* denoised, float* prev_velocity
 int ltx_euler_step_bf16(const void* sample, const float* denoised, float ratio, void* out, int64_t n,
                         void* stream);
 
+/* ---- text-conditioning features ------------------------------------------------
+ * GemmaFeaturesExtractorV2 normalisation (model/text_encoder/feature_extractor.py:
+ * 9-79) for `layers` Gemma hidden states of `tokens` x `dim` bf16 (layer l,
+ * token t at hidden + l*layer_stride + t*row_stride), in the reference's bf16
+ * arithmetic:  y = mask[t] ? bf16(x * bf16(1/sqrt(bf16(bf16(mean(bf16(x*x))) + eps)))) : 0,
+ *   out_video[t, l*dim + d] = bf16(y * scale_video),  out_audio likewise,
+ * eps / scales given as their bf16 values (python floats meeting bf16 arrays).
+ * Output rows (tokens, layers*dim) are layer-major; the aggregate-embedding
+ * weights are permuted to match (the reference's feature index is d*layers + l).
+ * mask: int32 (tokens), nonzero keeps the token; NULL keeps all.
+ */
+int ltx_gemma_features_bf16(const void* hidden, int64_t layers, int64_t tokens, int64_t dim,
+                            int64_t layer_stride, int64_t row_stride, const int32_t* mask, float eps,
+                            float scale_video, float scale_audio, void* out_video, void* out_audio,
+                            int64_t out_stride, void* stream);
+
 /* ---- latent layouts ------------------------------------------------------------
  * Swap of the two outer axes of an (A, B, R) array, out[b, a, r] = in[a, b, r],
  * for 2- or 4-byte elements; out must not alias in.  The reference's

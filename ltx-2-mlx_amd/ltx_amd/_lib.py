@@ -56,6 +56,7 @@ SIGNATURES: dict[str, list] = {
     "ltx_ge_correct_f32": [_vp, _vp, _vp, _int, _f32, _f32, _i64, _vp],
     "ltx_euler_step_bf16": [_vp, _vp, _f32, _vp, _i64, _vp],
     "ltx_swap_axes": [_vp, _i64, _i64, _i64, _int, _vp, _vp],
+    "ltx_gemma_features_bf16": [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _f32, _f32, _f32, _vp, _vp, _i64, _vp],
 }
 
 # Flag values (include/ltx_hip.h)

@@ -393,6 +393,7 @@ class _MatrixJob:
     owner: object
     attr: str
     rec: LinearRecord
+    transform: object = None  # optional layout change applied to the loaded (N, K) bf16 matrix
 
 
 @dataclass
@@ -450,7 +451,7 @@ class _Planner:
             else:
                 self.plan.jobs.append(_LinearJob(owner, attr, recs, bias_keys, forced))
 
-    def matrix(self, owner, attr: str, base: str):
+    def matrix(self, owner, attr: str, base: str, transform=None):
         rec = self.src.linear(base)
         if rec is None:
             self.plan.missing.append(base + ".weight")
@@ -465,7 +466,7 @@ class _Planner:
         elif rec.quantized:
             self.plan.errors.append(f"{base}.weight: quantised, the model keeps it bf16")
         else:
-            self.plan.jobs.append(_MatrixJob(owner, attr, rec))
+            self.plan.jobs.append(_MatrixJob(owner, attr, rec, transform))
 
     def vector(self, dst: torch.Tensor, name: str):
         key = self.src.tensor_key(name)
@@ -597,6 +598,21 @@ def _run_linear(job: _LinearJob, src: WeightSource, weight_format: str | None, d
     setattr(job.owner, job.attr, gemm.LinearWeight(target, w, scale, bias, qlinear=qlinear))
 
 
+def run_plan(plan: _Plan, src: WeightSource, weight_format: str | None, device) -> None:
+    """Execute a checked plan: fill every resident tensor from the source."""
+    device = torch.device(device)
+    for job in plan.jobs:
+        if isinstance(job, _LinearJob):
+            _run_linear(job, src, weight_format, device)
+        elif isinstance(job, _MatrixJob):
+            getattr(job.owner, job.attr).copy_(job.transform(src.load_bf16(job.rec, device))
+                                               if job.transform else src.load_bf16(job.rec, device))
+        else:
+            job.dst.copy_(src.load_f32(job.key, device).reshape(job.dst.shape))
+    if device.type == "cuda":
+        torch.cuda.synchronize(device)
+
+
 def install_weights(model, src: WeightSource, *, weight_format: str | None = None,
                     strict: bool = True) -> InstallCounts:
     """Load every tensor of ``model`` from ``src`` (see the module docstring)."""
@@ -614,16 +630,7 @@ def install_weights(model, src: WeightSource, *, weight_format: str | None = Non
         raise ValueError(f"{len(plan.missing)} tensors missing, e.g. " + ", ".join(plan.missing[:8]))
     if strict and extra:
         raise ValueError(f"{len(extra)} tensors have no place in the model, e.g. " + ", ".join(extra[:8]))
-    device = model.device
-    for job in plan.jobs:
-        if isinstance(job, _LinearJob):
-            _run_linear(job, src, weight_format, device)
-        elif isinstance(job, _MatrixJob):
-            getattr(job.owner, job.attr).copy_(src.load_bf16(job.rec, device))
-        else:
-            job.dst.copy_(src.load_f32(job.key, device).reshape(job.dst.shape))
-    if device.type == "cuda":
-        torch.cuda.synchronize(device)
+    run_plan(plan, src, weight_format, model.device)
     used = plan.consumed
     return InstallCounts(loaded=len(used), layout=sum(k.startswith(LAYOUT_KEY_PREFIX) for k in used),
                          quant=sum(k.startswith(QUANT_KEY_PREFIX) for k in used))

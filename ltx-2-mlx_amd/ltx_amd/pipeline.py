@@ -16,7 +16,9 @@
 ``set_latents`` / ``get_latents`` convert between the VAE latent layouts and
 the token rows (the patchifiers); ``save_final_latents``,
 ``save_distilled_two_stage_latents`` and ``load_stage1_latents`` read and
-write the reference's latent sidecars.
+write the reference's latent sidecars; ``load_text_conditioning`` /
+``set_contexts`` bring real text contexts (a conditioning sidecar or the
+connector's output) into a state.
 
 The sigma schedule lives on the device for the whole loop, RoPE tables are
 built once per stage, and a step enqueues its kernels without host
@@ -156,6 +158,44 @@ def infer_dimensions_from_stage1(video_latent: torch.Tensor) -> tuple[int, int, 
         raise ValueError(f"stage_1_video_latent must be 5D (B,C,F,H,W), got shape {tuple(video_latent.shape)}")
     frames = (video_latent.shape[2] - 1) * 8 + 1
     return video_latent.shape[3] * 64, video_latent.shape[4] * 64, frames
+
+
+def load_text_conditioning(path: str, device: str | torch.device = "cpu") -> dict:
+    """The text-conditioning sidecar of a run (generate.py:1531-1560): the
+    ``positive_video_encoding`` / ``negative_*`` / ``*_audio_encoding`` and
+    attention masks, or a legacy ``embedding`` + ``attention_mask`` file."""
+    from .sidecars import load_sidecar
+
+    arrays, _ = load_sidecar(path, device=device)
+    if "positive_video_encoding" not in arrays:
+        return {"format": "legacy", "positive_video_encoding": arrays["embedding"],
+                "positive_attention_mask": arrays["attention_mask"], "negative_video_encoding": None,
+                "negative_attention_mask": None, "positive_audio_encoding": None, "negative_audio_encoding": None}
+    keys = ("positive_video_encoding", "positive_attention_mask", "negative_video_encoding", "negative_attention_mask",
+            "positive_audio_encoding", "negative_audio_encoding")
+    out = {"format": "text_conditioning"}
+    out.update({k: arrays.get(k) for k in keys})
+    return out
+
+
+def set_contexts(state: DenoiseState, video_context: torch.Tensor, audio_context: torch.Tensor | None = None,
+                 negative_video_context: torch.Tensor | None = None,
+                 negative_audio_context: torch.Tensor | None = None) -> None:
+    """Replace the state's text contexts ((1, S, D) or (S, D), any S) -- e.g.
+    the connector's output or a loaded text-conditioning sidecar."""
+    dev = state.video_latent.device
+
+    def two_d(t):
+        t = t[0] if t.dim() == 3 else t
+        return t.to(device=dev, dtype=torch.bfloat16).contiguous()
+
+    state.video_context = two_d(video_context)
+    if audio_context is not None:
+        state.audio_context = two_d(audio_context)
+    if negative_video_context is not None:
+        state.negative_video_context = two_d(negative_video_context)
+    if negative_audio_context is not None:
+        state.negative_audio_context = two_d(negative_audio_context)
 
 
 def denoise_step(model: LTXModel, state: DenoiseState, step: int, pes=None,

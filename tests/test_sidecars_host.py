@@ -92,3 +92,23 @@ def test_stage_sidecars(tmp_path):
         pl.load_stage1_latents(final)
     with pytest.raises(ValueError, match="must be 5D"):
         pl.infer_dimensions_from_stage1(v2[0])
+
+
+def test_text_conditioning_sidecars(tmp_path):
+    from ltx_amd import pipeline as pl
+    from ltx_amd.sidecars import save_sidecar
+
+    pv, nv = torch.randn(1, 1024, 64).bfloat16(), torch.randn(1, 1024, 64).bfloat16()
+    pa = torch.randn(1, 1024, 32).bfloat16()
+    m = torch.ones(1, 1024, dtype=torch.int32)
+    p = save_sidecar(str(tmp_path / "run_text"), {"schema_version": torch.tensor(1, dtype=torch.int32),
+                                                  "positive_video_encoding": pv, "positive_attention_mask": m,
+                                                  "negative_video_encoding": nv, "positive_audio_encoding": pa},
+                     {"prompt": "p", "negative_prompt": ""})
+    c = pl.load_text_conditioning(p)
+    assert c["format"] == "text_conditioning" and torch.equal(c["positive_video_encoding"], pv)
+    assert c["negative_audio_encoding"] is None and torch.equal(c["positive_audio_encoding"], pa)
+    legacy = save_sidecar(str(tmp_path / "emb"), {"embedding": pv, "attention_mask": m})
+    c = pl.load_text_conditioning(legacy)
+    assert c["format"] == "legacy" and torch.equal(c["positive_video_encoding"], pv)
+    assert c["positive_audio_encoding"] is None
