@@ -219,6 +219,33 @@ int ltx_gemm_mxfp8_bf16(const void* A, int64_t lda, const uint8_t* Wq, int64_t l
                         const void* residual, int64_t ldr, const float* gate, int64_t sigmoid_from,
                         void* stream);
 
+/* Split-K forms of the three GEMMs for few-row products (the 68-token audio
+ * stream, 256-token contexts): `splits` blocks per 128x128 output tile each
+ * accumulate K / splits of the product into an fp32 partial tile in
+ * `workspace` (ltx_gemm_splitk_workspace_bytes(M, N, splits) bytes, 16-byte
+ * aligned, caller-owned), then one pass sums the partials in split order and
+ * applies the epilogue of the single-pass kernel (same flags, same rounding
+ * points; the fp32 sum order differs).  K % (64 * splits) == 0 (MXFP8:
+ * K % (128 * splits) == 0), 1 <= splits <= 64, tile override 0 or
+ * LTX_GEMM_TILE_128.  Same operand rules as above.
+ */
+int64_t ltx_gemm_splitk_workspace_bytes(int64_t M, int64_t N, int64_t splits);
+int ltx_gemm_splitk_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, const float* bias,
+                         void* C, int64_t ldc, int64_t M, int64_t N, int64_t K, int epilogue,
+                         const void* residual, int64_t ldr, const float* gate, int64_t sigmoid_from,
+                         int splits, float* workspace, int64_t workspace_bytes, void* stream);
+int ltx_gemm_splitk_w8a16_bf16(const void* A, int64_t lda, const int8_t* Wq, int64_t ldw,
+                               const float* w_scale, const float* bias, void* C, int64_t ldc,
+                               int64_t M, int64_t N, int64_t K, int epilogue, const void* residual,
+                               int64_t ldr, const float* gate, int64_t sigmoid_from, int splits,
+                               float* workspace, int64_t workspace_bytes, void* stream);
+int ltx_gemm_splitk_mxfp8_bf16(const void* A, int64_t lda, const uint8_t* Wq, int64_t ldw,
+                               const uint8_t* w_scale, int64_t ld_scale, const float* bias, void* C,
+                               int64_t ldc, int64_t M, int64_t N, int64_t K, int epilogue,
+                               const void* residual, int64_t ldr, const float* gate,
+                               int64_t sigmoid_from, int splits, float* workspace,
+                               int64_t workspace_bytes, void* stream);
+
 /* ---- weight formats (load-time) --------------------------------------------
  * MXFP8, OCP Microscaling v1.0 with E4M3 elements, blocks of 32 along K and an
  * E8M0 scale (the storage of loader/transformer_cache.py:1255-1267; codes (N,K)

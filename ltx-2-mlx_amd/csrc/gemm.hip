@@ -69,11 +69,15 @@ struct GemmArgs {
   const float* gate;   // fp32 (N)
   int sig_from;        // columns n >= sig_from get the 2*sigmoid head-gate epilogue
   int round_then_bias; // bias added to the bf16-rounded product (quantised-linear form)
-  int M, N, K;
+  float* partial;      // split-K: fp32 partial products [split][M][ldc], no epilogue
+  int M, N, K;         // split-K: K is the per-split depth
   int tiles_m, tiles_n;
 };
 
 constexpr int kGemmThreads = 256;
+// EPI value of the split-K pass: the accumulators go to the fp32 partial
+// buffer as they are, the epilogue runs in splitk_epilogue_kernel.
+constexpr int kEpiPartial = 16;
 constexpr int kGroupM = 4;
 constexpr int kNumXcd = 8;
 
@@ -204,9 +208,16 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
   const int wm = wave >> 1, wn = wave & 1;
 
   int tmi, tni;
-  tile_coords(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, tmi, tni);
+  // split-K: block b works on split b / tiles of tile b % tiles, the split's
+  // k range starting at kz * K
+  constexpr bool PARTIAL = EPI == kEpiPartial;
+  const int tiles = p.tiles_m * p.tiles_n;
+  const int kz = PARTIAL ? (int)blockIdx.x / tiles : 0;
+  tile_coords(PARTIAL ? (int)blockIdx.x % tiles : (int)blockIdx.x, PARTIAL ? tiles : (int)gridDim.x,
+              p.tiles_m, p.tiles_n, tmi, tni);
   const int m0 = tmi * BM, n0 = tni * BN;
   const int KT = p.K / BK;
+  const int64_t k0 = (int64_t)kz * p.K;
 
   // The epilogue's per-column vectors (bias; gate of the residual forms) are
   // loaded once here, one column per thread, and reach the epilogue through
@@ -230,7 +241,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
     int gm = m0 + r;
     gm = gm < p.M ? gm : p.M - 1;
     const int chunk = (lane % A_LPR) ^ chunk_xor<A_ROWB, SWZ>(r);
-    a_src[i] = (const char*)(p.A + (int64_t)gm * p.lda) + chunk * 16;
+    a_src[i] = (const char*)(p.A + (int64_t)gm * p.lda + k0) + chunk * 16;
   }
   const char* b_src[B_DMA];
   int b_dst[B_CONV ? B_DMA : 1];            // loader dequant: LDS byte offset of the row
@@ -244,7 +255,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
       const int chunk = (lane % B_LPR) ^ chunk_xor<B_ROWB, SWZ>(r);
       int gn = n0 + r;
       gn = gn < p.N ? gn : p.N - 1;
-      b_src[i] = (const char*)p.B + (int64_t)gn * p.ldb * (B8 ? 1 : 2) + chunk * 16;
+      b_src[i] = (const char*)p.B + ((int64_t)gn * p.ldb + k0) * (B8 ? 1 : 2) + chunk * 16;
     } else {
       // 64-byte code rows, 16 per wave instruction: lane -> row +lane/4,
       // codes 16*(lane%4) .. +16 (no swizzle: it applies to the bf16 writes)
@@ -253,8 +264,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
       gn = gn < p.N ? gn : p.N - 1;
       b_c16[i] = lane & 3;
       b_dst[i] = r * B_ROWB;
-      b_src[i] = (const char*)p.B + (int64_t)gn * p.ldb + b_c16[i] * 16;
-      if (BKIND == B_MXFP8) b_scr[i] = (const uint8_t*)p.bscale + (int64_t)gn * p.ld_scale;
+      b_src[i] = (const char*)p.B + (int64_t)gn * p.ldb + k0 + b_c16[i] * 16;
+      if (BKIND == B_MXFP8) b_scr[i] = (const uint8_t*)p.bscale + (int64_t)gn * p.ld_scale + k0 / 32;
       if (BKIND == B_INT8) b_s8[i] = ((const float*)p.bscale)[gn];
     }
   }
@@ -269,7 +280,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
     int gn = n0 + wn * WN + j * 32 + frag_r;
     gn = gn < p.N ? gn : p.N - 1;
     if (B_RAW && BKIND == B_INT8) s_i8[j] = ((const float*)p.bscale)[gn];
-    if (B_RAW && BKIND == B_MXFP8) sc_row[j] = (const uint8_t*)p.bscale + (int64_t)gn * p.ld_scale;
+    if (B_RAW && BKIND == B_MXFP8) sc_row[j] = (const uint8_t*)p.bscale + (int64_t)gn * p.ld_scale + k0 / 32;
   }
   // MXFP8 scales of one stage: 2 E8M0 bytes (k blocks 0/1 of the 64) per row.
   uint32_t sc_cur[TN], sc_next[TN];
@@ -606,6 +617,25 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
   __builtin_amdgcn_sched_barrier(0);
   mfmas(fa[LASTF], fb[LASTF], KSTEPS - 1);
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (PARTIAL) {
+    // acc[i][j] reg 4g+e holds C[m][n], m = i*32 + lane%32, n = j*32 + 8g +
+    // 4*(lane/32) + e (wave-local): four consecutive columns per store
+    float* P = p.partial + (int64_t)kz * p.M * p.ldc;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int gm = m0 + wm * WM + i * 32 + frag_r;
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int gn = n0 + wn * WN + j * 32 + 8 * g + 4 * frag_c;
+          if (gm < p.M && gn < p.N)
+            *reinterpret_cast<f32x4*>(P + (int64_t)gm * p.ldc + gn) =
+                f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+        }
+    }
+    return;
+  }
   wait_vmcnt<0>();  // the re-read stages land before the epilogue reuses LDS
   if (tid < BN) {
     col_lds[tid] = col_bias;
@@ -753,6 +783,105 @@ static int launch_kind(const GemmArgs& p, int epilogue, hipStream_t s) {
   return ltx_launch_status();
 }
 
+// ---- split-K ---------------------------------------------------------------
+// Few-row products (the 68-token audio stream, the 256-token text contexts)
+// give too few output tiles to fill 256 CUs, and each tile's K loop is a
+// serial latency chain.  Split-K runs `splits` K ranges as separate blocks
+// writing fp32 partial tiles; this kernel sums them in a fixed order (so the
+// result is deterministic) and applies the same epilogue as the single-pass
+// kernel's phases 1 and 2, eight columns per thread.
+template <int EPI>
+__global__ __launch_bounds__(256) void splitk_epilogue_kernel(GemmArgs p, int splits) {
+  constexpr bool RESID = EPI == LTX_GEMM_EPI_RESIDUAL || EPI == LTX_GEMM_EPI_RESIDUAL_ROUND;
+  const int nvec = p.N / 8;
+  const int64_t total = (int64_t)p.M * nvec;
+  const int64_t plane = (int64_t)p.M * p.N;
+  const bool rtb = p.round_then_bias != 0;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int m = (int)(idx / nvec);
+    const int n = (int)(idx % nvec) * 8;
+    float a[8];
+    {
+      const float* P = p.partial + (int64_t)m * p.N + n;
+      const f32x4 x0 = *reinterpret_cast<const f32x4*>(P);
+      const f32x4 x1 = *reinterpret_cast<const f32x4*>(P + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        a[e] = x0[e];
+        a[4 + e] = x1[e];
+      }
+      for (int z = 1; z < splits; ++z) {
+        const f32x4 y0 = *reinterpret_cast<const f32x4*>(P + z * plane);
+        const f32x4 y1 = *reinterpret_cast<const f32x4*>(P + z * plane + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          a[e] += y0[e];
+          a[4 + e] += y1[e];
+        }
+      }
+    }
+    bf16x8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float b = p.bias ? p.bias[n + e] : 0.0f;
+      float y = (rtb ? round_bf(a[e]) : a[e]) + b;
+      if (EPI == LTX_GEMM_EPI_GELU) y = gelu_tanh(round_bf(y));
+      if (EPI == LTX_GEMM_EPI_SIGMOID2) y = sigmoid2_bf(round_bf(y));
+      if (EPI == LTX_GEMM_EPI_BIAS && n + e >= p.sig_from) y = sigmoid2_bf(round_bf(y));
+      v[e] = (bf16)y;
+    }
+    if constexpr (RESID) {
+      const bf16x8 r = *reinterpret_cast<const bf16x8*>(p.R + (int64_t)m * p.ldr + n);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float y = (float)v[e], g = p.gate[n + e];
+        const float o = EPI == LTX_GEMM_EPI_RESIDUAL ? fmaf(g, y, (float)r[e]) : round_bf(y * g) + (float)r[e];
+        v[e] = (bf16)o;
+      }
+    }
+    *reinterpret_cast<bf16x8*>(p.C + (int64_t)m * p.ldc + n) = v;
+  }
+}
+
+template <int BKIND>
+static int launch_splitk(const GemmArgs& p0, int epilogue, int splits, float* workspace, hipStream_t s) {
+  const int epi = epilogue & 0xff;
+  const int tile = (epilogue >> 8) & 0xf;
+  if (tile != 0 && tile != 2) return LTX_ERR_UNSUPPORTED;  // 128x128 register-staged tiles
+  GemmArgs p = p0;
+  p.round_then_bias = (epilogue & LTX_GEMM_ROUND_THEN_BIAS) != 0;
+  // pass 1: partial products, per-split depth K / splits, row stride N
+  GemmArgs q = p;
+  q.K = p.K / splits;
+  q.partial = workspace;
+  q.ldc = p.N;
+  q.tiles_m = (p.M + 127) / 128;
+  q.tiles_n = (p.N + 127) / 128;
+  gemm_kernel<128, 128, 64, 2, BKIND, kEpiPartial, 0, LOAD_REG>
+      <<<q.tiles_m * q.tiles_n * splits, kGemmThreads, 0, s>>>(q);
+  // pass 2: sum + epilogue
+  p.partial = workspace;
+  const int64_t vecs = (int64_t)p.M * (p.N / 8);
+  int blocks = (int)((vecs + 255) / 256);
+  if (blocks > 4096) blocks = 4096;
+  switch (epi) {
+    case LTX_GEMM_EPI_BIAS: splitk_epilogue_kernel<LTX_GEMM_EPI_BIAS><<<blocks, 256, 0, s>>>(p, splits); break;
+    case LTX_GEMM_EPI_GELU: splitk_epilogue_kernel<LTX_GEMM_EPI_GELU><<<blocks, 256, 0, s>>>(p, splits); break;
+    case LTX_GEMM_EPI_RESIDUAL:
+      splitk_epilogue_kernel<LTX_GEMM_EPI_RESIDUAL><<<blocks, 256, 0, s>>>(p, splits);
+      break;
+    case LTX_GEMM_EPI_RESIDUAL_ROUND:
+      splitk_epilogue_kernel<LTX_GEMM_EPI_RESIDUAL_ROUND><<<blocks, 256, 0, s>>>(p, splits);
+      break;
+    case LTX_GEMM_EPI_SIGMOID2:
+      splitk_epilogue_kernel<LTX_GEMM_EPI_SIGMOID2><<<blocks, 256, 0, s>>>(p, splits);
+      break;
+    default: return LTX_ERR_INVALID_ARG;
+  }
+  return ltx_launch_status();
+}
+
 }  // namespace ltx
 
 using namespace ltx;
@@ -795,6 +924,7 @@ static GemmArgs make_args(const void* A, int64_t lda, const void* B, int64_t ldb
   p.gate = gate;
   p.sig_from = (int)(sigmoid_from < N ? (sigmoid_from < 0 ? 0 : sigmoid_from) : N);
   p.round_then_bias = 0;
+  p.partial = nullptr;
   p.M = (int)M;
   p.N = (int)N;
   p.K = (int)K;
@@ -844,4 +974,66 @@ extern "C" int ltx_gemm_mxfp8_bf16(const void* A, int64_t lda, const uint8_t* Wq
   GemmArgs p = make_args(A, lda, Wq, ldw, w_scale, ld_scale, bias, C, ldc, M, N, K, residual, ldr,
                          gate, sigmoid_from);
   return launch_kind<B_MXFP8>(p, epilogue, (hipStream_t)stream);
+}
+
+// ---- split-K entry points ------------------------------------------------------
+extern "C" int64_t ltx_gemm_splitk_workspace_bytes(int64_t M, int64_t N, int64_t splits) {
+  if (M < 0 || N < 0 || splits < 1) return -1;
+  return splits * M * N * 4;
+}
+
+static int splitk_check(int64_t M, int64_t N, int64_t K, int splits, const float* workspace,
+                        int64_t workspace_bytes) {
+  if (splits < 1 || splits > 64) return LTX_ERR_INVALID_ARG;
+  if (K % (64 * (int64_t)splits)) return LTX_ERR_UNSUPPORTED;
+  if (!workspace || workspace_bytes < ltx_gemm_splitk_workspace_bytes(M, N, splits)) return LTX_ERR_INVALID_ARG;
+  if (!al16(workspace)) return LTX_ERR_ALIGNMENT;
+  return LTX_OK;
+}
+
+extern "C" int ltx_gemm_splitk_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, const float* bias,
+                                    void* C, int64_t ldc, int64_t M, int64_t N, int64_t K, int epilogue,
+                                    const void* residual, int64_t ldr, const float* gate, int64_t sigmoid_from,
+                                    int splits, float* workspace, int64_t workspace_bytes, void* stream) {
+  int st = gemm_check(A, lda, W, ldw, C, ldc, M, N, K, epilogue, residual, ldr, gate, 2);
+  if (st != LTX_OK) return st;
+  if (M == 0 || N == 0) return LTX_OK;
+  if (K == 0) return LTX_ERR_UNSUPPORTED;
+  if ((st = splitk_check(M, N, K, splits, workspace, workspace_bytes)) != LTX_OK) return st;
+  GemmArgs p = make_args(A, lda, W, ldw, nullptr, 0, bias, C, ldc, M, N, K, residual, ldr, gate, sigmoid_from);
+  return launch_splitk<B_BF16>(p, epilogue, splits, workspace, (hipStream_t)stream);
+}
+
+extern "C" int ltx_gemm_splitk_w8a16_bf16(const void* A, int64_t lda, const int8_t* Wq, int64_t ldw,
+                                          const float* w_scale, const float* bias, void* C, int64_t ldc,
+                                          int64_t M, int64_t N, int64_t K, int epilogue, const void* residual,
+                                          int64_t ldr, const float* gate, int64_t sigmoid_from, int splits,
+                                          float* workspace, int64_t workspace_bytes, void* stream) {
+  int st = gemm_check(A, lda, Wq, ldw, C, ldc, M, N, K, epilogue, residual, ldr, gate, 1);
+  if (st != LTX_OK) return st;
+  if (!w_scale) return LTX_ERR_INVALID_ARG;
+  if (M == 0 || N == 0) return LTX_OK;
+  if (K == 0) return LTX_ERR_UNSUPPORTED;
+  if ((st = splitk_check(M, N, K, splits, workspace, workspace_bytes)) != LTX_OK) return st;
+  GemmArgs p = make_args(A, lda, Wq, ldw, w_scale, 0, bias, C, ldc, M, N, K, residual, ldr, gate, sigmoid_from);
+  return launch_splitk<B_INT8>(p, epilogue, splits, workspace, (hipStream_t)stream);
+}
+
+extern "C" int ltx_gemm_splitk_mxfp8_bf16(const void* A, int64_t lda, const uint8_t* Wq, int64_t ldw,
+                                          const uint8_t* w_scale, int64_t ld_scale, const float* bias, void* C,
+                                          int64_t ldc, int64_t M, int64_t N, int64_t K, int epilogue,
+                                          const void* residual, int64_t ldr, const float* gate,
+                                          int64_t sigmoid_from, int splits, float* workspace,
+                                          int64_t workspace_bytes, void* stream) {
+  int st = gemm_check(A, lda, Wq, ldw, C, ldc, M, N, K, epilogue, residual, ldr, gate, 1);
+  if (st != LTX_OK) return st;
+  if (!w_scale || ld_scale < K / 32) return LTX_ERR_INVALID_ARG;
+  if (ld_scale % 4 || ((uintptr_t)w_scale & 3u)) return LTX_ERR_ALIGNMENT;
+  if (M == 0 || N == 0) return LTX_OK;
+  if (K == 0) return LTX_ERR_UNSUPPORTED;
+  if ((st = splitk_check(M, N, K, splits, workspace, workspace_bytes)) != LTX_OK) return st;
+  if (K % (128 * (int64_t)splits)) return LTX_ERR_UNSUPPORTED;  // each split's scale words stay 4-byte aligned
+  GemmArgs p = make_args(A, lda, Wq, ldw, w_scale, ld_scale, bias, C, ldc, M, N, K, residual, ldr, gate,
+                         sigmoid_from);
+  return launch_splitk<B_MXFP8>(p, epilogue, splits, workspace, (hipStream_t)stream);
 }

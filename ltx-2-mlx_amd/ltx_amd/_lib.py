@@ -40,6 +40,12 @@ SIGNATURES: dict[str, list] = {
                             _i64, _vp],
     "ltx_gemm_mxfp8_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64,
                             _vp, _i64, _vp],
+    "ltx_gemm_splitk_bf16": [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64, _vp, _i64,
+                             _int, _vp, _i64, _vp],
+    "ltx_gemm_splitk_w8a16_bf16": [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64,
+                                   _vp, _i64, _int, _vp, _i64, _vp],
+    "ltx_gemm_splitk_mxfp8_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp,
+                                   _i64, _vp, _i64, _int, _vp, _i64, _vp],
     "ltx_quantize_mxfp8_bf16": [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp],
     "ltx_dequantize_mxfp8_bf16": [_vp, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _vp],
     "ltx_quantize_w8_bf16": [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp],
@@ -96,6 +102,8 @@ def lib() -> ctypes.CDLL:
         handle.ltx_attn_vt_padded_len.restype = _i64
         handle.ltx_attn_splitkv_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64]
         handle.ltx_attn_splitkv_workspace_bytes.restype = _i64
+        handle.ltx_gemm_splitk_workspace_bytes.argtypes = [_i64, _i64, _i64]
+        handle.ltx_gemm_splitk_workspace_bytes.restype = _i64
         handle.ltx_status_string.argtypes = [ctypes.c_int]
         handle.ltx_status_string.restype = ctypes.c_char_p
         _LIB = handle

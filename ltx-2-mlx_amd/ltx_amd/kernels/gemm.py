@@ -129,16 +129,41 @@ def dequantize(weight: LinearWeight) -> torch.Tensor:
     return out
 
 
+# Block budget of an automatic split-K launch (128x128 tiles x splits).
+SPLITK_MAX_BLOCKS = 80
+
+
+def auto_splits(m: int, n: int, k: int, kind: str, max_blocks: int | None = None) -> int:
+    """Split-K factor for a few-row product: the largest power of two keeping
+    at most ``max_blocks`` (default ``SPLITK_MAX_BLOCKS``) blocks of 128x128
+    tiles, at least 256 of K per split and K divisible by the split
+    granularity; 1 when the product already fills the chip (or has more than
+    256 rows)."""
+    max_blocks = SPLITK_MAX_BLOCKS if max_blocks is None else max_blocks
+    if m > 256 or k < 1024:
+        return 1
+    tiles = ((m + 127) // 128) * ((n + 127) // 128)
+    if tiles >= 160:
+        return 1
+    unit = 128 if kind == "mxfp8" else 64
+    s = 1
+    while tiles * s * 2 <= max_blocks and k % (unit * s * 2) == 0 and k // (s * 2) >= 256:
+        s *= 2
+    return s
+
+
 def linear(x: torch.Tensor, weight: LinearWeight, *, epilogue: int = EPI_BIAS,
            out: torch.Tensor | None = None, residual: torch.Tensor | None = None,
            gate: torch.Tensor | None = None, tile: int = TILE_AUTO,
-           sigmoid_from: int | None = None) -> torch.Tensor:
+           sigmoid_from: int | None = None, splits: int | None = None) -> torch.Tensor:
     """``epilogue(x @ W.T + b)`` for x (..., K) bf16; returns (..., N) bf16.
 
     For the residual epilogues, ``residual`` (..., N) bf16 and ``gate`` fp32
     (N) are required; ``out`` may be ``residual`` itself (in-place update).
     With ``EPI_BIAS``, columns ``n >= sigmoid_from`` get the 2*sigmoid head
     gate instead (fused gate-logit columns of a Q/QKV projection).
+    ``splits``: split-K factor (None: ``auto_splits`` for the 128x128 tiles,
+    1: single pass); the split form sums fp32 partials from a workspace.
     """
     k = weight.in_features
     n = weight.out_features
@@ -175,8 +200,30 @@ def linear(x: torch.Tensor, weight: LinearWeight, *, epilogue: int = EPI_BIAS,
     detail = f"{weight.kind} M={m} N={n} K={k} epi={epilogue}"
     hook = LAUNCH_HOOK
     info = (weight.kind, m, n, k, epilogue) if hook is not None else None
+    if splits is None:
+        splits = auto_splits(m, n, k, weight.kind) if tile in (TILE_AUTO, TILE_128) else 1
     if hook is not None:
         hook("pre", info)
+    if splits > 1:
+        ws_bytes = splits * m * n * 4
+        ws = torch.empty(splits * m * n, dtype=torch.float32, device=x.device)
+        if weight.kind == "bf16":
+            _lib.call("ltx_gemm_splitk_bf16", xv.data_ptr(), lda, weight.w.data_ptr(), weight.w.stride(0), bptr,
+                      ov.data_ptr(), ldc, m, n, k, flags, rptr, ldr, gptr, sig, splits, ws.data_ptr(), ws_bytes,
+                      stream, detail=detail)
+        elif weight.kind == "int8":
+            _lib.call("ltx_gemm_splitk_w8a16_bf16", xv.data_ptr(), lda, weight.w.data_ptr(), weight.w.stride(0),
+                      weight.scale.data_ptr(), bptr, ov.data_ptr(), ldc, m, n, k, flags, rptr, ldr, gptr, sig,
+                      splits, ws.data_ptr(), ws_bytes, stream, detail=detail)
+        elif weight.kind == "mxfp8":
+            _lib.call("ltx_gemm_splitk_mxfp8_bf16", xv.data_ptr(), lda, weight.w.data_ptr(), weight.w.stride(0),
+                      weight.scale.data_ptr(), weight.scale.stride(0), bptr, ov.data_ptr(), ldc, m, n, k, flags,
+                      rptr, ldr, gptr, sig, splits, ws.data_ptr(), ws_bytes, stream, detail=detail)
+        else:
+            raise ValueError(f"unknown weight format {weight.kind!r}")
+        if hook is not None:
+            hook("post", info)
+        return out
     if weight.kind == "bf16":
         _lib.call("ltx_gemm_bf16", xv.data_ptr(), lda, weight.w.data_ptr(), weight.w.stride(0), bptr,
                   ov.data_ptr(), ldc, m, n, k, flags, rptr, ldr, gptr, sig, stream, detail=detail)

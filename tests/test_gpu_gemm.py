@@ -209,3 +209,50 @@ def test_gemm_rejects_bad_shapes():
     wt = gemm.make_weight(torch.zeros((64, 100 * 0 + 96), dtype=torch.bfloat16, device=DEV))
     with pytest.raises(_lib.LtxKernelError):  # K = 96 is not a multiple of 64
         gemm.linear(torch.zeros((4, 96), dtype=torch.bfloat16, device=DEV), wt)
+
+
+@pytest.mark.parametrize("kind", ["bf16", "int8", "mxfp8"])
+@pytest.mark.parametrize("epi", ["bias", "gelu", "sigmoid2", "residual", "residual_round"])
+@pytest.mark.parametrize("M,K,N,splits", [(68, 2048, 8192, 4), (68, 8192, 2048, 16), (1, 4096, 1024, 8),
+                                          (100, 2048, 2080, 2), (256, 4096, 4096, 4)])
+def test_gemm_splitk(kind, epi, M, K, N, splits):
+    """Split-K (fp32 partials summed in split order, then the epilogue) against
+    the oracle and the single-pass kernel; the gate-logit columns too."""
+    from ltx_amd.kernels import gemm
+
+    print(f"splitk {kind} {epi} M={M} K={K} N={N} s={splits}", flush=True)
+    codes = {"bias": gemm.EPI_BIAS, "gelu": gemm.EPI_GELU, "sigmoid2": gemm.EPI_SIGMOID2,
+             "residual": gemm.EPI_RESIDUAL, "residual_round": gemm.EPI_RESIDUAL_ROUND}
+    rng = np.random.default_rng(M + K + N)
+    x = _bf(rng, (M, K))
+    W = _bf(rng, (N, K), 0.02)
+    b = bf16r(rng.standard_normal(N).astype(np.float32) * 0.1)
+    res = _bf(rng, (M, N))
+    g = rng.standard_normal(N).astype(np.float32) * 0.5
+    wt = gemm.make_weight(_t(W), _t(b, torch.float32), kind=kind)
+    sig = N - 32 if epi == "bias" else None
+
+    def run(s):
+        if epi.startswith("residual"):
+            rt = _t(res)
+            return gemm.linear(_t(x), wt, epilogue=codes[epi], out=rt, residual=rt, gate=_t(g, torch.float32),
+                               splits=s)
+        return gemm.linear(_t(x), wt, epilogue=codes[epi], splits=s, sigmoid_from=sig)
+
+    split, single = bf16_from_torch(run(splits)), bf16_from_torch(run(1))
+    torch.cuda.synchronize()
+    ref = oq.linear(x, _decoded(kind, W), b, epilogue=epi, residual=res, gate=g, round_then_bias=kind == "mxfp8")
+    if sig is not None:  # head-gate columns
+        ref[:, sig:] = oq.linear(x, _decoded(kind, W), b, epilogue="sigmoid2", round_then_bias=kind == "mxfp8")[:, sig:]
+    _check(split, ref, min_exact=0.85)
+    assert (ulp_diff_bf16(split, single) == 0).mean() >= 0.85
+
+
+def test_gemm_splitk_rejects_bad_splits():
+    from ltx_amd.kernels import gemm
+    from ltx_amd._lib import LtxKernelError
+
+    wt = gemm.make_weight(torch.zeros((64, 2048), dtype=torch.bfloat16, device=DEV), kind="mxfp8")
+    x = torch.zeros((4, 2048), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(LtxKernelError):
+        gemm.linear(x, wt, splits=32)  # 2048 % (128 * 32) != 0 for MXFP8

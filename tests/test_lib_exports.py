@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
     # every declared symbol is bound with a signature in the ctypes layer
     bound = set(_lib.SIGNATURES) | {"ltx_status_string", "ltx_attn_vt_padded_len",
-                                     "ltx_attn_splitkv_workspace_bytes"}
+                                     "ltx_attn_splitkv_workspace_bytes", "ltx_gemm_splitk_workspace_bytes"}
     assert set(declared_symbols()) <= bound, set(declared_symbols()) - bound
 
 
@@ -75,3 +75,9 @@ def test_argument_validation_without_gpu():
     assert lib.ltx_gemm_bf16(16, 64, 16, 64, None, 16, 64, 0, 64, 64, _lib.GEMM_ROUND_THEN_BIAS, None, 0, None,
                              64, None) == 0
     assert lib.ltx_gemm_bf16(16, 64, 16, 64, None, 16, 64, 0, 64, 64, 1 << 13, None, 0, None, 64, None) == -1
+    # split-K: workspace size, and too-small workspace / bad split counts rejected before any launch
+    assert lib.ltx_gemm_splitk_workspace_bytes(68, 2048, 4) == 4 * 68 * 2048 * 4
+    assert lib.ltx_gemm_splitk_bf16(16, 2048, 16, 2048, None, 16, 64, 4, 64, 2048, 0, None, 0, None, 64, 4,
+                                    16, 16, None) == -1
+    assert lib.ltx_gemm_splitk_bf16(16, 2048, 16, 2048, None, 16, 64, 4, 64, 2048, 0, None, 0, None, 64, 3,
+                                    16, 1 << 30, None) == -2
