@@ -673,9 +673,12 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
   // column of this wave tile takes the head-gate sigmoid is wave-uniform, so
   // the common case runs without it.
   char* E = lds + wave * EPI_WAVE;
-  const bool rtb = p.round_then_bias != 0;
-  auto phase1 = [&](auto sig_tag) {
+  // sig_tag / rtb_tag: compile-time forms of two block-uniform conditions
+  // (gate columns in this wave tile; bias added to the rounded product), so
+  // the per-element code has no branches
+  auto phase1 = [&](auto sig_tag, auto rtb_tag) {
     constexpr bool SIG = decltype(sig_tag)::value;
+    constexpr bool RTB = decltype(rtb_tag)::value;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
 #pragma unroll
@@ -689,7 +692,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float a = acc[i][j][4 * g + e];
-            y[e] = (rtb ? round_bf(a) : a) + bias4[e];
+            y[e] = (RTB ? round_bf(a) : a) + bias4[e];
             if (EPI == LTX_GEMM_EPI_GELU) y[e] = gelu_tanh(round_bf(y[e]));
             if (EPI == LTX_GEMM_EPI_SIGMOID2) y[e] = sigmoid2_bf(round_bf(y[e]));
             if (SIG && gn + e >= p.sig_from) y[e] = sigmoid2_bf(round_bf(y[e]));
@@ -702,10 +705,14 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
       }
     }
   };
-  if (EPI == LTX_GEMM_EPI_BIAS && n0 + wn * WN + WN > p.sig_from)
-    phase1(std::true_type{});
-  else
-    phase1(std::false_type{});
+  const bool sig = EPI == LTX_GEMM_EPI_BIAS && n0 + wn * WN + WN > p.sig_from;
+  if (p.round_then_bias) {
+    if (sig) phase1(std::true_type{}, std::true_type{});
+    else phase1(std::false_type{}, std::true_type{});
+  } else {
+    if (sig) phase1(std::true_type{}, std::false_type{});
+    else phase1(std::false_type{}, std::false_type{});
+  }
   __syncthreads();
 
   // phase 2: coalesced 16-byte stores (+ gated residual)
