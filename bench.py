@@ -254,7 +254,7 @@ def guided_step_ms(model, args, ta: int, s: int) -> dict:
         return time.perf_counter() - t0
 
     print(f"# guided loop: warmup + {args.guided_steps} steps", file=sys.stderr, flush=True)
-    run(1)
+    run(2)  # the shifted schedule needs two steps for finite sigmas
     wall = run(args.guided_steps)
     return {"ms_per_step": round(wall / args.guided_steps * 1e3, 3), "passes_per_step": 3,
             "steps": args.guided_steps, "timing": "eager",

@@ -45,7 +45,10 @@ class LTX2Scheduler:
         if stretch and steps > 0:
             one_minus = (f32(1.0) - sigmas).astype(np.float32)
             scale_factor = float(one_minus[steps - 1]) / (1.0 - terminal)
-            stretched = (f32(1.0) - one_minus / f32(scale_factor)).astype(np.float32)
+            # steps == 1: scale_factor is 0 and the first sigma becomes 0/0 = NaN,
+            # as the reference's array division gives
+            with np.errstate(divide="ignore", invalid="ignore"):
+                stretched = (f32(1.0) - one_minus / f32(scale_factor)).astype(np.float32)
             sigmas = np.where(sigmas != 0, stretched, sigmas).astype(np.float32)
         return sigmas.astype(np.float32)
 

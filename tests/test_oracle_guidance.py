@@ -103,3 +103,18 @@ def test_ltx2_scheduler_shift_closed_form():
     s2 = LTX2Scheduler().execute(steps=2, latent=lat, stretch=False)
     e2 = np.float32(np.exp(0.95))
     assert s2[1] == np.float32(e2 / (e2 + np.float32(1.0)))
+
+
+def test_ltx2_scheduler_one_step_stretch_is_nan():
+    """One step: the last non-zero sigma is sigma_0 = 1, so the stretch divides
+    0 by 0 (components/schedulers.py:74-89); the first sigma is NaN, silently,
+    and the shift alone (stretch off) is finite."""
+    import warnings
+
+    from ltx_amd.components.schedulers import LTX2Scheduler
+
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        s = LTX2Scheduler().execute(steps=1)
+    assert np.isnan(s[0]) and s[1] == 0.0
+    np.testing.assert_array_equal(LTX2Scheduler().execute(steps=1, stretch=False), np.float32([1.0, 0.0]))
