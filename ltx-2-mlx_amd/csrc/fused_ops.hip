@@ -6,10 +6,11 @@
 // the 16-byte vectors L, L+64, L+128, ... of the row, so every load and store
 // instruction of a wave moves one contiguous 1 KiB span of HBM.  The
 // per-channel parameters (1+scale, shift, gate) depend only on the lane's
-// channels, so a wave loads them into registers once and keeps them across
-// all the rows it visits (grid-stride over rows, at most 8 waves per CU of
-// work in flight).  Row reductions are wave-local shuffles; no LDS, no
-// barriers, no atomics.
+// channels: the gated add keeps its gate in registers across the rows a wave
+// visits, AdaLN keeps 1+scale and shift in LDS shared by the block's waves.
+// Rows are held packed (bf16) in registers and widened where used.  Row
+// reductions are wave-local shuffles; no barriers inside the row loop, no
+// atomics.
 #include "ltx_common.h"
 
 namespace ltx {
@@ -34,10 +35,8 @@ __device__ __forceinline__ void store8(bf16* p, const float* in) {
 // Streaming forms for the row kernels' activations: nontemporal loads and
 // stores (read once, written once) leave the caches to the data that is
 // reused; +8-10 % of HBM bandwidth on the 14640 x 4096 rows.
-__device__ __forceinline__ void load8_stream(const bf16* p, float* out) {
-  bf16x8 v = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(p));
-#pragma unroll
-  for (int i = 0; i < 8; ++i) out[i] = (float)v[i];
+__device__ __forceinline__ bf16x8 load8_stream(const bf16* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(p));
 }
 
 __device__ __forceinline__ void store8_stream(bf16* p, const float* in) {
@@ -87,16 +86,22 @@ __global__ __launch_bounds__(kRowBlock) void adaln_kernel(
     const float* onep = s_onep + z;
     const float* shp = s_shift + z;
     const bf16* xr = x + r * x_stride;
-    float xv[VPL][8];
+    // the row stays packed (bf16) in registers and is widened where used:
+    // half the VGPRs of a float copy, more rows in flight per SIMD
+    bf16x8 xv[VPL];
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) load8_stream(xr + (lane + j * kWave) * 8, xv[j]);
+    for (int j = 0; j < VPL; ++j)
+      xv[j] = load8_stream(xr + (lane + j * kWave) * 8);
     float inv = 1.0f;
     if (!no_norm) {
       float ss = 0.0f;
 #pragma unroll
       for (int j = 0; j < VPL; ++j)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) ss = fmaf(xv[j][i], xv[j][i], ss);
+        for (int i = 0; i < 8; ++i) {
+          const float v = (float)xv[j][i];
+          ss = fmaf(v, v, ss);
+        }
       ss = wave_sum(ss);
       inv = rsqrt_rn(ss * inv_c + eps);
     }
@@ -109,7 +114,7 @@ __global__ __launch_bounds__(kRowBlock) void adaln_kernel(
       load8f(shp + c0, sh);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        float n = xv[j][i] * inv;
+        float n = (float)xv[j][i] * inv;
         if (round_norm) n = round_bf(n);
         o[i] = n * op[i] + sh[i];
       }
@@ -135,22 +140,23 @@ __global__ __launch_bounds__(kRowBlock) void gated_add_kernel(
   for (int j = 0; j < VPL; ++j) load8f(gate + (lane + j * kWave) * 8, g[j]);
 
   for (int64_t r = wave0; r < rows; r += nwaves) {
-    float rv[VPL][8], bv[VPL][8];
+    bf16x8 rv[VPL], bv[VPL];  // packed, widened where used
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
       const int c0 = (lane + j * kWave) * 8;
-      load8_stream(residual + r * res_stride + c0, rv[j]);
-      load8_stream(branch + r * br_stride + c0, bv[j]);
+      rv[j] = load8_stream(residual + r * res_stride + c0);
+      bv[j] = load8_stream(branch + r * br_stride + c0);
     }
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
       float o[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
+        const float b = (float)bv[j][i], rr = (float)rv[j][i];
         if (round_prod)
-          o[i] = round_bf(bv[j][i] * g[j][i]) + rv[j][i];
+          o[i] = round_bf(b * g[j][i]) + rr;
         else
-          o[i] = fmaf(g[j][i], bv[j][i], rv[j][i]);
+          o[i] = fmaf(g[j][i], b, rr);
       }
       store8_stream(out + r * out_stride + (lane + j * kWave) * 8, o);
     }
@@ -418,9 +424,14 @@ using namespace ltx;
 
 static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-static inline int row_grid(int64_t rows) {
+// AdaLN and the gated add: up to one row per wave, so at 14640 rows every
+// row's loads are issued by the first wave that owns it (no grid-stride
+// second pass behind a wave's stores).
+constexpr int64_t kMaxStreamRowBlocks = 4096;
+
+static inline int row_grid(int64_t rows, int64_t cap = kMaxRowBlocks) {
   int64_t blocks = (rows + kWavesPerBlock - 1) / kWavesPerBlock;
-  if (blocks > kMaxRowBlocks) blocks = kMaxRowBlocks;
+  if (blocks > cap) blocks = cap;
   if (blocks < 1) blocks = 1;
   return (int)blocks;
 }
@@ -452,7 +463,7 @@ extern "C" int ltx_adaln_norm_fused_bf16(const void* x, int64_t x_stride, const 
   hipStream_t s = (hipStream_t)stream;
   const bf16* xp = (const bf16*)x;
   bf16* op = (bf16*)out;
-  const int grid = row_grid(rows);
+  const int grid = row_grid(rows, kMaxStreamRowBlocks);
   switch (C / 512) {
     case 1: adaln_kernel<1><<<grid, kRowBlock, 0, s>>>(xp, x_stride, scale, shift, op, out_stride, rows, eps, flags); break;
     case 2: adaln_kernel<2><<<grid, kRowBlock, 0, s>>>(xp, x_stride, scale, shift, op, out_stride, rows, eps, flags); break;
@@ -478,7 +489,7 @@ extern "C" int ltx_gated_add_fused_bf16(const void* residual, int64_t residual_s
   const bf16* rp = (const bf16*)residual;
   const bf16* bp = (const bf16*)branch;
   bf16* op = (bf16*)out;
-  const int grid = row_grid(rows);
+  const int grid = row_grid(rows, kMaxStreamRowBlocks);
   switch (C / 512) {
     case 1: gated_add_kernel<1><<<grid, kRowBlock, 0, s>>>(rp, residual_stride, bp, branch_stride, gate, op, out_stride, rows, flags); break;
     case 2: gated_add_kernel<2><<<grid, kRowBlock, 0, s>>>(rp, residual_stride, bp, branch_stride, gate, op, out_stride, rows, flags); break;
