@@ -343,7 +343,11 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
           rg[d] = u32x4{v[2], v[3], v[0], v[1]};
         }
         const u32x4 w = rg[d];
-        if (part == 0) {
+        // pieces of a load in four slots: the odd-row swap (part 0), the scale
+        // and the first code word (1), two words (2), the last word and the
+        // LDS writes (3) -- at most ~8 VALU instructions under one MFMA
+        const int dec_part = nparts == 4 ? 1 : 0;
+        if (part == dec_part) {
           if constexpr (BKIND == B_MXFP8) {
             // The loaded word goes straight into the empty asm, which pins the
             // byte extraction and decode here: hoisted to the top of the loop
@@ -357,7 +361,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
         }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          if (q * nparts / 4 != part) continue;
+          const int q_part = nparts == 4 ? (q == 0 ? 1 : (q == 3 ? 3 : 2)) : q * nparts / 4;
+          if (q_part != part) continue;
           const float sc = b_sc[i];
           if constexpr (BKIND == B_MXFP8) {
             b_o[i][2 * q] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[q], sc, false));
