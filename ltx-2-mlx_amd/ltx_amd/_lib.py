@@ -79,6 +79,7 @@ GEMM_EPI_SIGMOID2 = 4
 GEMM_TILE_256 = 1 << 8
 GEMM_TILE_128 = 2 << 8
 GEMM_TILE_256_DMA = 3 << 8
+GEMM_TILE_256x128 = 4 << 8
 GEMM_ROUND_THEN_BIAS = 1 << 12
 
 _LIB: ctypes.CDLL | None = None

@@ -86,7 +86,7 @@ def test_mxfp8_decoder_all_codes_bitexact():
 
 
 @pytest.mark.parametrize("kind", ["bf16", "int8", "mxfp8"])
-@pytest.mark.parametrize("tile", [1, 2, 3])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4])
 def test_gemm_identity_returns_decoded_weight(kind, tile):
     """C = I @ W'^T: each output is one product 1.0 * w' plus exact zeros."""
     from ltx_amd.kernels import gemm
@@ -135,7 +135,7 @@ def test_gemm_block_shapes(kind, K, N):
 
 
 @pytest.mark.parametrize("epi", ["bias", "gelu", "sigmoid2", "residual", "residual_round"])
-@pytest.mark.parametrize("tile", [1, 2, 3])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4])
 @pytest.mark.parametrize("kind", ["bf16", "mxfp8"])
 def test_gemm_epilogues(epi, tile, kind):
     """Every epilogue, with a non-zero bias: single rounding for bf16 weights
