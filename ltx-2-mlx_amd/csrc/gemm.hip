@@ -658,20 +658,25 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
   const int rsub = lane / CHUNKS;
   const int gn2 = n0 + wn * WN + ch * 8;
   const bool col_ok = gn2 < p.N;  // N % 8 == 0: a chunk is all in or all out
-  // Residual rows are fetched before phase 1 so their latency overlaps it
-  // (rows past M re-read row M-1, columns past N read column 0; neither is
-  // stored).  The residual may alias C: every residual element of this tile
-  // is read before any of its outputs is written.
+  // Residual rows (rows past M re-read row M-1, columns past N read column
+  // 0; neither is stored) are fetched once phase 1 has moved the
+  // accumulators to LDS: fetched any earlier, next to the 256 live
+  // accumulators, part of the tile spills to scratch (measured 6-15 % of the
+  // residual GEMMs' time).  Their latency overlaps the barrier after phase 1.
+  // The residual may alias C: every residual element of this tile is read
+  // before any of its outputs is written.
   bf16x8 res[RESID ? ITS : 1];
-  if constexpr (RESID) {
-    const int gnc = col_ok ? gn2 : 0;
+  auto fetch_res = [&]() {
+    if constexpr (RESID) {
+      const int gnc = col_ok ? gn2 : 0;
 #pragma unroll
-    for (int it = 0; it < ITS; ++it) {
-      int gm = m0 + wm * WM + it * ROWS_PER_IT + rsub;
-      gm = gm < p.M ? gm : p.M - 1;
-      res[it] = *reinterpret_cast<const bf16x8*>(p.R + (int64_t)gm * p.ldr + gnc);
+      for (int it = 0; it < ITS; ++it) {
+        int gm = m0 + wm * WM + it * ROWS_PER_IT + rsub;
+        gm = gm < p.M ? gm : p.M - 1;
+        res[it] = *reinterpret_cast<const bf16x8*>(p.R + (int64_t)gm * p.ldr + gnc);
+      }
     }
-  }
+  };
 
   // phase 1: acc[i][j] reg 4g+e holds C[m][n] with m = i*32 + lane%32 and
   // n = j*32 + 8g + 4*(lane/32) + e (wave-local coordinates).  Whether any
@@ -718,6 +723,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
     if (sig) phase1(std::true_type{}, std::false_type{});
     else phase1(std::false_type{}, std::false_type{});
   }
+  fetch_res();
   __syncthreads();
 
   // phase 2: coalesced 16-byte stores (+ gated residual)
