@@ -87,11 +87,13 @@ constexpr int kNumXcd = 8;
 // error ~2e-7, far below the bf16 rounding of the result; saturates correctly
 // at +-inf.
 __device__ __forceinline__ float gelu_tanh(float x) {
-  const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
-  const float u = k0 * (x + 0.044715f * x * x * x);
-  const float e = __builtin_amdgcn_exp2f(u * 2.8853900817779268f);  // exp(2u)
-  const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
-  return 0.5f * x * (1.0f + t);
+  // 0.5 x (1 + tanh(u)) with u = sqrt(2/pi) (x + 0.044715 x^3) is
+  // x sigmoid(2u) = x / (1 + 2^t), t = -2u log2(e) = x (A + B x^2):
+  // five VALU instructions and two transcendentals per element
+  constexpr float A = -2.0f * 0.7978845608028654f * 1.4426950408889634f;
+  constexpr float B = A * 0.044715f;
+  const float t = x * fmaf(B, x * x, A);
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
 }
 
 // 2 * bf16(sigmoid(y)) -- the head gate of attention.py:586-590 -- with the
