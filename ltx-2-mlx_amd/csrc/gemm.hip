@@ -563,9 +563,9 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
   // reads) in flight, which the 4-bit LDS counter can track exactly.
   // With the register loader, the fragment reads of k-step kk+1 go one after
   // each of the first TM+TN MFMAs of kk, and the LDS writes of the next stage
-  // (into wbuf), each followed by the global load of the stage after it into
-  // the same registers (kt_load), are spread evenly over these k-steps' MFMAs:
-  // no burst of LDS traffic queues up behind the other waves'.
+  // (into wbuf), each followed one MFMA later by the global load of the stage
+  // after it into the same registers (kt_load), are spread evenly over these
+  // k-steps' MFMAs: no burst of LDS traffic queues up behind the other waves'.
   auto leading_ksteps = [&](int buf, int wbuf, bool write, int kt_load) {
 #pragma unroll
     for (int kk = 0; kk < KSTEPS - 1; ++kk) {
@@ -583,10 +583,12 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
             const int slot0 = (d * SLOTS) / L;
 #pragma unroll
             for (int part = 0; part < np; ++part)
-              if (slot0 + part == kk * NM + m && write) {
-                lwrite(d, wbuf, part, np);
-                if (part == np - 1) gload(d, kt_load);
-              }
+              if (slot0 + part == kk * NM + m && write) lwrite(d, wbuf, part, np);
+            // the reload into the same registers goes one slot after the LDS
+            // write that reads them (issued right behind it, it waits for the
+            // write to take its data: 3 % of a bf16 GEMM)
+            const int reload = slot0 + np < SLOTS ? slot0 + np : SLOTS - 1;
+            if (reload == kk * NM + m && write) gload(d, kt_load);
           }
         });
       } else {
