@@ -1,0 +1,55 @@
+"""Host-side logic of bench.py: the one-GPU guard, the step's algorithmic
+flop count and the HBM-traffic record it reports (no GPU needed)."""
+
+from __future__ import annotations
+
+import json
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+sys.path.insert(0, str(ROOT))
+
+import bench  # noqa: E402
+
+
+def test_more_than_one_gpu_exits_with_a_message():
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2
+    msg = json.loads(r.stdout.strip().splitlines()[-1])
+    assert msg["n_gpus"] == 2 and "one GPU" in msg["error"]
+
+
+def test_step_flops_closed_form():
+    """48 blocks at 3456 video + 68 audio + 256 text tokens: 101.0 TFLOP.
+    Spot-check the composition: a video-only one-block step is the six
+    projection GEMM groups plus self and text attention plus the output
+    head, written out here from the block's shapes."""
+    total = bench.step_flops(3456, 68, 256, 48)
+    assert total == pytest.approx(101.01e12, rel=1e-3)
+    tv, s, d, h = 3456, 256, 4096, 32
+    gemm = (2 * tv * d * (3 * d + h) + 2 * tv * d * d          # self-attention QKV + gate, out
+            + 2 * tv * d * (d + h) + 2 * s * d * 2 * d + 2 * tv * d * d  # text attention Q + gate, KV, out
+            + 2 * tv * d * 4 * d * 2)                          # feed-forward up and down
+    attn = 4 * tv * tv * d + 4 * tv * s * d
+    head = 2 * tv * 128 * d * 2                                # patchify in, projection out
+    assert bench.step_flops(tv, 0, s, 1) == pytest.approx(gemm + attn + head, rel=1e-12)
+    # linear in the block count beyond the per-step head
+    assert bench.step_flops(tv, 68, s, 2) - bench.step_flops(tv, 68, s, 1) == pytest.approx(
+        bench.step_flops(tv, 68, s, 1) - bench.step_flops(tv, 68, s, 0), rel=1e-12)
+
+
+def test_traffic_record_is_consistent():
+    """The bytes the bench reports are the counter values scaled by the copy
+    calibration recorded next to them."""
+    rec = json.loads((ROOT / "profiles" / "gemm_ff_up_hbm_traffic.json").read_text())
+    for r in rec["launches"]:
+        expect = r["fetch_size_kib"] * 1024 * r["fetch_scale"] + r["write_size_kib"] * 1024 * r["write_scale"]
+        assert r["hbm_bytes"] == pytest.approx(expect, abs=1024)
+        assert bench.measured_traffic(r["kernel"], r["weights"]) == r["hbm_bytes"]
+        assert r["hbm_bytes"] > r["algorithmic_bytes"]
+    assert bench.measured_traffic("no such kernel", "mxfp8") is None
