@@ -17,6 +17,7 @@ the distilled text-to-video+audio path:
 
 from __future__ import annotations
 
+import hashlib
 from dataclasses import dataclass
 
 import numpy as np
@@ -33,6 +34,14 @@ AUDIO_HEADS = 32
 AUDIO_HEAD_DIM = 64
 AUDIO_IN_CHANNELS = 128
 AUDIO_CROSS_PE_MAX_POS = 20
+# distinct position sets whose RoPE tables an LTXModel keeps (one 6144-token
+# video set is ~100 MB of fp32 tables)
+ROPE_CACHE_ENTRIES = 2
+
+
+def _positions_digest(positions: np.ndarray) -> tuple:
+    arr = np.ascontiguousarray(positions)
+    return arr.shape, arr.dtype.str, hashlib.blake2b(arr.tobytes(), digest_size=16).hexdigest()
 
 
 @dataclass
@@ -139,10 +148,20 @@ class LTXModel:
 
     def rope(self, video_positions: np.ndarray, audio_positions: np.ndarray | None):
         """Token-major RoPE tables for a stage: (video self, video cross, audio
-        self, audio cross); computed once per set of positions."""
-        key = (video_positions.shape, video_positions.tobytes()[:64], None if audio_positions is None
-               else (audio_positions.shape, audio_positions.tobytes()[:64]))
-        if key not in self._rope_cache:
+        self, audio cross).
+
+        Tables are built once per distinct set of positions and reused across
+        the steps of a stage.  The cache key is a digest of the full position
+        arrays (shape, dtype and every byte), so two grids with the same token
+        count but different layouts (landscape vs portrait) get their own
+        tables; at most ``ROPE_CACHE_ENTRIES`` sets are kept, least recently
+        used first out.  A caller that captured a graph over the returned
+        tensors keeps them alive by holding the returned tuple.
+        """
+        key = (_positions_digest(video_positions), None if audio_positions is None
+               else _positions_digest(audio_positions))
+        hit = self._rope_cache.pop(key, None)
+        if hit is None:
             dev = self.device
             vpe = rope_tables(video_positions, self.video_dim, VIDEO_MAX_POS, dev)
             vxpe = ape = axpe = None
@@ -151,8 +170,11 @@ class LTXModel:
                 vxpe = rope_tables(video_positions[:, 0:1], self.audio_dim, (AUDIO_CROSS_PE_MAX_POS,), dev)
                 ape = rope_tables(audio_positions, self.audio_dim, AUDIO_MAX_POS, dev)
                 axpe = rope_tables(audio_positions[:, 0:1], self.audio_dim, (AUDIO_CROSS_PE_MAX_POS,), dev)
-            self._rope_cache[key] = (vpe, vxpe, ape, axpe)
-        return self._rope_cache[key]
+            hit = (vpe, vxpe, ape, axpe)
+        self._rope_cache[key] = hit  # re-inserted: most recently used last
+        while len(self._rope_cache) > ROPE_CACHE_ENTRIES:
+            self._rope_cache.pop(next(iter(self._rope_cache)))
+        return hit
 
     def _timestep_rows(self, sigma_dev: torch.Tensor, cross_sigma_dev: torch.Tensor, video: bool) -> None:
         """Fill the (16, D) timestep rows of one modality (model.py:160-187,
