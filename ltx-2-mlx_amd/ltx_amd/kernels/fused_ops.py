@@ -15,49 +15,60 @@ stream.  Otherwise the stock-framework expression runs, exactly as the
 reference falls back to its MLX expression (:192-201, :362-366).  The gate
 never depends on whether the library is present: a missing library raises.
 
-``LTX_FUSED_PROBE=1`` counts kernel vs fallback dispatches and prints the
-summary at exit (reference :12-69).
+``LTX_FUSED_PROBE=1`` tallies kernel vs fallback dispatches per operator and
+prints the kernel share at exit (the reference's switch, :12-69).
 """
 
 from __future__ import annotations
 
 import atexit
+import collections
 import os
 
 import torch
 
 from .. import _lib
 
-_PROBE_ENABLED = bool(os.environ.get("LTX_FUSED_PROBE"))
-_PROBE_COUNTS: dict[str, int] = {
-    "adaln_kernel": 0,
-    "adaln_fallback": 0,
-    "gated_add_kernel": 0,
-    "gated_add_fallback": 0,
-}
+class _DispatchTally:
+    """Counts, per operator, how many calls took the HIP kernel and how many
+    the fallback expression, when ``$LTX_FUSED_PROBE`` is set (the reference's
+    probe switch, kernels/fused_ops.py:12-69); the per-operator kernel share is
+    printed once at interpreter exit."""
+
+    PATHS = ("kernel", "fallback")
+
+    def __init__(self, ops: tuple[str, ...]):
+        self.enabled = bool(os.environ.get("LTX_FUSED_PROBE"))
+        self.ops = ops
+        self.tally = collections.Counter()
+        if self.enabled:
+            atexit.register(self.report)
+
+    def hit(self, op: str, path: str) -> None:
+        if self.enabled:
+            self.tally[op, path] += 1
+
+    def counts(self) -> dict[str, int]:
+        return {f"{op}_{path}": self.tally[op, path] for op in self.ops for path in self.PATHS}
+
+    def report(self) -> None:
+        lines = []
+        for op in self.ops:
+            k, f = self.tally[op, "kernel"], self.tally[op, "fallback"]
+            if k + f:
+                lines.append(f"  {op}: {k} on the HIP kernel, {f} on the fallback "
+                             f"({k / (k + f):.1%} kernel)")
+        if lines:
+            print("LTX_FUSED_PROBE dispatch tally", *lines, sep="\n")
 
 
-def _probe(name: str) -> None:
-    if _PROBE_ENABLED:
-        _PROBE_COUNTS[name] += 1
+_TALLY = _DispatchTally(("adaln", "gated_add"))
 
 
 def get_dispatch_counts() -> dict[str, int]:
-    """Copy of the dispatch counters (all zero unless LTX_FUSED_PROBE is set)."""
-    return dict(_PROBE_COUNTS)
-
-
-def _print_dispatch_summary() -> None:
-    total = sum(_PROBE_COUNTS.values())
-    if not _PROBE_ENABLED or total == 0:
-        return
-    print("\n[LTX_FUSED_PROBE] fused-op dispatch summary:")
-    for name, n in _PROBE_COUNTS.items():
-        print(f"  {name:<22} {n:>8}  ({100.0 * n / total:5.1f}%)")
-
-
-if _PROBE_ENABLED:
-    atexit.register(_print_dispatch_summary)
+    """``{op_path: calls}`` for op in (adaln, gated_add) and path in (kernel,
+    fallback); all zero unless ``$LTX_FUSED_PROBE`` is set."""
+    return _TALLY.counts()
 
 
 _ADALN_FUSED_EPS = 1e-6
@@ -115,9 +126,9 @@ def adaln_norm_fused(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, 
     kernel path rounds once, like the reference kernel.
     """
     if eps != _ADALN_FUSED_EPS or not _adaln_t2v_broadcast_compatible(x, scale, shift):
-        _probe("adaln_fallback")
+        _TALLY.hit("adaln", "fallback")
         return _adaln_norm_torch(x, scale, shift, eps)
-    _probe("adaln_kernel")
+    _TALLY.hit("adaln", "kernel")
     b, t, c = x.shape
     xv, xs = _lib.row_view(x, c)
     out = torch.empty((b, t, c), dtype=torch.bfloat16, device=x.device)
@@ -164,9 +175,9 @@ def gated_add_rows(res2d: torch.Tensor, res_stride: int, br2d: torch.Tensor, br_
 def gated_add_fused(residual: torch.Tensor, branch: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
     """Fused gated add: ``residual + branch * gate``, cast to residual.dtype."""
     if not _gated_add_t2v_broadcast_compatible(residual, branch, gate):
-        _probe("gated_add_fallback")
+        _TALLY.hit("gated_add", "fallback")
         return _gated_add_torch(residual, branch, gate)
-    _probe("gated_add_kernel")
+    _TALLY.hit("gated_add", "kernel")
     b, t, c = residual.shape
     rv, rs = _lib.row_view(residual, c)
     bv, bs = _lib.row_view(branch, c)

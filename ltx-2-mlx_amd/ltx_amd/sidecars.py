@@ -1,24 +1,31 @@
-"""Sidecar I/O: named latents / conditioning plus string metadata next to a
-run's output (LTX_2_MLX/sidecars.py:1-163).
+"""Sidecars: named tensors plus string metadata stored beside a run's output
+(latents of each stage, text conditioning).
 
-Two formats, chosen by ``$LTX_SIDECAR_FORMAT`` (default ``safetensors``):
+The on-disk formats are the reference's (LTX_2_MLX/sidecars.py), so files move
+between the two implementations in both directions:
 
-* ``safetensors``: tensors in their native dtype (bf16 included), string
-  metadata in the header's ``__metadata__`` -- the file the reference writes
-  with ``mx.save_safetensors`` and reads with ``mx.load(...,
-  return_metadata=True)``;
-* ``npz`` (legacy): numpy has no bf16, so bf16 tensors are widened to fp32 and
-  their dtype recorded as ``<key>_mlx_dtype`` (the reference writes MLX's dtype
-  name, e.g. ``mlx.core.bfloat16``); metadata as 0-d string arrays; read with
-  ``allow_pickle=False``.
+* ``safetensors`` -- tensors in their own dtype (bf16 stays bf16), metadata as
+  the header's ``__metadata__`` string map;
+* ``npz`` (legacy) -- a numpy zip archive.  numpy has no bf16, so every tensor
+  is stored widened where needed, with an entry ``<key>_mlx_dtype`` naming its
+  original dtype the way MLX prints it (``mlx.core.bfloat16``); metadata
+  entries are 0-d string arrays.
 
-Tensors are torch tensors (device tensors are copied to the host to write);
-``load_sidecar(path, device=...)`` returns them on ``device``.
+The writer's format comes from the ``fmt`` argument or ``$LTX_SIDECAR_FORMAT``
+(``safetensors`` when unset); the written file's extension always matches
+it.  Readers look at the file itself (a zip archive is the npz form,
+anything else must be safetensors), and ``find_sidecar`` prefers a
+``.safetensors`` file over an ``.npz`` one of the same stem.
+
+Tensors are torch tensors; device tensors are copied to the host to write,
+and ``load_sidecar(path, device=...)`` places what it reads on ``device``.
 """
 
 from __future__ import annotations
 
+import io
 import os
+from pathlib import Path
 
 import numpy as np
 import torch
@@ -26,92 +33,134 @@ import torch
 from .loader.safetensors_file import SafetensorsFile, write_safetensors
 
 SIDECAR_FORMAT_ENV = "LTX_SIDECAR_FORMAT"
-_DEFAULT_FORMAT = "safetensors"
-_FORMATS = ("npz", "safetensors")
-_MLX_NAMES = {torch.bfloat16: "bfloat16", torch.float16: "float16", torch.float32: "float32",
-              torch.int32: "int32", torch.int64: "int64", torch.uint8: "uint8", torch.int8: "int8",
-              torch.bool: "bool_"}
-_FROM_MLX = {v: k for k, v in _MLX_NAMES.items()}
+DTYPE_TAG_SUFFIX = "_mlx_dtype"
+_ZIP_MAGIC = b"PK\x03\x04"
+
+
+def _mlx_dtype_name(dtype: torch.dtype) -> str:
+    """How MLX prints the dtype that matches a torch dtype."""
+    short = str(dtype).split(".")[-1]
+    return "mlx.core." + ("bool_" if short == "bool" else short)
+
+
+def _torch_dtype_from_tag(tag: str) -> torch.dtype | None:
+    """Inverse of ``_mlx_dtype_name``; None for a name torch does not know."""
+    short = tag.strip().split(".")[-1].rstrip("_")
+    found = getattr(torch, short, None)
+    return found if isinstance(found, torch.dtype) else None
+
+
+class _SafetensorsSidecar:
+    name, suffix = "safetensors", ".safetensors"
+
+    @staticmethod
+    def write(path: Path, tensors: dict[str, torch.Tensor], metadata: dict[str, str]) -> None:
+        write_safetensors(path, ((k, t, None) for k, t in tensors.items()), metadata=metadata)
+
+    @staticmethod
+    def read(path: Path, device) -> tuple[dict[str, torch.Tensor], dict[str, str]]:
+        f = SafetensorsFile(path)
+        try:
+            return ({key: f.tensor(key, device) for key in f.keys()},
+                    {str(k): str(v) for k, v in f.metadata.items()})
+        finally:
+            f.close()
+
+
+class _NpzSidecar:
+    name, suffix = "npz", ".npz"
+
+    @staticmethod
+    def write(path: Path, tensors: dict[str, torch.Tensor], metadata: dict[str, str]) -> None:
+        entries: dict[str, np.ndarray] = {}
+        for key, t in tensors.items():
+            host = t.detach().cpu()
+            entries[key] = (host.to(torch.float32) if host.dtype == torch.bfloat16 else host).numpy()
+            entries[key + DTYPE_TAG_SUFFIX] = np.array(_mlx_dtype_name(host.dtype))
+        entries.update({k: np.array(v) for k, v in metadata.items()})
+        buf = io.BytesIO()
+        np.savez(buf, **entries)
+        tmp = path.with_name(f".{path.name}.tmp")
+        tmp.write_bytes(buf.getvalue())
+        os.replace(tmp, path)
+
+    @staticmethod
+    def read(path: Path, device) -> tuple[dict[str, torch.Tensor], dict[str, str]]:
+        tensors: dict[str, torch.Tensor] = {}
+        metadata: dict[str, str] = {}
+        with np.load(path, allow_pickle=False) as archive:
+            names = set(archive.files)
+            for name in sorted(names):
+                value = archive[name]
+                if name.endswith(DTYPE_TAG_SUFFIX) or value.dtype.kind in "US":
+                    # dtype tags are reported with the metadata, as the reference does
+                    metadata[name] = str(value)
+                    continue
+                t = torch.from_numpy(np.array(value))
+                tag = name + DTYPE_TAG_SUFFIX
+                want = _torch_dtype_from_tag(str(archive[tag])) if tag in names else None
+                tensors[name] = (t if want is None else t.to(want)).to(device)
+        return tensors, metadata
+
+
+_FORMATS = {c.name: c for c in (_SafetensorsSidecar, _NpzSidecar)}
+_DEFAULT = _SafetensorsSidecar.name
+# when both files of a stem exist, the first suffix here wins
+_LOOKUP_SUFFIXES = (_SafetensorsSidecar.suffix, _NpzSidecar.suffix)
+
+
+def _resolve(fmt: str | None):
+    source = "fmt" if fmt is not None else SIDECAR_FORMAT_ENV
+    name = (fmt if fmt is not None else os.environ.get(SIDECAR_FORMAT_ENV, _DEFAULT)).lower()
+    if name not in _FORMATS:
+        raise ValueError(f"unsupported sidecar format {name!r} (from {source}); "
+                         f"expected one of {tuple(sorted(_FORMATS))}")
+    return _FORMATS[name]
 
 
 def default_format() -> str:
-    """The format named by ``$LTX_SIDECAR_FORMAT`` (else the default)."""
-    fmt = os.environ.get(SIDECAR_FORMAT_ENV, _DEFAULT_FORMAT).lower()
-    if fmt not in _FORMATS:
-        raise ValueError(f"{SIDECAR_FORMAT_ENV}={fmt!r}; expected one of {_FORMATS}")
-    return fmt
+    """The writer's format when none is passed: ``$LTX_SIDECAR_FORMAT``
+    (case-insensitive) or ``safetensors``."""
+    return _resolve(None).name
 
 
-def _ext_for(fmt: str) -> str:
-    return ".safetensors" if fmt == "safetensors" else ".npz"
+def _stem(path) -> str:
+    root, _ext = os.path.splitext(os.fspath(path))
+    return root
 
 
 def sidecar_path(base_path: str, suffix: str = "", fmt: str | None = None) -> str:
-    """``base_path`` without its extension, plus ``suffix`` and the format's extension."""
-    fmt = fmt or default_format()
-    stem = os.path.splitext(base_path)[0]
-    return f"{stem}{suffix}{_ext_for(fmt)}"
+    """Sidecar file name for ``base_path``: its extension replaced by
+    ``suffix`` plus the format's extension (``run.mp4`` -> ``run_text.npz``)."""
+    return _stem(base_path) + suffix + _resolve(fmt).suffix
 
 
 def find_sidecar(base_path: str, suffix: str = "") -> str | None:
-    """The existing sidecar next to ``base_path`` (safetensors first, then npz)."""
-    stem = os.path.splitext(str(base_path))[0]
-    for ext in (".safetensors", ".npz"):
-        candidate = f"{stem}{suffix}{ext}"
-        if os.path.exists(candidate):
-            return candidate
-    return None
+    """The existing sidecar for ``base_path`` and ``suffix`` in either format,
+    or None."""
+    candidates = (_stem(base_path) + suffix + ext for ext in _LOOKUP_SUFFIXES)
+    return next((c for c in candidates if os.path.exists(c)), None)
 
 
 def save_sidecar(path: str, arrays: dict[str, torch.Tensor], metadata: dict[str, str] | None = None, *,
                  fmt: str | None = None) -> str:
-    """Write ``arrays`` and string ``metadata``; the extension follows the
-    format.  Returns the path written."""
-    metadata = {str(k): str(v) for k, v in (metadata or {}).items()}
-    fmt = (fmt or default_format()).lower()
-    if fmt not in _FORMATS:
-        raise ValueError(f"fmt={fmt!r}; expected one of {_FORMATS}")
-    out = os.path.splitext(path)[0] + _ext_for(fmt)
-    out_dir = os.path.dirname(out)
-    if out_dir:
-        os.makedirs(out_dir, exist_ok=True)
-    arrays = {k: torch.as_tensor(v) for k, v in arrays.items()}
-    if fmt == "safetensors":
-        write_safetensors(out, [(k, v, None) for k, v in arrays.items()], metadata=metadata)
-    else:
-        payload = {}
-        for key, t in arrays.items():
-            t = t.detach().cpu()
-            payload[key] = (t.float() if t.dtype == torch.bfloat16 else t).numpy()
-            payload[f"{key}_mlx_dtype"] = np.array(f"mlx.core.{_MLX_NAMES.get(t.dtype, str(t.dtype))}")
-        for mkey, mval in metadata.items():
-            payload[mkey] = np.array(mval)
-        np.savez(out, **payload)
-    return out
+    """Write ``arrays`` and ``metadata`` (values stringified) at ``path`` with
+    its extension set by the format; creates the parent directory.  Returns
+    the path written."""
+    codec = _resolve(fmt)
+    out = Path(_stem(path) + codec.suffix)
+    out.parent.mkdir(parents=True, exist_ok=True)
+    tensors = {str(k): torch.as_tensor(v) for k, v in arrays.items()}
+    codec.write(out, tensors, {str(k): str(v) for k, v in (metadata or {}).items()})
+    return str(out)
 
 
 def load_sidecar(path: str, device: str | torch.device = "cpu") -> tuple[dict[str, torch.Tensor], dict[str, str]]:
-    """``(arrays, metadata)`` of a sidecar in either format; tensors in their
-    original dtype on ``device``."""
-    if str(path).endswith(".safetensors"):
-        f = SafetensorsFile(path)
-        arrays = {k: f.tensor(k, device) for k in f.keys()}
-        return arrays, {str(k): str(v) for k, v in f.metadata.items()}
-    arrays: dict[str, torch.Tensor] = {}
-    metadata: dict[str, str] = {}
-    with np.load(path, allow_pickle=False) as data:
-        tags = {k[: -len("_mlx_dtype")]: str(data[k]) for k in data.files if k.endswith("_mlx_dtype")}
-        for key in data.files:
-            if key.endswith("_mlx_dtype"):
-                continue
-            val = data[key]
-            if val.dtype.kind in ("U", "S"):
-                metadata[key] = str(val)
-                continue
-            t = torch.from_numpy(np.array(val))
-            target = _FROM_MLX.get(tags.get(key, "").rsplit(".", 1)[-1])
-            if target is not None:
-                t = t.to(target)
-            arrays[key] = t.to(device)
-    metadata.update({f"{k}_mlx_dtype": v for k, v in tags.items()})
-    return arrays, metadata
+    """``(tensors, metadata)`` of a sidecar in either format, tensors in the
+    dtype they were saved from, on ``device``.  For the npz form the dtype
+    tags appear in the metadata too."""
+    p = Path(path)
+    with open(p, "rb") as fh:
+        magic = fh.read(len(_ZIP_MAGIC))
+    codec = _NpzSidecar if magic == _ZIP_MAGIC else _SafetensorsSidecar
+    return codec.read(p, device)

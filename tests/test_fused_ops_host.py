@@ -2,6 +2,8 @@
 gates and fallbacks (LTX_2_MLX tests/test_fused_ops.py:75-142, :162-217;
 tests/test_precision_plumbing.py:162-180), on CPU tensors."""
 
+import atexit
+
 import numpy as np
 import torch
 
@@ -83,3 +85,27 @@ def test_kernel_path_refuses_host_tensors():
         F.adaln_norm_fused(x, sc, sh, 1e-6)
     with pytest.raises(ValueError):
         F.gated_add_fused(r, b, g)
+
+
+def test_dispatch_tally_counts_fallbacks_and_reports(monkeypatch, capsys):
+    """``LTX_FUSED_PROBE``: per-operator kernel/fallback tally (reference
+    kernels/fused_ops.py:12-69); gate-rejected calls count as fallbacks."""
+    monkeypatch.setenv("LTX_FUSED_PROBE", "1")
+    tally = F._DispatchTally(("adaln", "gated_add"))
+    atexit.unregister(tally.report)  # reported below instead of at exit
+    monkeypatch.setattr(F, "_TALLY", tally)
+    x, sc, sh, gate, res, br = _inputs()
+    F.adaln_norm_fused(x, sc, sh, 1e-5)  # eps != 1e-6 -> fallback
+    F.adaln_norm_fused(x.float(), sc, sh, 1e-6)  # fp32 x -> fallback
+    F.gated_add_fused(res, br, gate.bfloat16())  # bf16 gate -> fallback
+    assert F.get_dispatch_counts() == {"adaln_kernel": 0, "adaln_fallback": 2,
+                                       "gated_add_kernel": 0, "gated_add_fallback": 1}
+    tally.hit("adaln", "kernel")
+    tally.report()
+    out = capsys.readouterr().out
+    assert "adaln: 1 on the HIP kernel, 2 on the fallback (33.3% kernel)" in out
+    assert "gated_add: 0 on the HIP kernel, 1 on the fallback (0.0% kernel)" in out
+    monkeypatch.delenv("LTX_FUSED_PROBE")
+    quiet = F._DispatchTally(("adaln",))
+    quiet.hit("adaln", "kernel")
+    assert quiet.counts() == {"adaln_kernel": 0, "adaln_fallback": 0}
