@@ -16,9 +16,17 @@ is the single-rounding fused kernel (fused_ops.py:172-175).
 
 Pinning: built from the pinned pieces (oracle.fused_ops, oracle.rope,
 oracle.attention, oracle.quant.linear semantics), and checked in
-tests/test_oracle_block.py by invariants of the residual wiring (zero gates
-make every sub-layer vanish; a zero A2V gate decouples audio from video;
-per-token independence of the FF path).
+tests/test_oracle_block.py by properties that a wiring mistake breaks:
+zero gates make every sub-layer vanish; a zero A2V gate decouples audio from
+video; the FF path is per token; each of the 12 (scale, shift) row pairs
+feeds its own sub-layer input (scale -1 / shift c turns that input into the
+constant c, so the update becomes one shared row), including the AV tables'
+scale-before-shift order, and the mirrored assignment fails; V2A reads the
+norm taken before A2V (the A2V weights cannot reach the audio output); each
+cross-PE table rotates its own side in both directions (a 90-degree table
+equals rotated projection rows); text cross-attention rounds twice, the
+self-attention residual once.  Test infrastructure only: the product never
+imports this module.
 """
 
 from __future__ import annotations
