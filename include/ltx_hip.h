@@ -7,7 +7,9 @@
  *     (2-byte IEEE bfloat16 elements), fp32 tensors as `float*`.
  *   - `stream` is a hipStream_t passed as `void*` (NULL = the null stream).
  *     Every call only enqueues work on that stream; nothing synchronises the
- *     host, allocates or frees memory, or keeps state between calls.
+ *     host, allocates or frees memory, or keeps state between calls (the one
+ *     exception, ltx_flash_attn_splitkv_noalloc_bf16, keeps a fixed scratch
+ *     array per GPU instead of taking a workspace).
  *   - Row-major 2-D tensors carry an explicit row stride in ELEMENTS.
  *   - The return value is an LTX_* status code.  LTX_ERR_UNSUPPORTED means the
  *     shape is outside what the kernel implements; the caller decides whether
@@ -44,6 +46,8 @@ extern "C" {
 #define LTX_ERR_UNSUPPORTED (-2)
 #define LTX_ERR_HIP (-3)
 #define LTX_ERR_ALIGNMENT (-4)
+/* The request needs more than the fixed scratch of a no-allocation entry point. */
+#define LTX_ERR_SCRATCH_LIMIT (-5)
 
 /* Human-readable name of a status code (static storage). */
 const char* ltx_status_string(int status);
@@ -392,6 +396,27 @@ int ltx_flash_attn_splitkv_bf16(const void* Q, int64_t q_rs, const void* K, int6
                                 const void* gate, int64_t gate_rs, int64_t Tq, int64_t Tk,
                                 int64_t H, int64_t head_dim, float scale, int64_t splits,
                                 void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ltx_flash_attn_splitkv_bf16 without the workspace argument and without any
+ * allocation: the partials go to a scratch array of
+ * LTX_ATTN_NOALLOC_SCRATCH_BYTES that the library holds in device memory, one
+ * per GPU, for the life of the process (its address is resolved once per
+ * device, on the first call whose stream is on that device).  No counterpart
+ * in the reference: it exists for callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments and result contract as
+ * ltx_flash_attn_splitkv_bf16; a request with
+ * ltx_attn_splitkv_workspace_bytes(Tq, H, head_dim, splits) above the limit
+ * returns LTX_ERR_SCRATCH_LIMIT and enqueues nothing.  Nothing in the scratch
+ * needs to start at zero.  Every call on one GPU uses that GPU's one array,
+ * so calls that may overlap on a GPU (different streams, or several host
+ * threads) race: serialise them. */
+#define LTX_ATTN_NOALLOC_SCRATCH_BYTES (32ll << 20)
+int ltx_flash_attn_splitkv_noalloc_bf16(const void* Q, int64_t q_rs, const void* K, int64_t k_rs,
+                                        const void* Vt, int64_t tk_pad, void* O, int64_t o_rs,
+                                        const void* gate, int64_t gate_rs, int64_t Tq, int64_t Tk,
+                                        int64_t H, int64_t head_dim, float scale, int64_t splits,
+                                        void* stream);
 
 #ifdef __cplusplus
 }

@@ -34,6 +34,7 @@
 // other P), so the O^T rescale runs in the first blocks and then almost
 // never.  Workgroups of one head are numbered contiguously per XCD so its
 // K/V stay in that XCD's L2.
+#include <mutex>
 #include <type_traits>
 
 #include "ltx_common.h"
@@ -666,4 +667,55 @@ extern "C" int ltx_flash_attn_splitkv_bf16(const void* Q, int64_t q_rs, const vo
   }
 #undef LTX_FAS
   return ltx_launch_status();
+}
+
+// ---- split-KV attention without allocation --------------------------------
+// The partials of the split-KV pass live in `scratch`, device memory that the
+// code object itself holds (one copy per GPU, kept until the process ends).
+// Every (split, query, head) row of a call is written by the pass before the
+// combine reads it, so nothing has to start at zero; calls that overlap on one
+// GPU share the array and race.  The host never passes `scratch` itself to a
+// kernel: its name is a host-side stand-in, and the device address comes from
+// hipGetSymbolAddress, resolved once per device with that device current.
+static __device__ __align__(256) unsigned char scratch[LTX_ATTN_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+int scratch_on_stream_device(hipStream_t stream, void** out) {
+  int cur = 0;
+  if (hipGetDevice(&cur) != hipSuccess) return LTX_ERR_HIP;
+  int dev = cur;
+  if (stream && hipStreamGetDevice(stream, &dev) != hipSuccess) return LTX_ERR_HIP;
+  if (dev < 0 || dev >= kMaxDevices) return LTX_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    if (dev != cur && hipSetDevice(dev) != hipSuccess) return LTX_ERR_HIP;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur && hipSetDevice(cur) != hipSuccess) return LTX_ERR_HIP;
+    if (e != hipSuccess || !p) return LTX_ERR_HIP;
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return LTX_OK;
+}
+}  // namespace
+
+extern "C" int ltx_flash_attn_splitkv_noalloc_bf16(const void* Q, int64_t q_rs, const void* K, int64_t k_rs,
+                                                   const void* Vt, int64_t tk_pad, void* O, int64_t o_rs,
+                                                   const void* gate, int64_t gate_rs, int64_t Tq, int64_t Tk,
+                                                   int64_t H, int64_t head_dim, float scale, int64_t splits,
+                                                   void* stream) {
+  if (splits < 1 || splits > 256) return LTX_ERR_INVALID_ARG;
+  const int64_t need = ltx_attn_splitkv_workspace_bytes(Tq, H, head_dim, splits);
+  if (need < 0) return LTX_ERR_INVALID_ARG;
+  if (need > LTX_ATTN_NOALLOC_SCRATCH_BYTES) return LTX_ERR_SCRATCH_LIMIT;
+  void* ws = nullptr;
+  const int st = scratch_on_stream_device((hipStream_t)stream, &ws);
+  if (st != LTX_OK) return st;
+  return ltx_flash_attn_splitkv_bf16(Q, q_rs, K, k_rs, Vt, tk_pad, O, o_rs, gate, gate_rs, Tq, Tk, H,
+                                     head_dim, scale, splits, ws, LTX_ATTN_NOALLOC_SCRATCH_BYTES, stream);
 }

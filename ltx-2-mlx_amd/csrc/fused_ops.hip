@@ -443,6 +443,7 @@ extern "C" const char* ltx_status_string(int status) {
     case LTX_ERR_UNSUPPORTED: return "unsupported shape";
     case LTX_ERR_HIP: return "HIP launch error";
     case LTX_ERR_ALIGNMENT: return "pointer or stride not 16-byte aligned";
+    case LTX_ERR_SCRATCH_LIMIT: return "request exceeds the fixed scratch of a no-allocation entry point";
     default: return "unknown status";
   }
 }

@@ -55,6 +55,8 @@ SIGNATURES: dict[str, list] = {
     "ltx_flash_attn_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _vp],
     "ltx_flash_attn_splitkv_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64,
                                     _f32, _i64, _vp, _i64, _vp],
+    "ltx_flash_attn_splitkv_noalloc_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64,
+                                            _i64, _i64, _f32, _i64, _vp],
     "ltx_broadcast_add_f32": [_vp, _vp, _vp, _i64, _i64, _vp],
     "ltx_x0_from_velocity_f32": [_vp, _vp, _f32, _vp, _i64, _vp],
     "ltx_guidance_f32": [_vp, _vp, _vp, _vp, _f32, _f32, _f32, _vp, _vp, _vp, _i64, _int, _vp],
@@ -81,6 +83,9 @@ GEMM_TILE_128 = 2 << 8
 GEMM_TILE_256_DMA = 3 << 8
 GEMM_TILE_256x128 = 4 << 8
 GEMM_ROUND_THEN_BIAS = 1 << 12
+# Status of a request above the fixed scratch of a no-allocation entry point
+ERR_SCRATCH_LIMIT = -5
+ATTN_NOALLOC_SCRATCH_BYTES = 32 << 20
 
 _LIB: ctypes.CDLL | None = None
 
