@@ -18,15 +18,28 @@ Prints ONE JSON line.  Besides ms/step and tokens/s it carries:
                 ``traffic`` = HBM bytes per launch from the rocprofv3
                 FETCH_SIZE / WRITE_SIZE summary committed in profiles/ for
                 this kernel and weight format (null when none matches);
+  gemm_step     every GEMM launch of those eager steps timed the same way,
+                per stream: flops / summed launch time (the audio stream's
+                launches overlap the video stream's, so their times include
+                sharing the chip); ff_up_mfma_pct is the roofline kernel alone;
+  gemm_shapes   the block's projection shapes at M=3456 (Q/K/V/out 4096x4096
+                x4, FF up 4096->16384, FF down 16384->4096) in int8 W8A16 and
+                MXFP8, each launch replayed from a HIP graph: ms, TFLOP/s and
+                fraction of the bf16 MFMA peak (the MFMAs are bf16);
   fused_ops     HBM GB/s of adaln_norm_fused / gated_add_fused at the
-                reference's test shape (T=14640, C=4096) over a >512 MB buffer
-                rotation (no Infinity-Cache reuse), launches replayed from a
-                HIP graph (kernel time, not host dispatch);
+                reference's test shape (T=14640, C=4096) and at 1296 tokens
+                (512x288x65), inputs and outputs rotating through >= 1.5 GB
+                (no Infinity-Cache reuse), launches replayed from a HIP graph
+                (kernel time, not host dispatch);
+  config5       ms per step of the same 48-block model at 768x512x121 (6144
+                video + 121 audio + 256 text tokens), the eight distilled
+                steps replayed as HIP graphs;
   guided_step   ms per step of the CFG/STG guided loop (three transformer
                 passes: positive, negative prompt, STG-perturbed; CFG-star and
                 STG guidance; Euler), eager launches;
   cpu_baseline  the oracle (CPU restatement of the reference block) timed on
-                this host for one AV block at the same shapes, x48.
+                this host for one AV block at the same shapes (1 warmup + 5
+                timed runs; mean and p50), x48.
 """
 
 from __future__ import annotations
@@ -67,6 +80,9 @@ def parse_args(argv=None):
                     help="also time this many CFG-star + STG guided steps (3 passes each, eager); 0 skips")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-fused-bench", action="store_true")
+    ap.add_argument("--no-config5", action="store_true", help="skip the 768x512x121 leg")
+    ap.add_argument("--no-gemm-shapes", action="store_true", help="skip the per-shape GEMM leg")
+    ap.add_argument("--cpu-runs", type=int, default=5, help="timed oracle block runs after one warmup")
     ap.add_argument("--counter-workload", choices=["ff-up", "ff-up-vs-library", "copy"], default=None,
                     help="run only a short workload for rocprofv3 --pmc passes and exit: the video FF "
                          "up-projection GEMM (4 launches, --weights format) or a 1 GiB device copy (3 "
@@ -141,14 +157,13 @@ def measured_traffic(kernel: str, weights: str):
     return None
 
 
-def fused_op_bandwidth(torch):
-    """adaln / gated_add HBM GB/s at T=14640, C=4096: the kernels launched
-    through their row-view launchers on preallocated buffers, inputs and
-    outputs each rotating through >= 1.5 GB so neither operand can be served
-    from the 256 MB last-level cache."""
+def fused_op_bandwidth(torch, T=14640, C=4096):
+    """adaln / gated_add HBM GB/s at (T, C): the kernels launched through
+    their row-view launchers on preallocated buffers, inputs and outputs each
+    rotating through >= 1.5 GB so neither operand can be served from the
+    256 MB last-level cache."""
     from ltx_amd.kernels.fused_ops import adaln_rows, gated_add_rows
 
-    T, C = 14640, 4096
     nbytes = T * C * 2
     nbuf = max(2, math.ceil(1.5e9 / nbytes))
     xs = [torch.randn((T, C), device="cuda").bfloat16() for _ in range(nbuf)]
@@ -167,8 +182,8 @@ def fused_op_bandwidth(torch):
         for i in range(nbuf):
             fn(i)
         torch.cuda.synchronize()
-        # replayed from a HIP graph so host dispatch does not pace the ~45 us kernels
-        iters = 8 * nbuf
+        # replayed from a HIP graph so host dispatch does not pace the short kernels
+        iters = max(8 * nbuf, 256)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             for i in range(iters):
@@ -190,8 +205,9 @@ def fused_op_bandwidth(torch):
     return res
 
 
-def cpu_baseline(tv: int, ta: int, s: int, layers: int, grid):
-    """Oracle AV block at full shapes on the host, x layers."""
+def cpu_baseline(tv: int, ta: int, s: int, layers: int, grid, runs: int = 5):
+    """Oracle AV block at full shapes on the host (one warmup, then ``runs``
+    timed runs), x layers."""
     import torch
 
     from oracle import block as ob
@@ -228,13 +244,146 @@ def cpu_baseline(tv: int, ta: int, s: int, layers: int, grid):
     vx, ax = rnd(tv, 4096, std=1.0), rnd(ta, 2048, std=1.0)
     vctx, actx = rnd(s, 4096, std=1.0), rnd(s, 2048, std=1.0)
     vada, aada = torch.randn(16, 4096, generator=g) * 0.05, torch.randn(16, 2048, generator=g) * 0.05
-    t0 = time.perf_counter()
-    ob.block(W, vx, ax, vada, aada, vctx, actx, *pes)
-    dt = time.perf_counter() - t0
-    return {"value": round(dt * layers * 1e3, 1), "unit": "ms/step", "cores": threads, "kind": "port",
+    ob.block(W, vx, ax, vada, aada, vctx, actx, *pes)  # warmup
+    times = []
+    for _ in range(max(1, runs)):
+        t0 = time.perf_counter()
+        ob.block(W, vx, ax, vada, aada, vctx, actx, *pes)
+        times.append(time.perf_counter() - t0)
+    mean, p50 = sum(times) / len(times), sorted(times)[len(times) // 2]
+    return {"value": round(mean * layers * 1e3, 1), "unit": "ms/step", "cores": threads, "kind": "port",
+            "p50": round(p50 * layers * 1e3, 1), "runs": len(times),
             "sample": f"one AV block (oracle, torch-CPU fp32 with the reference's bf16 roundings) at "
-                      f"{tv} video + {ta} audio + {s} text tokens, timed once ({dt:.2f} s) and x{layers} blocks; "
-                      f"the reference's own MLX CPU backend is not installable here"}
+                      f"{tv} video + {ta} audio + {s} text tokens: 1 warmup + {len(times)} timed runs "
+                      f"(mean {mean:.2f} s, p50 {p50:.2f} s per block), x{layers} blocks; the reference's own "
+                      f"MLX CPU backend is not installable here"}
+
+
+def gemm_step_profile(run_step, steps, tv, torch):
+    """Time every GEMM launch of ``steps`` eager steps with events recorded on
+    its own stream around the launch.  Returns (FF-up launch durations in ms,
+    per-stream summary)."""
+    from ltx_amd.kernels import gemm
+
+    recs = []
+    main = torch.cuda.current_stream().cuda_stream
+
+    def hook(phase, info):
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()
+        if phase == "pre":
+            recs.append([info, torch.cuda.current_stream().cuda_stream, e, None])
+        else:
+            recs[-1][3] = e
+
+    gemm.LAUNCH_HOOK = hook
+    try:
+        for i in range(steps):
+            run_step(i)
+        torch.cuda.synchronize()
+    finally:
+        gemm.LAUNCH_HOOK = None
+    ff_up, groups = [], {}
+    for (kind, m, n, k, epi), stream, pre, post in recs:
+        ms = pre.elapsed_time(post)
+        if epi == gemm.EPI_GELU and m == tv and k == 4096:
+            ff_up.append(ms)
+        g = groups.setdefault("video_stream" if stream == main else "audio_stream", [0, 0.0, 0.0])
+        g[0] += 1
+        g[1] += 2.0 * m * n * k
+        g[2] += ms
+    summary = {}
+    tot = [0, 0.0, 0.0]
+    for name, (cnt, fl, ms) in groups.items():
+        tot = [tot[0] + cnt, tot[1] + fl, tot[2] + ms]
+        summary[name] = {"launches_per_step": cnt // steps, "gflop_per_step": round(fl / steps / 1e9, 1),
+                         "ms_per_step": round(ms / steps, 3),
+                         "tflops": round(fl / (ms * 1e-3) / 1e12, 1),
+                         "frac_bf16_peak": round(fl / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+    summary["all"] = {"gflop_per_step": round(tot[1] / steps / 1e9, 1), "ms_per_step": round(tot[2] / steps, 3),
+                      "tflops": round(tot[1] / (tot[2] * 1e-3) / 1e12, 1),
+                      "frac_bf16_peak": round(tot[1] / (tot[2] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+    return ff_up, summary
+
+
+def gemm_shapes(torch, fmt: str, m: int = 3456) -> dict:
+    """The block's projection GEMMs at M rows in one weight format: each shape
+    launched 10 times from a HIP graph, best of three replays."""
+    from ltx_amd.kernels import gemm
+
+    g = torch.Generator(device="cuda").manual_seed(0)
+    shapes = (("qkv_out_4096x4096", 4096, 4096, 4), ("ff_up_4096x16384", 4096, 16384, 1),
+              ("ff_down_16384x4096", 16384, 4096, 1))
+    res, tot_ms, tot_fl = {}, 0.0, 0.0
+    for name, k, n, count in shapes:
+        x = torch.randn((m, k), generator=g, device="cuda").bfloat16()
+        w = (torch.randn((n, k), generator=g, device="cuda") * 0.02).bfloat16()
+        wt = gemm.make_weight(w, torch.zeros(n, device="cuda"), kind=fmt)
+        out = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+        gemm.linear(x, wt, out=out)
+        torch.cuda.synchronize()
+        iters = 10
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(iters):
+                gemm.linear(x, wt, out=out)
+        graph.replay()
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(3):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            graph.replay()
+            b.record()
+            torch.cuda.synchronize()
+            best = min(best, a.elapsed_time(b) / iters)
+        fl = 2.0 * m * n * k
+        res[name] = {"ms": round(best, 4), "tflops": round(fl / (best * 1e-3) / 1e12, 1),
+                     "frac_bf16_peak": round(fl / (best * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4), "per_block": count}
+        tot_ms += best * count
+        tot_fl += fl * count
+        del graph, x, w, wt, out
+    res["block_total"] = {"ms": round(tot_ms, 4), "gflop": round(tot_fl / 1e9, 1),
+                          "tflops": round(tot_fl / (tot_ms * 1e-3) / 1e12, 1),
+                          "frac_bf16_peak": round(tot_fl / (tot_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+    return res
+
+
+def config5_leg(model, torch, steps_timed: int = 16) -> dict:
+    """ms per step at 768x512x121: 6144 video + 121 audio + 256 text tokens,
+    the eight distilled steps captured as HIP graphs, one full warmup pass,
+    then ``steps_timed`` steps."""
+    from ltx_amd.pipeline import DenoiseState, denoise_step
+
+    st = DenoiseState(model, 512, 768, 121, text_tokens=256, audio_frames=121, seed=0)
+    pes = model.rope(st.video_positions, st.audio_positions)
+    nsig = len(st.sigmas) - 1
+    denoise_step(model, st, 0, pes)
+    torch.cuda.synchronize()
+    pool = torch.cuda.graph_pool_handle()
+    graphs = []
+    for i in range(nsig):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, pool=pool):
+            denoise_step(model, st, i, pes)
+        graphs.append(g)
+    for i in range(nsig):
+        graphs[i].replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps_timed):
+        graphs[i % nsig].replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / steps_timed * 1e3
+    finite = bool(torch.isfinite(st.video_latent.float()).all() and torch.isfinite(st.audio_latent.float()).all())
+    del graphs
+    tv, ta = st.video_tokens, st.audio_tokens
+    fl = step_flops(tv, ta, 256, model.num_layers)
+    return {"ms_per_step": round(ms, 3), "steps": steps_timed, "timing": "hip-graph replay",
+            "workload": f"{model.num_layers}-block AV denoise step at 768x512x121",
+            "video_tokens": tv, "audio_tokens": ta, "text_tokens": 256,
+            "tokens_per_s": round((tv + ta) / (ms * 1e-3), 1), "step_tflop": round(fl / 1e12, 2),
+            "step_tflops_achieved": round(fl / (ms * 1e-3) / 1e12, 1), "latents_finite": finite}
 
 
 def guided_step_ms(model, args, ta: int, s: int) -> dict:
@@ -328,24 +477,9 @@ def main(argv=None):
     wall = time.perf_counter() - t_start
     ms = wall / args.steps * 1e3
 
-    # dominant kernel: FF up-projection GEMM, timed with stream events in eager steps
-    ev = []
-
-    def hook(phase, info):
-        kind, m, n, k, epi = info
-        if epi == gemm.EPI_GELU and m == tv and k == 4096:
-            e = torch.cuda.Event(enable_timing=True)
-            e.record()
-            ev.append(e)
-
-    gemm.LAUNCH_HOOK = hook
-    try:
-        for i in range(args.kernel_steps):
-            run_step(i)
-        torch.cuda.synchronize()
-    finally:
-        gemm.LAUNCH_HOOK = None
-    durs = [ev[j].elapsed_time(ev[j + 1]) for j in range(0, len(ev), 2)]
+    # dominant kernel (FF up-projection GEMM) and every other GEMM, timed with
+    # stream events in eager steps
+    durs, gemm_step = gemm_step_profile(run_step, args.kernel_steps, tv, torch)
     k_ms = sum(durs) / len(durs)
     k_flop = 2.0 * tv * 4096 * 16384
     achieved = k_flop / (k_ms * 1e-3) / 1e12
@@ -367,19 +501,30 @@ def main(argv=None):
                    "weights": args.weights, "timing": "hip-graph replay" if graphs else "eager"},
         "tokens_per_s": round((tv + ta) / (ms * 1e-3), 1),
         "step_tflop": round(flops / 1e12, 2), "step_tflops_achieved": round(flops / (ms * 1e-3) / 1e12, 1),
-        "gemm_mfma_pct": round(100 * achieved / PEAK_BF16_TFLOPS, 1),
+        "ff_up_mfma_pct": round(100 * achieved / PEAK_BF16_TFLOPS, 1),
+        "gemm_mfma_pct_step": round(100 * gemm_step["all"]["frac_bf16_peak"], 1),
         "roofline": roofline,
+        "gemm_step": gemm_step,
     }
-    if not args.no_fused_bench or args.guided_steps > 0:
-        del graphs
+    del graphs
+    if not args.no_config5 and args.layers == 48:
+        print("# config 5: 768x512x121 graphs", file=sys.stderr, flush=True)
+        out["config5"] = config5_leg(model, torch)
     if args.guided_steps > 0:
         out["guided_step"] = guided_step_ms(model, args, ta, s)
+    del model, state
+    torch.cuda.empty_cache()
+    if not args.no_gemm_shapes:
+        print("# projection GEMM shapes at M=3456", file=sys.stderr, flush=True)
+        out["gemm_shapes"] = {fmt: gemm_shapes(torch, fmt) for fmt in ("int8", "mxfp8")}
     if not args.no_fused_bench:
+        print("# fused ops", file=sys.stderr, flush=True)
         out["fused_ops"] = fused_op_bandwidth(torch)
+        out["fused_ops"]["config1_T1296"] = fused_op_bandwidth(torch, T=1296)
     if not args.no_cpu_baseline:
         sys.path.insert(0, str(ROOT))
         print("# cpu baseline (oracle block on host cores) ...", file=sys.stderr, flush=True)
-        out["cpu_baseline"] = cpu_baseline(tv, ta, s, args.layers, grid)
+        out["cpu_baseline"] = cpu_baseline(tv, ta, s, args.layers, grid, runs=args.cpu_runs)
     print(json.dumps(out), flush=True)
     return 0
 
