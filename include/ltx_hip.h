@@ -184,7 +184,7 @@ int ltx_broadcast_add_f32(const float* table, const float* vec, float* out, int6
  * Requirements: K % 64 == 0, N % 8 == 0, 16-byte aligned pointers and row
  * strides; MXFP8 scales 4-byte aligned with ld_scale % 4 == 0.  `epilogue` is
  * one of LTX_GEMM_EPI_* optionally OR-ed with a tile override
- * (LTX_GEMM_TILE_256 / _128 / _256_DMA / _256x128; default: by problem size).
+ * (LTX_GEMM_TILE_256 / _128 / _256_DMA / _256x128 / _G8; default: by problem size).
  * With LTX_GEMM_EPI_BIAS, output columns n >= sigmoid_from get the head-gate
  * epilogue of LTX_GEMM_EPI_SIGMOID2 instead (pass N for none): the per-head
  * gate logits ride along with the Q / QKV projection in one GEMM.
@@ -200,6 +200,11 @@ int ltx_broadcast_add_f32(const float* table, const float* vec, float* out, int6
 #define LTX_GEMM_TILE_128 (2 << 8)
 #define LTX_GEMM_TILE_256_DMA (3 << 8) /* 256x256, LDS-DMA loader */
 #define LTX_GEMM_TILE_256x128 (4 << 8) /* 256 rows x 128 columns */
+/* 256x256, eight waves in two groups that alternate between global->LDS
+ * loads / fragment reads and MFMAs; 8-bit weights only (int8, and MXFP8 with
+ * K % 512 == 0 and 16-byte aligned scale rows), else LTX_ERR_UNSUPPORTED.
+ * The default for MXFP8 weights when 256x256 tiles are chosen. */
+#define LTX_GEMM_TILE_G8 (5 << 8)
 /* OR-ed into `epilogue`: the bias is added to the bf16-rounded product,
  * acc' = bf16(acc) + bias, before the epilogue's own steps -- the
  * quantised-linear form `quantized_matmul(x, w) + bias` of nn.QuantizedLinear

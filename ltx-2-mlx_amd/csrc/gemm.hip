@@ -762,6 +762,413 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
   }
 }
 
+// ---- 8-wave ping-pong kernel for 8-bit weights ------------------------------
+// 256x256 tile, K step 64, eight waves (two per SIMD) in two groups of four:
+// group 0 (waves 0-3) owns output rows 0-127 of the tile, group 1 (waves 4-7)
+// rows 128-255; wave w & 3 owns 64 output columns.  The groups run half a
+// stage apart: while one group issues its memory cluster (LDS fragment reads
+// of a stage, its share of the direct global->LDS loads two stages ahead, the
+// scale loads), the other group's compute cluster (the stage's 32 MFMAs with
+// the weight dequantisation interleaved) keeps the SIMD's matrix pipe busy.
+// A workgroup barrier separates the clusters.  Both operands reach LDS by
+// global_load_lds (no staging registers, no LDS write instructions): three
+// 48 KB stages of bf16 activations (256 x 128 B) and raw weight codes
+// (256 x 64 B).  The MXFP8 / int8 codes are dequantised per fragment with the
+// exact format arithmetic, so the bf16 MFMA sees bit-exact weights.
+//
+// Inside a stage the k order of the MFMA slots is permuted so that a lane
+// reads the codes of two k-steps with one 16-byte LDS read: k-step 2p+s, lane
+// half h covers k = 32p + 16h + 8s + [0, 8) for both operands (the E8M0 block
+// of that k range is p).  The sum over the stage is the same set of products.
+constexpr int kG8Threads = 512;
+// the automatic tile choice uses the 8-wave kernel for MXFP8 weights (int8
+// stays on the 4-wave kernel, whose once-per-workgroup dequantisation costs
+// less VALU than int8's per-fragment conversion)
+constexpr int kG8Stages = 3;
+
+template <int BKIND>
+struct G8Cfg {
+  static constexpr int BM = 256, BN = 256, BK = 64;
+  // MXFP8 dequantises with one conversion per two codes: 64x128 wave tiles
+  // (fewest LDS bytes per MFMA).  int8 needs ~2.5 VALU per code: 128x64, half
+  // the weight fragments per wave.
+  static constexpr int WM = BKIND == B_MXFP8 ? 64 : 128, WN = BKIND == B_MXFP8 ? 128 : 64;
+  static constexpr int TM = WM / 32, TN = WN / 32;
+  static constexpr int WAVES_M = BM / WM;
+  static constexpr int A_ROWB = BK * 2, B_ROWB = BK;  // bf16 activations, 8-bit codes
+  static constexpr int A_BYTES = BM * A_ROWB, B_BYTES = BN * B_ROWB;
+  static constexpr int STAGE = A_BYTES + B_BYTES;
+  static constexpr int A_DMA = A_BYTES / 1024 / 8, B_DMA = B_BYTES / 1024 / 8;  // per wave per stage
+  static constexpr int EPI_ROWB = WN * 2 + 16;
+  static constexpr int EPI_WAVE = WM * EPI_ROWB;
+  static constexpr int EPI_BYTES = 8 * EPI_WAVE;
+  static constexpr int LDS_BYTES = (kG8Stages * STAGE > EPI_BYTES) ? kG8Stages * STAGE : EPI_BYTES;
+  static constexpr int COL_BYTES = 2 * BN * 4;
+  // MXFP8 scales of eight stages (256 rows x 16 E8M0 bytes), double buffered
+  static constexpr int SC_OCT = BN * 16;
+  static constexpr int SC_BYTES = BKIND == B_MXFP8 ? 2 * SC_OCT : 0;
+  static_assert(LDS_BYTES + COL_BYTES + SC_BYTES <= 160 * 1024, "LDS");
+  static_assert(BKIND != B_BF16, "8-bit weights only");
+};
+
+// Workgroup barrier without the memory fence of __syncthreads(): the fence
+// would wait for every outstanding global->LDS load of the wave (they count as
+// LDS writes), including the ones meant to stay in flight across the barrier.
+// Callers wait for exactly what the barrier has to publish.
+__device__ __forceinline__ void barrier_nofence() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int BKIND, int EPI>
+__global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
+  using Cfg = G8Cfg<BKIND>;
+  constexpr int BN = Cfg::BN, WM = Cfg::WM, WN = Cfg::WN, TM = Cfg::TM, TN = Cfg::TN;
+  constexpr int A_ROWB = Cfg::A_ROWB, B_ROWB = Cfg::B_ROWB, A_BYTES = Cfg::A_BYTES, STAGE = Cfg::STAGE;
+  constexpr int A_DMA = Cfg::A_DMA, B_DMA = Cfg::B_DMA;
+  constexpr int EPI_ROWB = Cfg::EPI_ROWB, EPI_WAVE = Cfg::EPI_WAVE;
+  constexpr bool RESID = EPI == LTX_GEMM_EPI_RESIDUAL || EPI == LTX_GEMM_EPI_RESIDUAL_ROUND;
+  __shared__ __attribute__((aligned(1024))) char lds[Cfg::LDS_BYTES + Cfg::COL_BYTES + Cfg::SC_BYTES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int grp = wave >> 2;  // waves w and w + 4 share a SIMD
+  const int wm = wave % Cfg::WAVES_M, wn = wave / Cfg::WAVES_M;
+
+  int tmi, tni;
+  tile_coords((int)blockIdx.x, (int)gridDim.x, p.tiles_m, p.tiles_n, tmi, tni);
+  const int m0 = tmi * Cfg::BM, n0 = tni * BN;
+  const int KT = p.K / Cfg::BK;
+
+  float* col_lds = reinterpret_cast<float*>(lds + Cfg::LDS_BYTES);
+
+  // ---- direct-load sources.  A wave instruction fills one contiguous 1 KiB
+  // block of LDS, lane j its 16-byte slot j; the lane's source address picks
+  // the logical chunk that the slot holds under the XOR swizzle: 128-byte A
+  // rows (8 per block) use chunk ^ ((row / 2) % 8), 64-byte code rows (16 per
+  // block) chunk ^ ((row / 4) % 4); each conflict-free for 16 lanes reading
+  // one chunk of 16 consecutive rows.  Rows past M / N re-read the last row.
+  // 32-bit byte offsets from the operand bases (launch_g8 checks they fit),
+  // so each load takes a scalar base and one offset register
+  const char* const a_base = (const char*)p.A;
+  const char* const b_base = (const char*)p.B;
+  uint32_t a_src[A_DMA];
+#pragma unroll
+  for (int d = 0; d < A_DMA; ++d) {
+    const int r = 8 * (8 * d + wave) + (lane >> 3);
+    int gm = m0 + r;
+    gm = gm < p.M ? gm : p.M - 1;
+    const int chunk = (lane & 7) ^ ((r >> 1) & 7);
+    a_src[d] = (uint32_t)((int64_t)gm * p.lda * 2) + chunk * 16;
+  }
+  uint32_t b_src[B_DMA];
+#pragma unroll
+  for (int d = 0; d < B_DMA; ++d) {
+    const int r = 16 * (8 * d + wave) + (lane >> 2);
+    int gn = n0 + r;
+    gn = gn < p.N ? gn : p.N - 1;
+    const int chunk = (lane & 3) ^ ((r >> 2) & 3);
+    b_src[d] = (uint32_t)((int64_t)gn * p.ldb) + chunk * 16;
+  }
+  auto dma_stage = [&](int kt, int buf) {
+    char* As = lds + buf * STAGE;
+    const char* ak = a_base + (int64_t)kt * (Cfg::BK * 2);
+    const char* bk = b_base + (int64_t)kt * Cfg::BK;
+#pragma unroll
+    for (int d = 0; d < A_DMA; ++d) dma16(ak + a_src[d], As + (8 * d + wave) * 1024);
+#pragma unroll
+    for (int d = 0; d < B_DMA; ++d) dma16(bk + b_src[d], As + A_BYTES + (8 * d + wave) * 1024);
+  };
+
+  // ---- per-lane fragment coordinates and weight scales
+  const int fr = lane & 31, h = lane >> 5;
+  int a_off[TM], b_off[TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) a_off[i] = (wm * WM + i * 32 + fr) * A_ROWB;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) b_off[j] = (wn * WN + j * 32 + fr) * B_ROWB;
+  const int a_swz = (fr >> 1) & 7;  // rows i*32 + fr share it
+  const int b_swz = (fr >> 2) & 3;
+  // MXFP8 scales reach LDS by direct loads too, eight stages at a time: the
+  // loop then holds no register-destined global load, whose first use would
+  // make the compiler wait for every load in flight (its wait counting does
+  // not see the direct loads).  Octet o of a tile is 256 weight rows x 16
+  // bytes (the E8M0 of k-blocks 16o..16o+15, i.e. stages 8o..8o+7), laid out
+  // [row][16]; waves 0-3 each move 64 rows per octet.  int8: the row scale
+  // in a register.
+  const uint8_t* const sc_base = (const uint8_t*)p.bscale;
+  char* const sc_lds = lds + Cfg::LDS_BYTES + Cfg::COL_BYTES;
+  uint32_t sc_src = 0;
+  {
+    int gn = n0 + (wave & 3) * 64 + lane;
+    gn = gn < p.N ? gn : p.N - 1;
+    sc_src = (uint32_t)((int64_t)gn * p.ld_scale);
+  }
+  const int noct = KT >> 3;
+  auto dma_scales = [&](int oct) {
+    if constexpr (BKIND == B_MXFP8) {
+      if (grp == 0) {
+        oct = oct < noct ? oct : noct - 1;  // past the end: re-read the last octet
+        dma16(sc_base + oct * 16 + sc_src, sc_lds + (oct & 1) * Cfg::SC_OCT + wave * 1024);
+      }
+    }
+  };
+  float s_i8[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    int gn = n0 + wn * WN + j * 32 + fr;
+    gn = gn < p.N ? gn : p.N - 1;
+    if (BKIND == B_INT8) s_i8[j] = ((const float*)p.bscale)[gn];
+  }
+  uint32_t scw[TN];  // this stage pair's E8M0 bytes of the lane's weight rows
+  // global memory instructions of a stage's first memory cluster: the direct
+  // loads of stage kt+2, plus (group 0, MXFP8) the scales in the first stage
+  // of an octet
+  constexpr int VM_DMA = A_DMA + B_DMA;
+  constexpr int VM_SCALES = BKIND == B_MXFP8 ? 1 : 0;
+
+  bf16x8 fa[4][TM];  // A fragments of the stage's four k-steps
+  u32x4 fb[2][TN];   // weight codes of the stage's two k-step pairs (16 per lane)
+  auto read_stage = [&](int kt) {
+    const char* As = lds + (kt % kG8Stages) * STAGE;
+    const char* Bs = As + A_BYTES;
+    if constexpr (BKIND == B_MXFP8) {
+      const char* sa = sc_lds + ((kt >> 3) & 1) * Cfg::SC_OCT + ((kt & 7) >> 1) * 4;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) scw[j] = *reinterpret_cast<const uint32_t*>(sa + (wn * WN + j * 32 + fr) * 16);
+    }
+#pragma unroll
+    for (int pp = 0; pp < 2; ++pp) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        fb[pp][j] = *reinterpret_cast<const u32x4*>(Bs + b_off[j] + (((2 * pp + h) ^ b_swz) * 16));
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          fa[2 * pp + s][i] =
+              *reinterpret_cast<const bf16x8*>(As + a_off[i] + (((4 * pp + 2 * h + s) ^ a_swz) * 16));
+    }
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  // codes of one k-step (two 4-byte words) -> bf16 fragment
+  auto dequant = [&](uint32_t w0, uint32_t w1, float sc) -> bf16x8 {
+    uint32_t o[4];
+    if constexpr (BKIND == B_MXFP8) {
+      o[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, sc, false));
+      o[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, sc, true));
+      o[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, sc, false));
+      o[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, sc, true));
+    } else {
+      const float nb = -128.0f * sc;
+      const uint32_t ws[2] = {w0 ^ 0x80808080u, w1 ^ 0x80808080u};
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        const uint32_t u = ws[d];
+        bf16x2 p0, p1;
+        p0[0] = (bf16)fmaf((float)(u & 0xffu), sc, nb);
+        p0[1] = (bf16)fmaf((float)((u >> 8) & 0xffu), sc, nb);
+        p1[0] = (bf16)fmaf((float)((u >> 16) & 0xffu), sc, nb);
+        p1[1] = (bf16)fmaf((float)(u >> 24), sc, nb);
+        o[2 * d] = __builtin_bit_cast(uint32_t, p0);
+        o[2 * d + 1] = __builtin_bit_cast(uint32_t, p1);
+      }
+    }
+    return __builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]});
+  };
+
+  // compute cluster of stage kt: 4 k-steps x TN x TM MFMAs, each weight
+  // fragment dequantised right before its MFMAs (the compiler hoists the
+  // conversions of the next fragment under the current MFMAs)
+  auto compute_stage = [&](int kt) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int pp = kk >> 1, s = kk & 1;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        float sc;
+        if constexpr (BKIND == B_MXFP8)
+          sc = e8m0_to_f32((scw[j] >> (16 * (kt & 1) + 8 * pp)) & 0xffu);
+        else
+          sc = s_i8[j];
+        const bf16x8 b = dequant(fb[pp][j][2 * s], fb[pp][j][2 * s + 1], sc);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, fa[kk][i], acc[i][j], 0, 0, 0);
+      }
+    }
+  };
+
+  // ---- prologue: scales of octet 0, stages 0 and 1 in flight, then one
+  // barrier for all waves
+  dma_scales(0);
+  dma_stage(0, 0);
+  if (KT > 1) dma_stage(1, 1);
+  wait_vmcnt<0>();
+  __syncthreads();
+  if (grp == 1) barrier_nofence();  // group 1 runs half a stage behind
+
+  // Clusters are whole stages.  Stage s is first read by group 0's memory
+  // cluster of stage s (global half-stage 2s), so its data must be in LDS by
+  // the barrier before it.  The direct loads of stage s are issued in the
+  // memory clusters of stage s-2; each group waits for them in its last
+  // cluster before that barrier -- group 0 at the end of its compute cluster
+  // of stage s-1, group 1 at the end of its memory cluster of stage s-1 --
+  // leaving only that stage's own loads in flight.  Past the last stage the
+  // direct loads re-read stage KT-1 into the buffer nobody reads any more,
+  // so every stage issues the same loads and the waits are exact.  The scales
+  // of octet o+1 go out (group 0) with stage 8o's loads.
+  // SUB = kt % 8 (compile-time in the unrolled loop).
+  auto stage_iter = [&](int kt, auto sub) {
+    constexpr int SUB = decltype(sub)::value;
+    constexpr int VM = VM_DMA + (SUB == 0 ? VM_SCALES : 0);  // group 0; group 1 issues no scales
+    // memory cluster
+    if (SUB == 0) dma_scales((kt >> 3) + 1);
+    dma_stage(kt + 2 < KT ? kt + 2 : KT - 1, (kt + 2) % kG8Stages);
+    read_stage(kt);
+    wait_lgkmcnt0();
+    if (grp == 1) wait_vmcnt<VM_DMA>();
+    barrier_nofence();
+    // compute cluster
+    __builtin_amdgcn_s_setprio(1);
+    compute_stage(kt);
+    __builtin_amdgcn_s_setprio(0);
+    if (grp == 0) wait_vmcnt<VM>();
+    barrier_nofence();
+  };
+  int kt = 0;
+  for (; kt + 7 < KT; kt += 8) {
+    stage_iter(kt, std::integral_constant<int, 0>{});
+    stage_iter(kt + 1, std::integral_constant<int, 1>{});
+    stage_iter(kt + 2, std::integral_constant<int, 2>{});
+    stage_iter(kt + 3, std::integral_constant<int, 3>{});
+    stage_iter(kt + 4, std::integral_constant<int, 4>{});
+    stage_iter(kt + 5, std::integral_constant<int, 5>{});
+    stage_iter(kt + 6, std::integral_constant<int, 6>{});
+    stage_iter(kt + 7, std::integral_constant<int, 7>{});
+  }
+  // int8 only (MXFP8 takes K % 512 == 0): the last KT % 8 stages
+  for (; kt < KT; ++kt) stage_iter(kt, std::integral_constant<int, 1>{});
+  if (grp == 0) barrier_nofence();
+  wait_vmcnt<0>();
+
+  // ---- epilogue (every wave is past its last LDS fragment read)
+  if (tid < BN) {
+    float col_bias = 0.0f, col_gate = 0.0f;
+    if (n0 + tid < p.N) {
+      if (p.bias) col_bias = p.bias[n0 + tid];
+      if (RESID) col_gate = p.gate[n0 + tid];
+    }
+    col_lds[tid] = col_bias;
+    col_lds[BN + tid] = col_gate;
+  }
+  __syncthreads();
+  constexpr int CHUNKS = WN / 8;
+  constexpr int ROWS_PER_IT = 64 / CHUNKS;
+  constexpr int ITS = WM / ROWS_PER_IT;
+  const int ch = lane % CHUNKS;
+  const int rsub = lane / CHUNKS;
+  const int gn2 = n0 + wn * WN + ch * 8;
+  const bool col_ok = gn2 < p.N;
+  char* E = lds + wave * EPI_WAVE;
+  auto phase1 = [&](auto sig_tag, auto rtb_tag) {
+    constexpr bool SIG = decltype(sig_tag)::value;
+    constexpr bool RTB = decltype(rtb_tag)::value;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int nl = j * 32 + 8 * g + 4 * h;
+        const int gn = n0 + wn * WN + nl;
+        const f32x4 bias4 = *reinterpret_cast<const f32x4*>(col_lds + wn * WN + nl);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          float y[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float a = acc[i][j][4 * g + e];
+            y[e] = (RTB ? round_bf(a) : a) + bias4[e];
+            if (EPI == LTX_GEMM_EPI_GELU) y[e] = gelu_tanh(round_bf(y[e]));
+            if (EPI == LTX_GEMM_EPI_SIGMOID2) y[e] = sigmoid2_bf(round_bf(y[e]));
+            if (SIG && gn + e >= p.sig_from) y[e] = sigmoid2_bf(round_bf(y[e]));
+          }
+          bf16x4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = (bf16)y[e];
+          *reinterpret_cast<bf16x4*>(E + (i * 32 + fr) * EPI_ROWB + nl * 2) = v;
+        }
+      }
+    }
+  };
+  const bool sig = EPI == LTX_GEMM_EPI_BIAS && n0 + wn * WN + WN > p.sig_from;
+  if (p.round_then_bias) {
+    if (sig) phase1(std::true_type{}, std::true_type{});
+    else phase1(std::false_type{}, std::true_type{});
+  } else {
+    if (sig) phase1(std::true_type{}, std::false_type{});
+    else phase1(std::false_type{}, std::false_type{});
+  }
+  // residual rows after the accumulators are in LDS (fewer live registers);
+  // every residual element of the tile is read before its output is written
+  bf16x8 res[RESID ? ITS : 1];
+  if constexpr (RESID) {
+    const int gnc = col_ok ? gn2 : 0;
+#pragma unroll
+    for (int it = 0; it < ITS; ++it) {
+      int gm = m0 + wm * WM + it * ROWS_PER_IT + rsub;
+      gm = gm < p.M ? gm : p.M - 1;
+      res[it] = *reinterpret_cast<const bf16x8*>(p.R + (int64_t)gm * p.ldr + gnc);
+    }
+  }
+  __syncthreads();
+  float g8[8];
+  if constexpr (RESID) {
+    const f32x4 ga = *reinterpret_cast<const f32x4*>(col_lds + BN + wn * WN + ch * 8);
+    const f32x4 gb = *reinterpret_cast<const f32x4*>(col_lds + BN + wn * WN + ch * 8 + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      g8[e] = ga[e];
+      g8[4 + e] = gb[e];
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < ITS; ++it) {
+    const int ml = it * ROWS_PER_IT + rsub;
+    const int gm = m0 + wm * WM + ml;
+    bf16x8 v = *reinterpret_cast<const bf16x8*>(E + ml * EPI_ROWB + ch * 16);
+    if constexpr (RESID) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float y = (float)v[e];
+        float o;
+        if (EPI == LTX_GEMM_EPI_RESIDUAL)
+          o = fmaf(g8[e], y, (float)res[it][e]);
+        else
+          o = round_bf(y * g8[e]) + (float)res[it][e];
+        v[e] = (bf16)o;
+      }
+    }
+    if (gm < p.M && col_ok) *reinterpret_cast<bf16x8*>(p.C + (int64_t)gm * p.ldc + gn2) = v;
+  }
+}
+
+template <int BKIND, int EPI>
+static void launch_g8(GemmArgs p, hipStream_t s) {
+  p.tiles_m = (p.M + 255) / 256;
+  p.tiles_n = (p.N + 255) / 256;
+  gemm8_kernel<BKIND, EPI><<<p.tiles_m * p.tiles_n, kG8Threads, 0, s>>>(p);
+}
+
 template <int BM, int BN, int BK, int STAGES, int BKIND, int EPI, int SWZ = 0, int LOADER = LOAD_DMA>
 static void launch_tile(GemmArgs p, hipStream_t s) {
   p.tiles_m = (p.M + BM - 1) / BM;
@@ -769,17 +1176,41 @@ static void launch_tile(GemmArgs p, hipStream_t s) {
   gemm_kernel<BM, BN, BK, STAGES, BKIND, EPI, SWZ, LOADER><<<p.tiles_m * p.tiles_n, kGemmThreads, 0, s>>>(p);
 }
 
-// Tile shapes (all K step 64, two LDS stages): 256x256 and 128x128 with the
-// register-staged loader (1 and 2; 128x128 runs two workgroups per CU),
-// 256x256 with the LDS-DMA loader (3) and 256x128 register-staged (4).
+// Whether the 8-wave kernel takes a problem: 8-bit weights; for MXFP8 whole
+// eight-stage scale octets (K % 512) in 16-byte aligned pieces.
+template <int BKIND>
+static bool g8_ok(const GemmArgs& p) {
+  if (BKIND == B_BF16) return false;
+  // operand byte offsets are 32-bit in the kernel
+  if ((int64_t)p.M * p.lda * 2 >= ((int64_t)1 << 32) || (int64_t)p.N * p.ldb >= ((int64_t)1 << 32) ||
+      (int64_t)p.N * p.ld_scale >= ((int64_t)1 << 32))
+    return false;
+  if (BKIND == B_MXFP8)
+    return p.K % 512 == 0 && p.ld_scale % 16 == 0 && ((uintptr_t)p.bscale & 15u) == 0;
+  return true;
+}
+
+// Tile shapes (all K step 64): 256x256 and 128x128 with the register-staged
+// loader (1 and 2; 128x128 runs two workgroups per CU), 256x256 with the
+// LDS-DMA loader (3), 256x128 register-staged (4), and the 8-wave 256x256
+// kernel for 8-bit weights (5).
 template <int BKIND, int EPI>
-static void launch_epi(const GemmArgs& p, int tile, hipStream_t s) {
+static int launch_epi(const GemmArgs& p, int tile, hipStream_t s) {
   if (tile == 0) {
     // Large tiles when they still give most CUs a tile; 128x128 otherwise.
     // (256x128 tiles, 5 % faster on A2V Q alone, were 0.25 ms slower per
     // step with the audio stream sharing the CUs: explicit only.)
     const int64_t big = (int64_t)((p.M + 255) / 256) * ((p.N + 255) / 256);
-    tile = big >= 160 ? 1 : 2;
+    tile = big >= 160 ? (BKIND == B_MXFP8 && g8_ok<BKIND>(p) ? 5 : 1) : 2;
+  }
+  if (tile == 5) {
+    if constexpr (BKIND != B_BF16) {
+      if (!g8_ok<BKIND>(p)) return LTX_ERR_UNSUPPORTED;
+      launch_g8<BKIND, EPI>(p, s);
+      return LTX_OK;
+    } else {
+      return LTX_ERR_UNSUPPORTED;
+    }
   }
   if (tile == 1)
     launch_tile<256, 256, 64, 2, BKIND, EPI, 0, LOAD_REG>(p, s);
@@ -789,23 +1220,26 @@ static void launch_epi(const GemmArgs& p, int tile, hipStream_t s) {
     launch_tile<256, 128, 64, 2, BKIND, EPI, 0, LOAD_REG>(p, s);
   else
     launch_tile<256, 256, 64, 2, BKIND, EPI, 0, LOAD_DMA>(p, s);
+  return LTX_OK;
 }
 
 template <int BKIND>
 static int launch_kind(const GemmArgs& p, int epilogue, hipStream_t s) {
   const int epi = epilogue & 0xff;
   const int tile = (epilogue >> 8) & 0xf;
-  if (tile > 4) return LTX_ERR_INVALID_ARG;
+  if (tile > 5) return LTX_ERR_INVALID_ARG;
   GemmArgs q = p;
   q.round_then_bias = (epilogue & LTX_GEMM_ROUND_THEN_BIAS) != 0;
+  int st;
   switch (epi) {
-    case LTX_GEMM_EPI_BIAS: launch_epi<BKIND, LTX_GEMM_EPI_BIAS>(q, tile, s); break;
-    case LTX_GEMM_EPI_GELU: launch_epi<BKIND, LTX_GEMM_EPI_GELU>(q, tile, s); break;
-    case LTX_GEMM_EPI_RESIDUAL: launch_epi<BKIND, LTX_GEMM_EPI_RESIDUAL>(q, tile, s); break;
-    case LTX_GEMM_EPI_RESIDUAL_ROUND: launch_epi<BKIND, LTX_GEMM_EPI_RESIDUAL_ROUND>(q, tile, s); break;
-    case LTX_GEMM_EPI_SIGMOID2: launch_epi<BKIND, LTX_GEMM_EPI_SIGMOID2>(q, tile, s); break;
+    case LTX_GEMM_EPI_BIAS: st = launch_epi<BKIND, LTX_GEMM_EPI_BIAS>(q, tile, s); break;
+    case LTX_GEMM_EPI_GELU: st = launch_epi<BKIND, LTX_GEMM_EPI_GELU>(q, tile, s); break;
+    case LTX_GEMM_EPI_RESIDUAL: st = launch_epi<BKIND, LTX_GEMM_EPI_RESIDUAL>(q, tile, s); break;
+    case LTX_GEMM_EPI_RESIDUAL_ROUND: st = launch_epi<BKIND, LTX_GEMM_EPI_RESIDUAL_ROUND>(q, tile, s); break;
+    case LTX_GEMM_EPI_SIGMOID2: st = launch_epi<BKIND, LTX_GEMM_EPI_SIGMOID2>(q, tile, s); break;
     default: return LTX_ERR_INVALID_ARG;
   }
+  if (st != LTX_OK) return st;
   return ltx_launch_status();
 }
 
