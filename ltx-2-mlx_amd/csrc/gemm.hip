@@ -111,6 +111,14 @@ __device__ __forceinline__ float e8m0_to_f32(uint32_t s) {
   return __uint_as_float((s << 23) | special);
 }
 
+// The same value in vector instructions only (no lane-mask round trip):
+// 2^-127 * 2^s by ldexp -- exact, 2^-127 itself a denormal (denormals are
+// kept) -- and s = 255 (+inf from ldexp) turned into NaN by x + (x - x).
+__device__ __forceinline__ float e8m0_to_f32_valu(uint32_t s) {
+  const float x = __builtin_amdgcn_ldexpf(__uint_as_float(0x00400000u), (int)s);
+  return x + (x - x);
+}
+
 __device__ __forceinline__ void tile_coords(int bid, int nblocks, int tiles_m, int tiles_n, int& tm,
                                             int& tn) {
   // XCD-contiguous renumbering: hardware sends block b to XCD b % 8.
@@ -781,12 +789,27 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
 // half h covers k = 32p + 16h + 8s + [0, 8) for both operands (the E8M0 block
 // of that k range is p).  The sum over the stage is the same set of products.
 constexpr int kG8Threads = 512;
+// dword 3 of a raw buffer descriptor on gfx9-class GPUs (untyped, 32-bit
+// data format so that dwordx4 loads are not format-converted)
+constexpr int kBufferRsrcWord3 = 0x00020000;
+
+// 16 bytes per lane from base + voff + soff (bounded by num_records bytes) to
+// LDS at lds_dst + 16 * lane: a buffer load with the lds modifier.  The
+// descriptor is built from wave-uniform values (scalar registers; the
+// compiler hoists it out of loops).  Kept out of the kernel bodies, whose
+// host-side launch stubs are not emitted when they name the descriptor type.
+__device__ __forceinline__ void buffer_dma16(const void* base, int num_records, uint32_t voff, int soff,
+                                             char* lds_dst) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, num_records, kBufferRsrcWord3);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds_dst, 16, voff, soff, 0, 0);
+}
 // the automatic tile choice uses the 8-wave kernel for MXFP8 weights (int8
 // stays on the 4-wave kernel, whose once-per-workgroup dequantisation costs
 // less VALU than int8's per-fragment conversion)
 constexpr int kG8Stages = 3;
 
-template <int BKIND>
+template <int BKIND, int kG8Stages_ = 3>
 struct G8Cfg {
   static constexpr int BM = 256, BN = 256, BK = 64;
   // MXFP8 dequantises with one conversion per two codes: 64x128 wave tiles
@@ -798,6 +821,9 @@ struct G8Cfg {
   static constexpr int A_ROWB = BK * 2, B_ROWB = BK;  // bf16 activations, 8-bit codes
   static constexpr int A_BYTES = BM * A_ROWB, B_BYTES = BN * B_ROWB;
   static constexpr int STAGE = A_BYTES + B_BYTES;
+  // LDS: the three A stages, then the three B stages (every fragment read is
+  // then a fixed per-lane register plus an immediate offset below 64 KiB)
+  static constexpr int B_REGION = kG8Stages_ * A_BYTES;
   static constexpr int A_DMA = A_BYTES / 1024 / 8, B_DMA = B_BYTES / 1024 / 8;  // per wave per stage
   static constexpr int EPI_ROWB = WN * 2 + 16;
   static constexpr int EPI_WAVE = WM * EPI_ROWB;
@@ -825,7 +851,8 @@ template <int BKIND, int EPI>
 __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   using Cfg = G8Cfg<BKIND>;
   constexpr int BN = Cfg::BN, WM = Cfg::WM, WN = Cfg::WN, TM = Cfg::TM, TN = Cfg::TN;
-  constexpr int A_ROWB = Cfg::A_ROWB, B_ROWB = Cfg::B_ROWB, A_BYTES = Cfg::A_BYTES, STAGE = Cfg::STAGE;
+  constexpr int A_ROWB = Cfg::A_ROWB, B_ROWB = Cfg::B_ROWB, A_BYTES = Cfg::A_BYTES, B_BYTES = Cfg::B_BYTES;
+  constexpr int B_REGION = Cfg::B_REGION;
   constexpr int A_DMA = Cfg::A_DMA, B_DMA = Cfg::B_DMA;
   constexpr int EPI_ROWB = Cfg::EPI_ROWB, EPI_WAVE = Cfg::EPI_WAVE;
   constexpr bool RESID = EPI == LTX_GEMM_EPI_RESIDUAL || EPI == LTX_GEMM_EPI_RESIDUAL_ROUND;
@@ -833,7 +860,10 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // wave-uniform values live in scalar registers: the memory clusters then
+  // compute their LDS destinations and load bases with scalar instructions
+  // (vector instructions of one wave take matrix-pipe slots from the other)
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int grp = wave >> 2;  // waves w and w + 4 share a SIMD
   const int wm = wave % Cfg::WAVES_M, wn = wave / Cfg::WAVES_M;
 
@@ -850,10 +880,13 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   // rows (8 per block) use chunk ^ ((row / 2) % 8), 64-byte code rows (16 per
   // block) chunk ^ ((row / 4) % 4); each conflict-free for 16 lanes reading
   // one chunk of 16 consecutive rows.  Rows past M / N re-read the last row.
-  // 32-bit byte offsets from the operand bases (launch_g8 checks they fit),
-  // so each load takes a scalar base and one offset register
-  const char* const a_base = (const char*)p.A;
-  const char* const b_base = (const char*)p.B;
+  // Direct loads as buffer loads: a buffer descriptor per operand (scalar
+  // registers), a fixed 32-bit per-lane byte offset in one vector register,
+  // the stage's advance as the scalar offset and the LDS destination in M0
+  // -- no vector instructions per load (vector instructions of one wave take
+  // matrix-pipe slots from the other).  The descriptors' record counts bound
+  // every load to its operand (g8_ok checks the 32-bit extents).
+  const int a_records = (int)((int64_t)p.M * p.lda * 2), b_records = (int)((int64_t)p.N * p.ldb);
   uint32_t a_src[A_DMA];
 #pragma unroll
   for (int d = 0; d < A_DMA; ++d) {
@@ -873,24 +906,33 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
     b_src[d] = (uint32_t)((int64_t)gn * p.ldb) + chunk * 16;
   }
   auto dma_stage = [&](int kt, int buf) {
-    char* As = lds + buf * STAGE;
-    const char* ak = a_base + (int64_t)kt * (Cfg::BK * 2);
-    const char* bk = b_base + (int64_t)kt * Cfg::BK;
+    char* As = lds + buf * A_BYTES;
+    char* Bs = lds + B_REGION + buf * B_BYTES;
 #pragma unroll
-    for (int d = 0; d < A_DMA; ++d) dma16(ak + a_src[d], As + (8 * d + wave) * 1024);
+    for (int d = 0; d < A_DMA; ++d)
+      buffer_dma16(p.A, a_records, a_src[d], kt * (Cfg::BK * 2), As + (8 * d + wave) * 1024);
 #pragma unroll
-    for (int d = 0; d < B_DMA; ++d) dma16(bk + b_src[d], As + A_BYTES + (8 * d + wave) * 1024);
+    for (int d = 0; d < B_DMA; ++d)
+      buffer_dma16(p.B, b_records, b_src[d], kt * Cfg::BK, Bs + (8 * d + wave) * 1024);
   };
 
-  // ---- per-lane fragment coordinates and weight scales
+  // ---- per-lane fragment read bases: LDS byte addresses of the lane's first
+  // fragment for each XOR pattern -- A per (pair pp, step s) of a stage and
+  // a low / high base (stage buffers 0-1 / 1-2 within the 16-bit immediate),
+  // B per pair pp -- so that every fragment read is base + immediate
   const int fr = lane & 31, h = lane >> 5;
-  int a_off[TM], b_off[TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i) a_off[i] = (wm * WM + i * 32 + fr) * A_ROWB;
-#pragma unroll
-  for (int j = 0; j < TN; ++j) b_off[j] = (wn * WN + j * 32 + fr) * B_ROWB;
   const int a_swz = (fr >> 1) & 7;  // rows i*32 + fr share it
   const int b_swz = (fr >> 2) & 3;
+  int a_lo[4], a_hi[4], b_base[2];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int pp = v >> 1, s = v & 1;
+    a_lo[v] = (wm * WM + fr) * A_ROWB + (((4 * pp + 2 * h + s) ^ a_swz) * 16);
+    a_hi[v] = a_lo[v] + A_BYTES;
+  }
+#pragma unroll
+  for (int pp = 0; pp < 2; ++pp)
+    b_base[pp] = B_REGION + (wn * WN + fr) * B_ROWB + (((2 * pp + h) ^ b_swz) * 16);
   // MXFP8 scales reach LDS by direct loads too, eight stages at a time: the
   // loop then holds no register-destined global load, whose first use would
   // make the compiler wait for every load in flight (its wait counting does
@@ -898,8 +940,9 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   // bytes (the E8M0 of k-blocks 16o..16o+15, i.e. stages 8o..8o+7), laid out
   // [row][16]; waves 0-3 each move 64 rows per octet.  int8: the row scale
   // in a register.
-  const uint8_t* const sc_base = (const uint8_t*)p.bscale;
   char* const sc_lds = lds + Cfg::LDS_BYTES + Cfg::COL_BYTES;
+  const int sc_records = BKIND == B_MXFP8 ? (int)((int64_t)p.N * p.ld_scale) : 0;
+  const int sc_read = Cfg::LDS_BYTES + Cfg::COL_BYTES + (wn * WN + fr) * 16;
   uint32_t sc_src = 0;
   {
     int gn = n0 + (wave & 3) * 64 + lane;
@@ -911,7 +954,7 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
     if constexpr (BKIND == B_MXFP8) {
       if (grp == 0) {
         oct = oct < noct ? oct : noct - 1;  // past the end: re-read the last octet
-        dma16(sc_base + oct * 16 + sc_src, sc_lds + (oct & 1) * Cfg::SC_OCT + wave * 1024);
+        buffer_dma16(p.bscale, sc_records, sc_src, oct * 16, sc_lds + (oct & 1) * Cfg::SC_OCT + wave * 1024);
       }
     }
   };
@@ -931,25 +974,28 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
 
   bf16x8 fa[4][TM];  // A fragments of the stage's four k-steps
   u32x4 fb[2][TN];   // weight codes of the stage's two k-step pairs (16 per lane)
-  auto read_stage = [&](int kt) {
-    const char* As = lds + (kt % kG8Stages) * STAGE;
-    const char* Bs = As + A_BYTES;
+  // fragment reads of stage kt, which sits in buffer BUF (compile-time)
+  auto read_stage = [&](int kt, auto bufc) {
+    constexpr int BUF = decltype(bufc)::value;
     if constexpr (BKIND == B_MXFP8) {
-      const char* sa = sc_lds + ((kt >> 3) & 1) * Cfg::SC_OCT + ((kt & 7) >> 1) * 4;
+      const int sa = sc_read + ((kt >> 3) & 1) * Cfg::SC_OCT + ((kt & 7) >> 1) * 4;
 #pragma unroll
-      for (int j = 0; j < TN; ++j) scw[j] = *reinterpret_cast<const uint32_t*>(sa + (wn * WN + j * 32 + fr) * 16);
+      for (int j = 0; j < TN; ++j) scw[j] = *reinterpret_cast<const uint32_t*>(lds + sa + j * 32 * 16);
     }
 #pragma unroll
     for (int pp = 0; pp < 2; ++pp) {
 #pragma unroll
       for (int j = 0; j < TN; ++j)
-        fb[pp][j] = *reinterpret_cast<const u32x4*>(Bs + b_off[j] + (((2 * pp + h) ^ b_swz) * 16));
+        fb[pp][j] = *reinterpret_cast<const u32x4*>(lds + b_base[pp] + BUF * B_BYTES + j * 32 * B_ROWB);
 #pragma unroll
       for (int s = 0; s < 2; ++s)
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < TM; ++i) {
+          const int* base = BUF == 0 ? a_lo : a_hi;
+          constexpr int rel = (BUF == 0 ? 0 : BUF - 1) * A_BYTES;
           fa[2 * pp + s][i] =
-              *reinterpret_cast<const bf16x8*>(As + a_off[i] + (((4 * pp + 2 * h + s) ^ a_swz) * 16));
+              *reinterpret_cast<const bf16x8*>(lds + base[2 * pp + s] + rel + i * 32 * A_ROWB);
+        }
     }
   };
 
@@ -987,24 +1033,51 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
     return __builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]});
   };
 
-  // compute cluster of stage kt: 4 k-steps x TN x TM MFMAs, each weight
-  // fragment dequantised right before its MFMAs (the compiler hoists the
-  // conversions of the next fragment under the current MFMAs)
+  // compute cluster of stage kt: 4 k-steps x TN weight fragments x TM MFMAs.
+  // Fragment f+1 is dequantised while the MFMAs of fragment f run (two
+  // register sets, alternating), and the scheduler is told to interleave:
+  // per fragment one MFMA, half the next fragment's conversions, the other
+  // MFMA(s), the other half.  The scale decodes of the stage's second pair
+  // ride along with its first pair.
   auto compute_stage = [&](int kt) {
+    float scf[2][TN];
+    auto decode = [&](int pp, int j) {
+      if constexpr (BKIND == B_MXFP8)
+        scf[pp][j] = e8m0_to_f32_valu(__builtin_amdgcn_ubfe(scw[j], 16 * (kt & 1) + 8 * pp, 8));
+      else
+        scf[pp][j] = s_i8[j];
+    };
+    constexpr int NF = 4 * TN;
+    auto frag_dequant = [&](int f) -> bf16x8 {
+      const int kk = f / TN, j = f % TN, pp = kk >> 1, s = kk & 1;
+      return dequant(fb[pp][j][2 * s], fb[pp][j][2 * s + 1], scf[pp][j]);
+    };
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int pp = kk >> 1, s = kk & 1;
+    for (int j = 0; j < TN; ++j) decode(0, j);
+    bf16x8 bq[2];
+    bq[0] = frag_dequant(0);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        float sc;
-        if constexpr (BKIND == B_MXFP8)
-          sc = e8m0_to_f32((scw[j] >> (16 * (kt & 1) + 8 * pp)) & 0xffu);
-        else
-          sc = s_i8[j];
-        const bf16x8 b = dequant(fb[pp][j][2 * s], fb[pp][j][2 * s + 1], sc);
+    for (int f = 0; f < NF; ++f) {
+      const int kk = f / TN, j = f % TN;
+      if (f < TN) decode(1, f);  // the second pair's scales, early
+      if (f + 1 < NF) bq[(f + 1) & 1] = frag_dequant(f + 1);
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, fa[kk][i], acc[i][j], 0, 0, 0);
+      for (int i = 0; i < TM; ++i)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bq[f & 1], fa[kk][i], acc[i][j], 0, 0, 0);
+      // one MFMA, some vector instructions, the other MFMA(s), the rest
+      if constexpr (BKIND == B_MXFP8) {
+        static_assert(TM == 2, "interleave written for two MFMAs per fragment");
+        if (f < TN) {  // 4 conversions + 4 decode instructions
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+        } else {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+        }
       }
     }
   };
@@ -1029,13 +1102,13 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   // so every stage issues the same loads and the waits are exact.  The scales
   // of octet o+1 go out (group 0) with stage 8o's loads.
   // SUB = kt % 8 (compile-time in the unrolled loop).
-  auto stage_iter = [&](int kt, auto sub) {
-    constexpr int SUB = decltype(sub)::value;
-    constexpr int VM = VM_DMA + (SUB == 0 ? VM_SCALES : 0);  // group 0; group 1 issues no scales
+  auto stage_iter = [&](int kt, auto bufc) {
+    constexpr int BUF = decltype(bufc)::value;
+    const bool oct_start = BKIND == B_MXFP8 && (kt & 7) == 0;
     // memory cluster
-    if (SUB == 0) dma_scales((kt >> 3) + 1);
-    dma_stage(kt + 2 < KT ? kt + 2 : KT - 1, (kt + 2) % kG8Stages);
-    read_stage(kt);
+    if (oct_start) dma_scales((kt >> 3) + 1);
+    dma_stage(kt + 2 < KT ? kt + 2 : KT - 1, (BUF + 2) % kG8Stages);
+    read_stage(kt, bufc);
     wait_lgkmcnt0();
     if (grp == 1) wait_vmcnt<VM_DMA>();
     barrier_nofence();
@@ -1043,22 +1116,23 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
     __builtin_amdgcn_s_setprio(1);
     compute_stage(kt);
     __builtin_amdgcn_s_setprio(0);
-    if (grp == 0) wait_vmcnt<VM>();
+    if (grp == 0) {
+      if (oct_start) wait_vmcnt<VM_DMA + VM_SCALES>();
+      else wait_vmcnt<VM_DMA>();
+    }
     barrier_nofence();
   };
+  typedef std::integral_constant<int, 0> B0;
+  typedef std::integral_constant<int, 1> B1;
+  typedef std::integral_constant<int, 2> B2;
   int kt = 0;
-  for (; kt + 7 < KT; kt += 8) {
-    stage_iter(kt, std::integral_constant<int, 0>{});
-    stage_iter(kt + 1, std::integral_constant<int, 1>{});
-    stage_iter(kt + 2, std::integral_constant<int, 2>{});
-    stage_iter(kt + 3, std::integral_constant<int, 3>{});
-    stage_iter(kt + 4, std::integral_constant<int, 4>{});
-    stage_iter(kt + 5, std::integral_constant<int, 5>{});
-    stage_iter(kt + 6, std::integral_constant<int, 6>{});
-    stage_iter(kt + 7, std::integral_constant<int, 7>{});
+  for (; kt + 2 < KT; kt += 3) {
+    stage_iter(kt, B0{});
+    stage_iter(kt + 1, B1{});
+    stage_iter(kt + 2, B2{});
   }
-  // int8 only (MXFP8 takes K % 512 == 0): the last KT % 8 stages
-  for (; kt < KT; ++kt) stage_iter(kt, std::integral_constant<int, 1>{});
+  if (kt < KT) stage_iter(kt, B0{});
+  if (kt + 1 < KT) stage_iter(kt + 1, B1{});
   if (grp == 0) barrier_nofence();
   wait_vmcnt<0>();
 
@@ -1181,9 +1255,9 @@ static void launch_tile(GemmArgs p, hipStream_t s) {
 template <int BKIND>
 static bool g8_ok(const GemmArgs& p) {
   if (BKIND == B_BF16) return false;
-  // operand byte offsets are 32-bit in the kernel
-  if ((int64_t)p.M * p.lda * 2 >= ((int64_t)1 << 32) || (int64_t)p.N * p.ldb >= ((int64_t)1 << 32) ||
-      (int64_t)p.N * p.ld_scale >= ((int64_t)1 << 32))
+  // operand extents are 31-bit buffer record counts in the kernel
+  if ((int64_t)p.M * p.lda * 2 >= ((int64_t)1 << 31) || (int64_t)p.N * p.ldb >= ((int64_t)1 << 31) ||
+      (int64_t)p.N * p.ld_scale >= ((int64_t)1 << 31))
     return false;
   if (BKIND == B_MXFP8)
     return p.K % 512 == 0 && p.ld_scale % 16 == 0 && ((uintptr_t)p.bscale & 15u) == 0;
