@@ -83,9 +83,10 @@ def parse_args(argv=None):
     ap.add_argument("--no-config5", action="store_true", help="skip the 768x512x121 leg")
     ap.add_argument("--no-gemm-shapes", action="store_true", help="skip the per-shape GEMM leg")
     ap.add_argument("--cpu-runs", type=int, default=5, help="timed oracle block runs after one warmup")
-    ap.add_argument("--counter-workload", choices=["ff-up", "ff-up-vs-library", "copy"], default=None,
+    ap.add_argument("--counter-workload", choices=["ff-up", "ff-up-vs-library", "copy", "fused-ops"], default=None,
                     help="run only a short workload for rocprofv3 --pmc passes and exit: the video FF "
-                         "up-projection GEMM (4 launches, --weights format) or a 1 GiB device copy (3 "
+                         "up-projection GEMM (4 launches, --weights format), the three row kernels (adaln, "
+                         "gated add, QK-norm + RoPE; 4 cache-cold launches each) or a 1 GiB device copy (3 "
                          "launches, the FETCH_SIZE / WRITE_SIZE calibration)")
     return ap.parse_args(argv)
 
@@ -95,7 +96,13 @@ def counter_workload(kind: str, weights: str) -> None:
 
     from ltx_amd.kernels import gemm
 
-    if kind == "copy":
+    if kind == "fused-ops":
+        # each row kernel 4 times on cache-cold rotating buffers (counter runs)
+        _, launchers = fused_op_launchers(torch)
+        for name, fn, _ in launchers:
+            for i in range(4):
+                fn(i)
+    elif kind == "copy":
         src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
         for _ in range(3):
@@ -157,28 +164,49 @@ def measured_traffic(kernel: str, weights: str):
     return None
 
 
-def fused_op_bandwidth(torch, T=14640, C=4096):
-    """adaln / gated_add HBM GB/s at (T, C): the kernels launched through
-    their row-view launchers on preallocated buffers, inputs and outputs each
-    rotating through >= 1.5 GB so neither operand can be served from the
-    256 MB last-level cache."""
+def fused_op_launchers(torch, T=14640, C=4096, heads=32):
+    """The three HBM-bound row kernels at (T, C) on preallocated buffers that
+    rotate through >= 1.5 GB per operand, so no operand is served from the
+    256 MB last-level cache.  QK-norm + RoPE works in place on the Q and K
+    columns of a fused (T, 3C) projection output (the block's layout) with
+    the shared (T, C/2) fp32 cos / sin tables.  Returns (nbuf, [(name,
+    launch(i), algorithmic bytes per launch)])."""
     from ltx_amd.kernels.fused_ops import adaln_rows, gated_add_rows
+    from ltx_amd.kernels.rope_ops import qknorm_rope_
 
     nbytes = T * C * 2
-    nbuf = max(2, math.ceil(1.5e9 / nbytes))
+    nbuf = max(3, math.ceil(1.5e9 / nbytes))
     xs = [torch.randn((T, C), device="cuda").bfloat16() for _ in range(nbuf)]
     bs = [torch.randn((T, C), device="cuda").bfloat16() for _ in range(nbuf)]
     outs = [torch.empty((T, C), device="cuda", dtype=torch.bfloat16) for _ in range(nbuf)]
     scale = torch.randn(C, device="cuda") * 0.1
     shift = torch.randn(C, device="cuda") * 0.1
     gate = torch.randn(C, device="cuda") * 0.5
+    nq = max(3, math.ceil(1.5e9 / (T * (3 * C * 2 + C * 4))))
+    qkv = [torch.randn((T, 3 * C), device="cuda").bfloat16() for _ in range(nq)]
+    tabs = [(torch.rand((T, C // 2), device="cuda") * 2 - 1, torch.rand((T, C // 2), device="cuda") * 2 - 1)
+            for _ in range(nq)]
+    wq = torch.rand(C, device="cuda") + 0.5
+    wk = torch.rand(C, device="cuda") + 0.5
+    return nbuf, [
+        ("adaln_norm_fused", lambda i: adaln_rows(xs[i % nbuf], C, scale, shift, outs[(i + 1) % nbuf],
+                                                  C, T, C, 1e-6, 0),
+         2 * nbytes + 2 * C * 4),
+        ("gated_add_fused", lambda i: gated_add_rows(xs[i % nbuf], C, bs[i % nbuf], C, gate,
+                                                     outs[(i + 1) % nbuf], C, T, C, 0),
+         3 * nbytes + C * 4),
+        ("qknorm_rope", lambda i: qknorm_rope_(qkv[i % nq][:, :C], wq, tabs[i % nq], qkv[i % nq][:, C:2 * C], wk,
+                                               tabs[i % nq], heads),
+         4 * nbytes + 2 * T * (C // 2) * 4 + 2 * C * 4),
+    ]
+
+
+def fused_op_bandwidth(torch, T=14640, C=4096):
+    """HBM GB/s of the row kernels (fused_op_launchers), each replayed from a
+    HIP graph, best of three replays."""
+    nbuf, launchers = fused_op_launchers(torch, T, C)
     res = {}
-    for name, fn, algo in (("adaln_norm_fused", lambda i: adaln_rows(xs[i], C, scale, shift, outs[(i + 1) % nbuf],
-                                                                      C, T, C, 1e-6, 0),
-                            2 * nbytes + 2 * C * 4),
-                           ("gated_add_fused", lambda i: gated_add_rows(xs[i], C, bs[i], C, gate, outs[(i + 1) % nbuf],
-                                                                        C, T, C, 0),
-                            3 * nbytes + C * 4)):
+    for name, fn, algo in launchers:
         for i in range(nbuf):
             fn(i)
         torch.cuda.synchronize()
@@ -201,7 +229,7 @@ def fused_op_bandwidth(torch, T=14640, C=4096):
         del g
         res[name] = {"us": round(t * 1e6, 2), "GB/s": round(algo / t / 1e9, 1),
                      "frac_hbm_peak": round(algo / t / 1e9 / PEAK_HBM_GBPS, 3), "bytes": algo}
-    del xs, bs, outs
+    del launchers
     return res
 
 

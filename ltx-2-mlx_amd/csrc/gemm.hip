@@ -812,10 +812,11 @@ constexpr int kG8Stages = 3;
 template <int BKIND, int kG8Stages_ = 3>
 struct G8Cfg {
   static constexpr int BM = 256, BN = 256, BK = 64;
-  // MXFP8 dequantises with one conversion per two codes: 64x128 wave tiles
-  // (fewest LDS bytes per MFMA).  int8 needs ~2.5 VALU per code: 128x64, half
-  // the weight fragments per wave.
-  static constexpr int WM = BKIND == B_MXFP8 ? 64 : 128, WN = BKIND == B_MXFP8 ? 128 : 64;
+  // 128x64 wave tiles: each weight fragment is dequantised by the two waves
+  // that share its columns rather than four (64x128 tiles read fewer LDS
+  // bytes per MFMA, but MXFP8 measured 2.5 % slower with them: the
+  // conversions cost more power than the extra fragment reads)
+  static constexpr int WM = 128, WN = 64;
   static constexpr int TM = WM / 32, TN = WN / 32;
   static constexpr int WAVES_M = BM / WM;
   static constexpr int A_ROWB = BK * 2, B_ROWB = BK;  // bf16 activations, 8-bit codes
@@ -1035,10 +1036,8 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
 
   // compute cluster of stage kt: 4 k-steps x TN weight fragments x TM MFMAs.
   // Fragment f+1 is dequantised while the MFMAs of fragment f run (two
-  // register sets, alternating), and the scheduler is told to interleave:
-  // per fragment one MFMA, half the next fragment's conversions, the other
-  // MFMA(s), the other half.  The scale decodes of the stage's second pair
-  // ride along with its first pair.
+  // register sets, alternating).  The scale decodes of the stage's second
+  // pair ride along with its first pair.
   auto compute_stage = [&](int kt) {
     float scf[2][TN];
     auto decode = [&](int pp, int j) {
@@ -1064,21 +1063,6 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
 #pragma unroll
       for (int i = 0; i < TM; ++i)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bq[f & 1], fa[kk][i], acc[i][j], 0, 0, 0);
-      // one MFMA, some vector instructions, the other MFMA(s), the rest
-      if constexpr (BKIND == B_MXFP8) {
-        static_assert(TM == 2, "interleave written for two MFMAs per fragment");
-        if (f < TN) {  // 4 conversions + 4 decode instructions
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-        } else {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
-        }
-      }
     }
   };
 
