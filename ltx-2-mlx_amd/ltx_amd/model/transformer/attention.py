@@ -49,11 +49,15 @@ class Attention:
         return [w for w in (self.proj_q, self.proj_kv, self.to_out) if w is not None]
 
     def core(self, x: torch.Tensor, context: torch.Tensor | None = None,
-             pe: tuple | None = None, k_pe: tuple | None = None) -> torch.Tensor:
-        """Everything up to (not including) ``to_out``; returns (Tq, inner) bf16.
+             pe: tuple | None = None, k_pe: tuple | None = None, passes: int = 1) -> torch.Tensor:
+        """Everything up to (not including) ``to_out``; returns (passes*Tq, inner) bf16.
 
-        x: (Tq, query_dim) bf16; context: (Tk, context_dim) bf16 for
-        cross-attention.  pe / k_pe: token-major (cos, sin) tables or None.
+        x: (passes*Tq, query_dim) bf16 -- ``passes`` independent sequences of
+        Tq tokens stacked by rows (the batched passes of a guided step);
+        context: (passes*Tk, context_dim) bf16 for cross-attention, sequence
+        p's keys in rows [p*Tk, (p+1)*Tk).  pe / k_pe: token-major (cos, sin)
+        tables of one sequence, or None.  The projections run once over all
+        rows; QK-norm + RoPE, V's transpose and the attention run per sequence.
         """
         inner, heads = self.inner_dim, self.heads
         gate_cols = heads if self.gated else 0
@@ -71,9 +75,21 @@ class Attention:
             k_tab = pe if k_pe is None else k_pe
             if pe is None:
                 k_tab = None
-        qknorm_rope_(q, self.q_norm, pe, k, self.k_norm, k_tab, heads, self.norm_eps)
-        vt = attn_k.transpose_v(v, heads)
-        return attn_k.flash_attention(q, k, None, heads, vt=vt, gate=g)
+        if passes == 1:
+            qknorm_rope_(q, self.q_norm, pe, k, self.k_norm, k_tab, heads, self.norm_eps)
+            vt = attn_k.transpose_v(v, heads)
+            return attn_k.flash_attention(q, k, None, heads, vt=vt, gate=g)
+        tq, tk = q.shape[0] // passes, k.shape[0] // passes
+        if tq * passes != q.shape[0] or tk * passes != k.shape[0]:
+            raise ValueError(f"{q.shape[0]} query / {k.shape[0]} key rows do not split into {passes} passes")
+        out = torch.empty((q.shape[0], inner), dtype=torch.bfloat16, device=q.device)
+        for p in range(passes):
+            qp, kp, vp = q[p * tq:(p + 1) * tq], k[p * tk:(p + 1) * tk], v[p * tk:(p + 1) * tk]
+            gp = None if g is None else g[p * tq:(p + 1) * tq]
+            qknorm_rope_(qp, self.q_norm, pe, kp, self.k_norm, k_tab, heads, self.norm_eps)
+            vt = attn_k.transpose_v(vp, heads)
+            attn_k.flash_attention(qp, kp, None, heads, vt=vt, gate=gp, out=out[p * tq:(p + 1) * tq])
+        return out
 
     def __call__(self, x: torch.Tensor, context: torch.Tensor | None = None, mask=None,
                  pe: tuple | None = None, k_pe: tuple | None = None) -> torch.Tensor:

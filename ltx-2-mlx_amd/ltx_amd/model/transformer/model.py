@@ -202,7 +202,7 @@ class LTXModel:
                  pes: tuple, audio_latent: torch.Tensor | None = None,
                  audio_context: torch.Tensor | None = None,
                  profile_events: list | None = None,
-                 perturbations=None) -> tuple[torch.Tensor, torch.Tensor | None]:
+                 perturbations=None, passes: int = 1) -> tuple[torch.Tensor, torch.Tensor | None]:
         """One transformer forward -> (video velocity (T, 128), audio velocity).
 
         Latents are 2-D (T, 128) bf16; contexts (S, D) bf16; ``sigma_dev`` is
@@ -210,11 +210,22 @@ class LTXModel:
         ``BatchedPerturbationConfig``) skips attention sub-layers per block, the
         STG / modality-isolated passes (model.py:1044-1310 hands it to every
         block).
+
+        ``passes`` > 1 runs that many passes of the same latents and timestep
+        as one forward, their tokens stacked by rows (M = passes * T in every
+        projection): contexts are then (passes, S, D) -- one per pass -- or a
+        shared (S, D), ``perturbations`` holds one config per pass, and the
+        velocities come back as (passes, T, 128).  The batched passes of a
+        guided step (av_pipeline.py:688-717 runs them one after another).
         """
         vpe, vxpe, ape, axpe = pes
         run_audio = self.audio_config is not None and audio_latent is not None and audio_latent.shape[0] > 0
+
+        def stacked(x):  # (T, C) -> (passes, T, C)
+            return x if passes == 1 else x.unsqueeze(0).expand(passes, *x.shape).contiguous()
+
         # preprocess
-        vx = gemm.linear(video_latent, self.patchify_proj)
+        vx = stacked(gemm.linear(video_latent, self.patchify_proj))
         self._timestep_rows(sigma_dev, sigma_dev, video=True)
         stream = _lib.stream_of(vx)
         _lib.call("ltx_broadcast_add_f32", self.video_tables.data_ptr(), self._temb_v.data_ptr(),
@@ -223,7 +234,7 @@ class LTXModel:
                                 cross_positional_embeddings=vxpe)
         audio = None
         if run_audio:
-            ax = gemm.linear(audio_latent, self.audio_patchify_proj)
+            ax = stacked(gemm.linear(audio_latent, self.audio_patchify_proj))
             self._timestep_rows(sigma_dev, sigma_dev, video=False)
             _lib.call("ltx_broadcast_add_f32", self.audio_tables.data_ptr(), self._temb_a.data_ptr(),
                       self._ada_a.data_ptr(), self.num_layers, ADA_ROWS * self.audio_dim, stream)
@@ -246,10 +257,17 @@ class LTXModel:
             torch.cuda.current_stream().wait_stream(side)
             audio.x.record_stream(torch.cuda.current_stream())
         # output heads
-        v_out = self._output(video.x, self.scale_shift_table, self._emb_v, self.proj_out)
+        def rows(x):
+            return x.reshape(-1, x.shape[-1])
+
+        def unstack(y):
+            return y if passes == 1 else y.view(passes, -1, y.shape[-1])
+
+        v_out = unstack(self._output(rows(video.x), self.scale_shift_table, self._emb_v, self.proj_out))
         a_out = None
         if run_audio:
-            a_out = self._output(audio.x, self.audio_scale_shift_table, self._emb_a, self.audio_proj_out)
+            a_out = unstack(self._output(rows(audio.x), self.audio_scale_shift_table, self._emb_a,
+                                         self.audio_proj_out))
         return v_out, a_out
 
     def _output(self, x: torch.Tensor, table: torch.Tensor, emb: torch.Tensor, proj: gemm.LinearWeight) -> torch.Tensor:

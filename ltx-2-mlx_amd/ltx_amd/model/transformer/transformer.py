@@ -202,12 +202,25 @@ class BasicAVTransformerBlock:
     # -- forward --------------------------------------------------------------
     def __call__(self, video: TransformerArgs | None, audio: TransformerArgs | None,
                  perturbations=None, profile_events: list | None = None) -> tuple:
+        """One block on P stacked passes.  ``x`` is (T, C) for one pass or
+        (P, T, C) for P passes (the batched passes of a guided step: same
+        latents and timestep, their own text contexts and perturbations);
+        ``context`` is (S, D) / (1, S, D) shared by every pass, or (P, S, D).
+        ``perturbations`` holds one config per pass (or one for all): a pass
+        whose sub-layer is skipped keeps its rows unchanged there, like the
+        reference's per-sample mask (transformer.py:425-465)."""
         eps = self.norm_eps
         vx = video.x if video is not None else None
         ax = audio.x if audio is not None else None
+        npass = 1
         for x in (vx, ax):
             if x is not None and x.dim() == 3 and x.shape[0] != 1:
-                raise NotImplementedError("batch size 1 only (the T2V hot path)")
+                npass = x.shape[0]
+        for x in (vx, ax):
+            if x is not None and x.dim() == 3 and x.shape[0] not in (1, npass):
+                raise ValueError(f"video and audio pass counts differ ({vx.shape[0]} vs {ax.shape[0]})")
+            if x is not None and x.dim() == 2 and npass > 1:
+                raise ValueError("stacked passes need (P, T, C) inputs for both modalities")
         started = time.perf_counter()
 
         def mark(name: str) -> None:
@@ -224,21 +237,71 @@ class BasicAVTransformerBlock:
         run_a2v = run_vx and ax is not None and ax.numel() > 0
         run_v2a = run_ax and vx is not None and vx.numel() > 0
 
-        def skip(kind: str) -> bool:
-            return perturbations is not None and perturbations.all_in_batch(kind, self.idx)
+        def keep(kind: str) -> list[bool]:
+            """Per pass: does the sub-layer run?"""
+            if perturbations is None:
+                return [True] * npass
+            m = perturbations.mask(kind, self.idx)
+            if len(m) == 1:
+                m = m * npass
+            if len(m) != npass:
+                raise ValueError(f"{len(m)} perturbation configs for {npass} passes")
+            return [v != 0.0 for v in m]
+
+        def runs(mask: list[bool]) -> list[tuple[int, int]]:
+            """Maximal ranges [p0, p1) of consecutive running passes."""
+            out, p = [], 0
+            while p < npass:
+                if mask[p]:
+                    q = p
+                    while q < npass and mask[q]:
+                        q += 1
+                    out.append((p, q))
+                    p = q
+                else:
+                    p += 1
+            return out
 
         flags = self._adaln_flags
         rn = _lib.ADALN_ROUND_NORM
-        # 2-D working views; the first residual update of each stream writes a
-        # fresh buffer so the caller's input tensors are never modified.
-        v2 = vx[0] if (vx is not None and vx.dim() == 3) else vx
-        a2 = ax[0] if (ax is not None and ax.dim() == 3) else ax
+        # 2-D working views (passes stacked by rows); the first residual update
+        # of each stream writes a fresh buffer so the caller's input tensors are
+        # never modified.
+        v2 = vx.reshape(-1, vx.shape[-1]) if (vx is not None and vx.dim() == 3) else vx
+        a2 = ax.reshape(-1, ax.shape[-1]) if (ax is not None and ax.dim() == 3) else ax
+        tv = v2.shape[0] // npass if v2 is not None else 0
+        ta = a2.shape[0] // npass if a2 is not None else 0
         v_owned = a_owned = False
 
         def residual_gemm(o, weight, stream_x, owned, gate, epi):
             out = stream_x if owned else torch.empty_like(stream_x)
             gemm.linear(o, weight, epilogue=epi, out=out, residual=stream_x, gate=gate)
             return out
+
+        def partial_residual(x2, owned, t, rng, sublayer):
+            """Run ``sublayer(dst, src, p0, p1) -> None`` (dst = src + the
+            sub-layer's gated branch; dst may be src) on the passes of each
+            range of ``rng``; the other passes' rows stay as they are (copied
+            once into a fresh stream when the input is not owned).  Returns the
+            (owned) stream."""
+            out = x2 if owned else torch.empty_like(x2)
+            p = 0
+            for p0, p1 in rng + [(npass, npass)]:
+                if not owned and p0 > p:
+                    out[p * t:p0 * t].copy_(x2[p * t:p0 * t])
+                if p1 > p0:
+                    sublayer(out[p0 * t:p1 * t], x2[p0 * t:p1 * t], p0, p1)
+                p = p1
+            return out
+
+        def ctx_rows(args, p0, p1):
+            """Text-context rows of passes [p0, p1): per-pass contexts are
+            stacked (P, S, D); a shared (S, D) context serves every pass."""
+            c = args.context
+            if c.dim() == 3 and c.shape[0] == npass and npass > 1:
+                return c[p0:p1].reshape(-1, c.shape[-1]), p1 - p0
+            c2 = c[0] if c.dim() == 3 else c
+            return c2, 1
 
         # A2V runs whenever video runs and audio tokens exist, even with the
         # audio stream disabled (transformer.py:426-427); it reads both tables.
@@ -263,16 +326,29 @@ class BasicAVTransformerBlock:
 
         if run_vx:
             pe = _tables(video.positional_embeddings)
-            if not skip("skip_video_self_attn"):
+            rng = runs(keep("skip_video_self_attn"))
+            if rng == [(0, npass)]:
                 h = adaln(v2, ada_v[ROW_SCALE_MSA], ada_v[ROW_SHIFT_MSA], eps, flags)
-                o = self.attn1.core(h, pe=pe)
+                o = self.attn1.core(h, pe=pe, passes=npass)
                 v2 = residual_gemm(o, self.attn1.to_out, v2, v_owned, ada_v[ROW_GATE_MSA], gemm.EPI_RESIDUAL)
                 v_owned = True
-                mark("video self-attn")
-            ctx = video.context[0] if video.context.dim() == 3 else video.context
+            elif rng:
+                def video_self(dst, src, p0, p1):
+                    h = adaln(src, ada_v[ROW_SCALE_MSA], ada_v[ROW_SHIFT_MSA], eps, flags)
+                    o = self.attn1.core(h, pe=pe, passes=p1 - p0)
+                    gemm.linear(o, self.attn1.to_out, epilogue=gemm.EPI_RESIDUAL, out=dst, residual=src,
+                                gate=ada_v[ROW_GATE_MSA])
+                v2 = partial_residual(v2, v_owned, tv, rng, video_self)
+                v_owned = True
+            mark("video self-attn")
             a = adaln(v2, ada_v[ROW_SCALE_Q], ada_v[ROW_SHIFT_Q], eps, rn)
-            c = adaln(ctx, ada_v[ROW_SCALE_KV], ada_v[ROW_SHIFT_KV], eps, _lib.ADALN_NO_NORM)
-            o = self.attn2.core(a, c)
+            c, cp = ctx_rows(video, 0, npass)
+            c = adaln(c, ada_v[ROW_SCALE_KV], ada_v[ROW_SHIFT_KV], eps, _lib.ADALN_NO_NORM)
+            if cp == npass:
+                o = self.attn2.core(a, c, passes=npass)
+            else:
+                o = torch.cat([self.attn2.core(a[p * tv:(p + 1) * tv], c) for p in range(npass)], 0) \
+                    if npass > 1 else self.attn2.core(a, c)
             v2 = residual_gemm(o, self.attn2.to_out, v2, v_owned, ada_v[ROW_GATE_Q], gemm.EPI_RESIDUAL_ROUND)
             v_owned = True
             mark("video text-attn")
@@ -280,17 +356,30 @@ class BasicAVTransformerBlock:
         if run_ax:
             with on_audio():
                 pe = _tables(audio.positional_embeddings)
-                if not skip("skip_audio_self_attn"):
+                rng = runs(keep("skip_audio_self_attn"))
+                if rng == [(0, npass)]:
                     h = adaln(a2, ada_a[ROW_SCALE_MSA], ada_a[ROW_SHIFT_MSA], eps, flags)
-                    o = self.audio_attn1.core(h, pe=pe)
+                    o = self.audio_attn1.core(h, pe=pe, passes=npass)
                     a2 = residual_gemm(o, self.audio_attn1.to_out, a2, a_owned, ada_a[ROW_GATE_MSA],
                                        gemm.EPI_RESIDUAL)
                     a_owned = True
-                    mark("audio self-attn")
-                ctx = audio.context[0] if audio.context.dim() == 3 else audio.context
+                elif rng:
+                    def audio_self(dst, src, p0, p1):
+                        h = adaln(src, ada_a[ROW_SCALE_MSA], ada_a[ROW_SHIFT_MSA], eps, flags)
+                        o = self.audio_attn1.core(h, pe=pe, passes=p1 - p0)
+                        gemm.linear(o, self.audio_attn1.to_out, epilogue=gemm.EPI_RESIDUAL, out=dst, residual=src,
+                                    gate=ada_a[ROW_GATE_MSA])
+                    a2 = partial_residual(a2, a_owned, ta, rng, audio_self)
+                    a_owned = True
+                mark("audio self-attn")
                 a = adaln(a2, ada_a[ROW_SCALE_Q], ada_a[ROW_SHIFT_Q], eps, rn)
-                c = adaln(ctx, ada_a[ROW_SCALE_KV], ada_a[ROW_SHIFT_KV], eps, _lib.ADALN_NO_NORM)
-                o = self.audio_attn2.core(a, c)
+                c, cp = ctx_rows(audio, 0, npass)
+                c = adaln(c, ada_a[ROW_SCALE_KV], ada_a[ROW_SHIFT_KV], eps, _lib.ADALN_NO_NORM)
+                if cp == npass:
+                    o = self.audio_attn2.core(a, c, passes=npass)
+                else:
+                    o = torch.cat([self.audio_attn2.core(a[p * ta:(p + 1) * ta], c) for p in range(npass)], 0) \
+                        if npass > 1 else self.audio_attn2.core(a, c)
                 a2 = residual_gemm(o, self.audio_attn2.to_out, a2, a_owned, ada_a[ROW_GATE_Q],
                                    gemm.EPI_RESIDUAL_ROUND)
                 a_owned = True
@@ -310,19 +399,38 @@ class BasicAVTransformerBlock:
                 main.wait_event(side.record_event())
                 as_a2v.record_stream(main)
                 vs_v2a.record_stream(side)
-            if run_a2v and not skip("skip_a2v_cross_attn"):
-                o = self.audio_to_video_attn.core(vs_a2v, as_a2v, pe=vpe, k_pe=ape)
+            rng = runs(keep("skip_a2v_cross_attn")) if run_a2v else []
+            if rng == [(0, npass)]:
+                o = self.audio_to_video_attn.core(vs_a2v, as_a2v, pe=vpe, k_pe=ape, passes=npass)
                 v2 = residual_gemm(o, self.audio_to_video_attn.to_out, v2, v_owned, ada_v[ROW_GATE_AV],
                                    gemm.EPI_RESIDUAL)
                 v_owned = True
+            elif rng:
+                def a2v(dst, src, p0, p1):
+                    o = self.audio_to_video_attn.core(vs_a2v[p0 * tv:p1 * tv], as_a2v[p0 * ta:p1 * ta], pe=vpe,
+                                                      k_pe=ape, passes=p1 - p0)
+                    gemm.linear(o, self.audio_to_video_attn.to_out, epilogue=gemm.EPI_RESIDUAL, out=dst,
+                                residual=src, gate=ada_v[ROW_GATE_AV])
+                v2 = partial_residual(v2, v_owned, tv, rng, a2v)
+                v_owned = True
+            if run_a2v:
                 mark("audio->video attn")
-            if run_v2a and not skip("skip_v2a_cross_attn"):
+            rng = runs(keep("skip_v2a_cross_attn")) if run_v2a else []
+            if rng:
                 with on_audio():
                     if side is not None:
                         side.wait_event(ev_v)
-                    o = self.video_to_audio_attn.core(as_v2a, vs_v2a, pe=ape, k_pe=vpe)
-                    a2 = residual_gemm(o, self.video_to_audio_attn.to_out, a2, a_owned, ada_a[ROW_GATE_AV],
-                                       gemm.EPI_RESIDUAL)
+                    if rng == [(0, npass)]:
+                        o = self.video_to_audio_attn.core(as_v2a, vs_v2a, pe=ape, k_pe=vpe, passes=npass)
+                        a2 = residual_gemm(o, self.video_to_audio_attn.to_out, a2, a_owned, ada_a[ROW_GATE_AV],
+                                           gemm.EPI_RESIDUAL)
+                    else:
+                        def v2a(dst, src, p0, p1):
+                            o = self.video_to_audio_attn.core(as_v2a[p0 * ta:p1 * ta], vs_v2a[p0 * tv:p1 * tv],
+                                                              pe=ape, k_pe=vpe, passes=p1 - p0)
+                            gemm.linear(o, self.video_to_audio_attn.to_out, epilogue=gemm.EPI_RESIDUAL, out=dst,
+                                        residual=src, gate=ada_a[ROW_GATE_AV])
+                        a2 = partial_residual(a2, a_owned, ta, rng, v2a)
                     a_owned = True
                     mark("video->audio attn")
 
@@ -342,7 +450,7 @@ class BasicAVTransformerBlock:
         def pack(args, x2, x_in, owned):
             if args is None or not owned:
                 return args
-            return args.replace(x=x2[None] if x_in.dim() == 3 else x2)
+            return args.replace(x=x2.reshape(x_in.shape) if x_in.dim() == 3 else x2)
 
         return pack(video, v2, vx, v_owned), pack(audio, a2, ax, a_owned)
 

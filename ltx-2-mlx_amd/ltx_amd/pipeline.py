@@ -232,57 +232,170 @@ def _velocities(model: LTXModel, state: DenoiseState, sig, pes, video_context, a
                           perturbations=perturbations)
 
 
-def denoise_cfg_av(model: LTXModel, state: DenoiseState, *, video_guider, audio_guider, stg_guider=None,
-                   stg_perturbations=None, stg_cutoff: float = 1.0, ge_gamma: float = 0.0,
-                   callback=None) -> DenoiseState:
-    """Guided joint denoising with separate guidance per modality
-    (av_pipeline.py:625-757), in place on ``state``'s latents."""
-    from .components.diffusion_steps import to_denoised
+def _stacked_passes(model: LTXModel, state: DenoiseState, sig, pes, contexts: list, perturbations: list):
+    """The passes of one guided step as one forward with their tokens
+    stacked by rows: ``contexts`` holds (video, audio) context pairs, one per
+    pass; ``perturbations`` one ``PerturbationConfig`` (or None) per pass.
+    Returns per-pass (video velocity, audio velocity) pairs."""
+    from .components.perturbations import BatchedPerturbationConfig, PerturbationConfig
 
-    pes = model.rope(state.video_positions, state.audio_positions)
-    stepper = EulerDiffusionStep()
-    num_steps = len(state.sigmas) - 1
-    need_cfg = video_guider.enabled() or audio_guider.enabled()
+    n = len(contexts)
     audio = state.audio_tokens > 0
-    prev_velocity = None
-    for step in range(num_steps):
+    vctx = torch.stack([c[0] for c in contexts])
+    actx = torch.stack([c[1] for c in contexts]) if audio else None
+    pert = None
+    if any(p is not None for p in perturbations):
+        pert = BatchedPerturbationConfig([p if p is not None else PerturbationConfig.empty() for p in perturbations])
+    v, a = model.velocity(state.video_latent, vctx, sig, pes, state.audio_latent if audio else None, actx,
+                          perturbations=pert, passes=n)
+    return [(v[i], a[i] if audio else None) for i in range(n)]
+
+
+class CfgAvLoop:
+    """The guided joint denoising loop with separate guidance per modality
+    (av_pipeline.py:625-757) as a step function over a ``DenoiseState``:
+    ``step(i)`` enqueues step i (its transformer passes, guidance, optional
+    GE velocity correction and the Euler update, in place on the state's
+    latents) without host synchronisation.
+
+    With ``batch_passes`` (default) the positive, negative-prompt and STG
+    passes of a step run as one forward over their stacked tokens (the
+    reference runs them one after another, av_pipeline.py:688-717); each
+    pass's tokens see exactly the arithmetic of a pass of its own.  The
+    contexts of the stacked passes must have equal lengths; otherwise, or with
+    ``batch_passes=False``, the passes run one after another.
+
+    ``capture()`` records every step as a HIP graph (one per step: the step's
+    sigmas and flags are launch arguments); ``replay(i)`` then runs step i
+    from its graph, on the same state buffers -- a new generation of the same
+    shape and schedule writes its noise into ``state.video_latent`` /
+    ``state.audio_latent`` in place and replays."""
+
+    def __init__(self, model: LTXModel, state: DenoiseState, *, video_guider, audio_guider, stg_guider=None,
+                 stg_perturbations=None, stg_cutoff: float = 1.0, ge_gamma: float = 0.0,
+                 batch_passes: bool = True):
+        self.model, self.state = model, state
+        self.video_guider, self.audio_guider, self.stg_guider = video_guider, audio_guider, stg_guider
+        self.stg_perturbations, self.stg_cutoff, self.ge_gamma = stg_perturbations, stg_cutoff, ge_gamma
+        self.batch_passes = batch_passes
+        self.pes = model.rope(state.video_positions, state.audio_positions)
+        self.stepper = EulerDiffusionStep()
+        self.num_steps = len(state.sigmas) - 1
+        self.need_cfg = video_guider.enabled() or audio_guider.enabled()
+        self.audio = state.audio_tokens > 0
+        self.stg_one = None
+        if stg_perturbations is not None:
+            if len(stg_perturbations.perturbations) != 1:
+                raise ValueError("the STG pass takes one perturbation config")
+            self.stg_one = stg_perturbations.perturbations[0]
+        # GE correction: the previous step's velocity (fixed buffer, so every
+        # step's graph reads and writes the same memory) and whether it holds one
+        self.prev_velocity = (torch.empty(state.video_latent.shape, dtype=torch.float32, device=model.device)
+                              if ge_gamma > 0 else None)
+        self.prev_valid = False
+        self.graphs: list | None = None
+
+    def step(self, step: int) -> None:
+        from .components.diffusion_steps import to_denoised
+
+        model, state, pes, audio = self.model, self.state, self.pes, self.audio
         sigma = state.sigmas[step]
         sig = state.sigmas_dev[step:step + 1]
-        v_pos, a_pos = _velocities(model, state, sig, pes, state.video_context, state.audio_context)
+        stg_active = (self.stg_guider is not None and self.stg_guider.enabled() and self.stg_perturbations is not None
+                      and (step + 1) / self.num_steps <= self.stg_cutoff)
+        pos_ctx = (state.video_context, state.audio_context)
+        neg_ctx = (state.negative_video_context, state.negative_audio_context)
+        contexts, perts = [pos_ctx], [None]
+        if self.need_cfg:
+            contexts.append(neg_ctx)
+            perts.append(None)
+        if stg_active:
+            contexts.append(pos_ctx)
+            perts.append(self.stg_one)
+        same_len = all(c[0].shape == pos_ctx[0].shape and (not audio or c[1].shape == pos_ctx[1].shape)
+                       for c in contexts)
+        if self.batch_passes and len(contexts) > 1 and same_len:
+            vel = _stacked_passes(model, state, sig, pes, contexts, perts)
+        else:
+            vel = [_velocities(model, state, sig, pes, c[0], c[1],
+                               perturbations=None if p is None else self.stg_perturbations)
+                   for c, p in zip(contexts, perts)]
+        v_pos, a_pos = vel[0]
         video_d = to_denoised(state.video_latent, v_pos, sigma)
         audio_d = to_denoised(state.audio_latent, a_pos, sigma) if audio else None
-        if need_cfg:
-            v_neg, a_neg = _velocities(model, state, sig, pes, state.negative_video_context,
-                                       state.negative_audio_context)
-            video_d = video_guider.guide(video_d, to_denoised(state.video_latent, v_neg, sigma))
+        if self.need_cfg:
+            v_neg, a_neg = vel[1]
+            video_d = self.video_guider.guide(video_d, to_denoised(state.video_latent, v_neg, sigma))
             if audio:
-                audio_d = audio_guider.guide(audio_d, to_denoised(state.audio_latent, a_neg, sigma))
-        stg_active = (stg_guider is not None and stg_guider.enabled() and stg_perturbations is not None
-                      and (step + 1) / num_steps <= stg_cutoff)
+                audio_d = self.audio_guider.guide(audio_d, to_denoised(state.audio_latent, a_neg, sigma))
         if stg_active:
-            v_ptb, _ = _velocities(model, state, sig, pes, state.video_context, state.audio_context,
-                                   perturbations=stg_perturbations)
-            video_d = stg_guider.guide(video_d, to_denoised(state.video_latent, v_ptb, sigma))
-        if ge_gamma > 0 and sigma > 0:
-            valid = prev_velocity is not None
-            if prev_velocity is None:
-                prev_velocity = torch.empty_like(video_d)
-            _lib.call("ltx_ge_correct_f32", _lib.ptr(state.video_latent), _lib.ptr(video_d), _lib.ptr(prev_velocity),
-                      int(valid), float(sigma), float(ge_gamma), video_d.numel(), _lib.stream_of(video_d))
-        stepper.step(state.video_latent, video_d, state.sigmas, step, out=state.video_latent)
+            v_ptb, _ = vel[-1]
+            video_d = self.stg_guider.guide(video_d, to_denoised(state.video_latent, v_ptb, sigma))
+        if self.ge_gamma > 0 and sigma > 0:
+            _lib.call("ltx_ge_correct_f32", _lib.ptr(state.video_latent), _lib.ptr(video_d),
+                      _lib.ptr(self.prev_velocity), int(self.prev_valid), float(sigma), float(self.ge_gamma),
+                      video_d.numel(), _lib.stream_of(video_d))
+            self.prev_valid = True
+        self.stepper.step(state.video_latent, video_d, state.sigmas, step, out=state.video_latent)
         if audio:
-            stepper.step(state.audio_latent, audio_d, state.sigmas, step, out=state.audio_latent)
-        if callback is not None:
-            callback(step, state)
-    return state
+            self.stepper.step(state.audio_latent, audio_d, state.sigmas, step, out=state.audio_latent)
+
+    def run(self, callback=None) -> DenoiseState:
+        """Every step in order (from the graphs when captured)."""
+        for i in range(self.num_steps):
+            if self.graphs is not None:
+                self.graphs[i].replay()
+            else:
+                self.step(i)
+            if callback is not None:
+                callback(i, self.state)
+        return self.state
+
+    def capture(self, pool=None) -> "CfgAvLoop":
+        """Record every step as a HIP graph (nothing runs).  The first step's
+        work is run once eagerly first -- on a copy of the latents, restored
+        after -- so every lazily built table and workspace exists before
+        capture."""
+        st = self.state
+        saved = (st.video_latent.clone(), st.audio_latent.clone(), self.prev_valid)
+        self.step(0)
+        torch.cuda.synchronize()
+        st.video_latent.copy_(saved[0])
+        st.audio_latent.copy_(saved[1])
+        self.prev_valid = saved[2]
+        pool = torch.cuda.graph_pool_handle() if pool is None else pool
+        graphs = []
+        for i in range(self.num_steps):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, pool=pool):
+                self.step(i)
+            graphs.append(g)
+        torch.cuda.synchronize()
+        self.graphs = graphs
+        self.prev_valid = saved[2]
+        return self
+
+
+def denoise_cfg_av(model: LTXModel, state: DenoiseState, *, video_guider, audio_guider, stg_guider=None,
+                   stg_perturbations=None, stg_cutoff: float = 1.0, ge_gamma: float = 0.0,
+                   callback=None, batch_passes: bool = True) -> DenoiseState:
+    """Guided joint denoising with separate guidance per modality
+    (av_pipeline.py:625-757), in place on ``state``'s latents; the loop of
+    ``CfgAvLoop`` run eagerly."""
+    loop = CfgAvLoop(model, state, video_guider=video_guider, audio_guider=audio_guider, stg_guider=stg_guider,
+                     stg_perturbations=stg_perturbations, stg_cutoff=stg_cutoff, ge_gamma=ge_gamma,
+                     batch_passes=batch_passes)
+    return loop.run(callback)
 
 
 def denoise_multimodal_av(model: LTXModel, state: DenoiseState, *, video_guider, audio_guider,
-                          callback=None) -> DenoiseState:
+                          callback=None, batch_passes: bool = True) -> DenoiseState:
     """Multi-modal guided joint denoising (pipelines/two_stage.py:306-388):
     conditioned pass, unconditioned pass when either guider runs CFG,
     modality-isolated pass (A2V and V2A skipped in every block) when either
-    runs modality guidance; ``MultiModalGuider.calculate`` per modality."""
+    runs modality guidance; ``MultiModalGuider.calculate`` per modality.
+    ``batch_passes`` stacks the passes of a step into one forward, as in
+    ``denoise_cfg_av``."""
     from .components.diffusion_steps import to_denoised
     from .components.perturbations import modality_isolation_config
 
@@ -298,15 +411,30 @@ def denoise_multimodal_av(model: LTXModel, state: DenoiseState, *, video_guider,
         def den(v, a):
             return to_denoised(x_v, v, sigma), (to_denoised(x_a, a, sigma) if audio else None)
 
-        cond_v, cond_a = den(*_velocities(model, state, sig, pes, state.video_context, state.audio_context))
+        pos_ctx = (state.video_context, state.audio_context)
+        contexts, perts = [pos_ctx], [None]
+        do_uncond = video_guider.do_unconditional_generation() or audio_guider.do_unconditional_generation()
+        do_iso = video_guider.do_isolated_modality_generation() or audio_guider.do_isolated_modality_generation()
+        if do_uncond:
+            contexts.append((state.negative_video_context, state.negative_audio_context))
+            perts.append(None)
+        if do_iso:
+            contexts.append(pos_ctx)
+            perts.append(iso.perturbations[0])
+        same_len = all(c[0].shape == pos_ctx[0].shape and (not audio or c[1].shape == pos_ctx[1].shape)
+                       for c in contexts)
+        if batch_passes and len(contexts) > 1 and same_len:
+            vel = _stacked_passes(model, state, sig, pes, contexts, perts)
+        else:
+            vel = [_velocities(model, state, sig, pes, c[0], c[1], perturbations=None if p is None else iso)
+                   for c, p in zip(contexts, perts)]
+        cond_v, cond_a = den(*vel[0])
         uncond_v = uncond_a = 0.0
-        if video_guider.do_unconditional_generation() or audio_guider.do_unconditional_generation():
-            uncond_v, uncond_a = den(*_velocities(model, state, sig, pes, state.negative_video_context,
-                                                  state.negative_audio_context))
+        if do_uncond:
+            uncond_v, uncond_a = den(*vel[1])
         mod_v = mod_a = 0.0
-        if video_guider.do_isolated_modality_generation() or audio_guider.do_isolated_modality_generation():
-            mod_v, mod_a = den(*_velocities(model, state, sig, pes, state.video_context, state.audio_context,
-                                            perturbations=iso))
+        if do_iso:
+            mod_v, mod_a = den(*vel[-1])
         video_d = video_guider.calculate(cond_v, uncond_v, 0.0, mod_v)
         stepper.step(x_v, video_d, state.sigmas, step, out=x_v)
         if audio:

@@ -239,3 +239,131 @@ def test_multimodal_loop_matches_oracle():
         print(f"step {step}: video cos {cv:.6f} audio cos {ca:.6f}", flush=True)
         assert cv >= 0.999 and ca >= 0.999
         vl, al = got[step]
+
+
+@pytest.mark.parametrize("loop", ["cfg_stg", "multimodal"])
+def test_batched_passes_match_sequential_passes(loop):
+    """The passes of a guided step stacked into one forward (M = passes * T
+    in every projection, attention per pass, perturbed sub-layers skipped for
+    their pass only) against the same passes run one after another, over a
+    3-step trajectory: the latents agree as closely as the loop agrees with the
+    oracle (the projections' kernel / split-K choice changes with M, guidance
+    scales up to 7 amplify the fp32 summation-order differences, and the two
+    trajectories drift apart step by step).  Pass
+    isolation itself is checked bit-exactly by
+    test_stacked_pass_velocities_match_single_passes."""
+    from ltx_amd.components.guiders import (CFGStarRescalingGuider, MultiModalGuider, MultiModalGuiderParams,
+                                            STGGuider)
+    from ltx_amd.components.perturbations import create_batched_stg_config
+    from ltx_amd.pipeline import denoise_cfg_av, denoise_multimodal_av
+
+    print(f"batched vs sequential passes: {loop}", flush=True)
+    steps = 3
+    runs = {}
+    for batched in (True, False):
+        model, state, _, _ = _setup(steps)
+        got = []
+        cb = lambda s, st: got.append((st.video_latent.float().cpu().clone(), st.audio_latent.float().cpu().clone()))
+        if loop == "cfg_stg":
+            denoise_cfg_av(model, state, video_guider=CFGStarRescalingGuider(3.0),
+                           audio_guider=CFGStarRescalingGuider(7.0), stg_guider=STGGuider(1.0),
+                           stg_perturbations=create_batched_stg_config(1, blocks=[1]), stg_cutoff=0.75,
+                           callback=cb, batch_passes=batched)
+        else:
+            denoise_multimodal_av(model, state,
+                                  video_guider=MultiModalGuider(MultiModalGuiderParams(cfg_scale=3.0,
+                                                                                       modality_scale=3.0)),
+                                  audio_guider=MultiModalGuider(MultiModalGuiderParams(cfg_scale=7.0,
+                                                                                       modality_scale=3.0)),
+                                  callback=cb, batch_passes=batched)
+        torch.cuda.synchronize()
+        runs[batched] = got
+    for step in range(steps):
+        (bv, ba), (sv, sa) = runs[True][step], runs[False][step]
+        cv, ca = cos_sim(bv.numpy(), sv.numpy()), cos_sim(ba.numpy(), sa.numpy())
+        rv = (bv - sv).abs().max().item() / sv.abs().max().item()
+        print(f"step {step}: video cos {cv:.7f} rel {rv:.2e} audio cos {ca:.7f}", flush=True)
+        assert cv >= 0.999 and ca >= 0.999
+
+
+def test_stacked_pass_velocities_match_single_passes():
+    """model.velocity over three stacked passes -- positive context, negative
+    context, positive context with block 1's video self-attention skipped.
+    Against stacks of the same shape (same M in every projection, so the same
+    kernels) holding other passes: each pass's velocities are bit-identical --
+    no pass sees another's rows.  Against single-pass forwards (M three times
+    smaller: other kernel / split-K choices): equal to fp32 summation order."""
+    from ltx_amd.components.perturbations import (BatchedPerturbationConfig, PerturbationConfig,
+                                                  create_stg_perturbation)
+
+    print("stacked pass velocities", flush=True)
+    model, state, _, _ = _setup(2)
+    pes = model.rope(state.video_positions, state.audio_positions)
+    sig = state.sigmas_dev[0:1]
+    stg = create_stg_perturbation(blocks=[1])
+    none = PerturbationConfig.empty()
+    pos = (state.video_context, state.audio_context, none)
+    neg = (state.negative_video_context, state.negative_audio_context, none)
+    ptb = (state.video_context, state.audio_context, stg)
+
+    def stacked(passes):
+        v, a = model.velocity(state.video_latent, torch.stack([p[0] for p in passes]), sig, pes,
+                              state.audio_latent, torch.stack([p[1] for p in passes]),
+                              perturbations=BatchedPerturbationConfig([p[2] for p in passes]), passes=len(passes))
+        return v.float().cpu(), a.float().cpu()
+
+    mixed = stacked([pos, neg, ptb])
+    # stacks of the same shape (the third pass perturbed, so every projection
+    # has the same M as in the mixed stack): the positive / negative copies
+    # agree with each other and with the mixed stack's pass
+    ref_pos = stacked([pos, pos, ptb])
+    ref_neg = stacked([neg, neg, ptb])
+    for m in (0, 1):
+        assert torch.equal(ref_pos[m][0], ref_pos[m][1]) and torch.equal(ref_neg[m][0], ref_neg[m][1])
+        assert torch.equal(mixed[m][0], ref_pos[m][0]), f"{'video audio'.split()[m]} positive pass"
+        assert torch.equal(mixed[m][1], ref_neg[m][0]), f"{'video audio'.split()[m]} negative pass"
+        assert torch.equal(mixed[m][2], ref_pos[m][2]) and torch.equal(mixed[m][2], ref_neg[m][2]), \
+            f"{'video audio'.split()[m]} perturbed pass"
+    for i, p in enumerate((pos, neg, ptb)):
+        v1, a1 = model.velocity(state.video_latent, p[0], sig, pes, state.audio_latent, p[1],
+                                perturbations=BatchedPerturbationConfig([p[2]]))
+        for name, got, ref in (("video", mixed[0][i], v1.float().cpu()), ("audio", mixed[1][i], a1.float().cpu())):
+            c = cos_sim(got.numpy(), ref.numpy())
+            print(f"pass {i} {name} stacked vs single: cos {c:.7f}", flush=True)
+            assert c >= 0.9999
+    # the perturbed and negative passes are different forwards than the positive one
+    assert cos_sim(mixed[0][2].numpy(), mixed[0][0].numpy()) < 0.99999
+    assert cos_sim(mixed[0][1].numpy(), mixed[0][0].numpy()) < 0.99999
+
+
+def test_captured_guided_loop_is_bit_identical_to_eager():
+    """The CFG-star + STG + GE loop (stacked passes) captured as one HIP graph
+    per step: replaying the graphs gives the eager loop's latents bit for bit
+    at every step; a second generation (the initial noise written back in
+    place, eager work in between) replays to the same latents again."""
+    from ltx_amd.components.guiders import CFGStarRescalingGuider, STGGuider
+    from ltx_amd.components.perturbations import create_batched_stg_config
+    from ltx_amd.pipeline import CfgAvLoop
+
+    print("captured guided loop", flush=True)
+    steps = 3
+    kw = dict(video_guider=CFGStarRescalingGuider(3.0), audio_guider=CFGStarRescalingGuider(7.0),
+              stg_guider=STGGuider(1.0), stg_perturbations=create_batched_stg_config(1, blocks=[1]),
+              stg_cutoff=0.75, ge_gamma=0.5)
+    model, state, _, _ = _setup(steps)
+    noise = (state.video_latent.clone(), state.audio_latent.clone())
+    eager = []
+    CfgAvLoop(model, state, **kw).run(lambda i, st: eager.append((st.video_latent.clone(), st.audio_latent.clone())))
+    state.video_latent.copy_(noise[0])
+    state.audio_latent.copy_(noise[1])
+    loop = CfgAvLoop(model, state, **kw).capture()
+    for gen in range(2):
+        state.video_latent.copy_(noise[0])
+        state.audio_latent.copy_(noise[1])
+        torch.randn(1 << 20, device="cuda").sum().item()  # unrelated eager work between generations
+        got = []
+        loop.run(lambda i, st: got.append((st.video_latent.clone(), st.audio_latent.clone())))
+        torch.cuda.synchronize()
+        for i in range(steps):
+            assert torch.equal(got[i][0], eager[i][0]), f"generation {gen} step {i} video"
+            assert torch.equal(got[i][1], eager[i][1]), f"generation {gen} step {i} audio"
