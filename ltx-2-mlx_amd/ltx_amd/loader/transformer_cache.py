@@ -23,6 +23,7 @@ written through a temporary file and renamed, metadata last.
 from __future__ import annotations
 
 import json
+import os
 from dataclasses import dataclass
 from pathlib import Path
 from typing import Any
@@ -82,12 +83,54 @@ def cache_artifacts_exist(cache_file: Path) -> bool:
 
 
 def clear_cache_artifacts(cache_file: Path) -> None:
-    """Remove a single-file cache and any shards before a rebuild."""
+    """Remove a cache before a rebuild: ``metadata.json`` first (a cache
+    without it is an incomplete build), then the single file and any shards."""
     cache_file = Path(cache_file)
+    meta = cache_file.parent / METADATA_FILENAME
+    if meta.exists():
+        meta.unlink()
     if cache_file.exists():
         cache_file.unlink()
     for shard in existing_cache_shards(cache_file):
         shard.unlink()
+
+
+def cache_payload(weights_path: str | Path, *, include_audio: bool,
+                  transformer_cache_quantize: str = TRANSFORMER_CACHE_QUANTIZE_OFF) -> dict[str, Any]:
+    """The build description stored as ``metadata.json``, with the fields and
+    values the reference's cache payload has for the builds made here
+    (loader/transformer_cache.py:453-514): schema version, the source file's
+    resolved path / size / mtime, the audio flag, the (empty) layout
+    pretranspose lists, the quantisation mode when not off, and
+    ``fp8_dequant_policy`` 2 for checkpoints holding FP8 tensors -- so the
+    reference's metadata comparison accepts a cache built here."""
+    from .fp8_checkpoint import checkpoint_has_fp8_tensors
+
+    src = Path(weights_path).expanduser().resolve()
+    st = src.stat()
+    payload: dict[str, Any] = {
+        "schema_version": CACHE_SCHEMA_VERSION,
+        "source": {"path": str(src), "size": st.st_size, "mtime_ns": st.st_mtime_ns},
+        "include_audio": bool(include_audio),
+        "video_ff_layout_specs": [],
+        "video_ff_layout_layers": [],
+        "video_attn_layout_specs": [],
+        "video_attn_layout_layers": [],
+    }
+    if transformer_cache_quantize != TRANSFORMER_CACHE_QUANTIZE_OFF:
+        payload["transformer_cache_quantize"] = transformer_cache_quantize
+    if checkpoint_has_fp8_tensors(src):
+        payload["fp8_dequant_policy"] = 2
+    return payload
+
+
+def _write_metadata(cache_file: Path, payload: dict[str, Any]) -> None:
+    """``metadata.json`` through a temporary file and an atomic rename: a
+    reader sees the old file, no file, or the whole new one."""
+    final = Path(cache_file).parent / METADATA_FILENAME
+    tmp = final.with_name(final.name + ".tmp")
+    tmp.write_text(json.dumps(payload, indent=2, sort_keys=True) + "\n")
+    os.replace(tmp, final)
 
 
 def cache_files(cache_file: Path) -> list[Path]:
@@ -268,9 +311,6 @@ def build_transformer_cache(weights_path: str | Path, cache_file: Path, *, inclu
         pending_bytes += t.numel() * t.element_size()
         loaded += 1
     flush()
-    meta = {"schema_version": CACHE_SCHEMA_VERSION, "source": str(Path(weights_path).resolve()),
-            "include_audio": include_audio}
-    if quantize:
-        meta["transformer_cache_quantize"] = transformer_cache_quantize
-    (cache_file.parent / METADATA_FILENAME).write_text(json.dumps(meta, indent=2, sort_keys=True) + "\n")
+    _write_metadata(cache_file, cache_payload(weights_path, include_audio=include_audio,
+                                              transformer_cache_quantize=transformer_cache_quantize))
     return TransformerCacheResult(cache_file, True, loaded, 0, quant)

@@ -294,3 +294,57 @@ def test_stock_checkpoint_bf16(tmp_path):
     for path in Wv["vectors"]:
         Wv["vectors"][path] = W["vectors"][path]
     fx.check_against_named(mv, Wv)
+
+
+def test_build_writes_reference_metadata_last_and_atomically(tmp_path, monkeypatch):
+    """build_transformer_cache on a stock bf16 checkpoint (mode off, host):
+    metadata.json holds the reference's payload fields for such a build
+    (loader/transformer_cache.py:453-514 -- schema version, source path /
+    size / mtime_ns, audio flag, the four empty layout lists; no
+    quantisation key when off), written last with no temporary file left; a
+    rebuild deletes the old metadata.json before it writes any shard, so a
+    build interrupted mid-way leaves no metadata beside partial shards."""
+    import os
+
+    from ltx_amd.loader import transformer_cache as tc
+
+    W = _W(layers=2, audio=True, seed=3)
+    ckpt = tmp_path / "ltx.safetensors"
+    fx.write_safetensors(ckpt, fx.checkpoint_items(W))
+    cache = tmp_path / "cache" / "transformer.safetensors"
+    tc.build_transformer_cache(ckpt, cache, include_audio=True, device="cpu", shard_limit_bytes=1 << 16)
+    meta_path = cache.parent / "metadata.json"
+    meta = json.loads(meta_path.read_text())
+    st = os.stat(ckpt)
+    assert meta == {
+        "schema_version": 1,
+        "source": {"path": str(ckpt.resolve()), "size": st.st_size, "mtime_ns": st.st_mtime_ns},
+        "include_audio": True,
+        "video_ff_layout_specs": [], "video_ff_layout_layers": [],
+        "video_attn_layout_specs": [], "video_attn_layout_layers": [],
+    }
+    assert not list(cache.parent.glob("*.tmp"))
+    shards = tc.existing_cache_shards(cache)
+    assert len(shards) >= 2
+    # every shard is older than (or as old as) the metadata written after it
+    assert all(s.stat().st_mtime_ns <= meta_path.stat().st_mtime_ns for s in shards)
+    # the quantisation mode enters the payload when not off
+    assert tc.cache_payload(ckpt, include_audio=False, transformer_cache_quantize="mxfp8-blocks") == {
+        **{k: v for k, v in meta.items() if k != "include_audio"}, "include_audio": False,
+        "transformer_cache_quantize": "mxfp8-blocks"}
+
+    # a rebuild that fails at its second shard: the old metadata is gone already
+    calls = {"n": 0}
+    real_write = tc.write_safetensors
+
+    def failing_write(path, items, **kw):
+        calls["n"] += 1
+        if calls["n"] == 2:
+            raise OSError("disk full")
+        return real_write(path, items, **kw)
+
+    monkeypatch.setattr(tc, "write_safetensors", failing_write)
+    with pytest.raises(OSError, match="disk full"):
+        tc.build_transformer_cache(ckpt, cache, include_audio=True, device="cpu", shard_limit_bytes=1 << 16)
+    assert not meta_path.exists()
+    assert tc.read_cache_metadata(cache) is None
