@@ -417,6 +417,70 @@ def config5_leg(model, torch, steps_timed: int = 16) -> dict:
             "step_tflops_achieved": round(fl / (ms * 1e-3) / 1e12, 1), "latents_finite": finite}
 
 
+def per_block_leg(torch, args, ta: int, s: int, replays: int = 20) -> dict:
+    """One transformer block at 768x512x65, bf16 weights ~N(0, 0.02), AdaLN
+    rows from the model's timestep MLPs at sigma = 0.5: the video-only block
+    (3456 video + 256 text tokens) and the joint AV block (+ 68 audio
+    tokens, audio on its second stream).  Each block call is captured as a
+    HIP graph and replayed; ms per block call, best of three runs."""
+    from ltx_amd import _lib
+    from ltx_amd.kernels import gemm
+    from ltx_amd.model.transformer.model import LTXModel
+    from ltx_amd.model.transformer.transformer import ADA_ROWS, TransformerArgs
+    from ltx_amd.pipeline import DenoiseState
+
+    res = {}
+    for name, audio in (("video_block_bf16", False), ("av_block_bf16", True)):
+        m = LTXModel(num_layers=1, weight_format="bf16", seed=3, audio=audio)
+        st = DenoiseState(m, args.height, args.width, args.frames, text_tokens=s,
+                          audio_frames=ta if audio else 0, seed=3)
+        vpe, vxpe, ape, axpe = m.rope(st.video_positions, st.audio_positions if audio else None)
+        sig = torch.full((1,), 0.5, device="cuda")
+        stream = torch.cuda.current_stream().cuda_stream
+        vx = gemm.linear(st.video_latent, m.patchify_proj)
+        m._timestep_rows(sig, sig, video=True)
+        _lib.call("ltx_broadcast_add_f32", m.video_tables.data_ptr(), m._temb_v.data_ptr(), m._ada_v.data_ptr(),
+                  1, ADA_ROWS * m.video_dim, stream)
+        video = TransformerArgs(x=vx, context=st.video_context, timesteps=m._temb_v[:9],
+                                positional_embeddings=vpe, cross_positional_embeddings=vxpe)
+        audio_args = None
+        block = m.transformer_blocks[0]
+        block.ada_rows_video = m._ada_v[0]
+        if audio:
+            ax = gemm.linear(st.audio_latent, m.audio_patchify_proj)
+            m._timestep_rows(sig, sig, video=False)
+            _lib.call("ltx_broadcast_add_f32", m.audio_tables.data_ptr(), m._temb_a.data_ptr(), m._ada_a.data_ptr(),
+                      1, ADA_ROWS * m.audio_dim, stream)
+            audio_args = TransformerArgs(x=ax, context=st.audio_context, timesteps=m._temb_a[:9],
+                                         positional_embeddings=ape, cross_positional_embeddings=axpe)
+            block.ada_rows_audio = m._ada_a[0]
+            block.audio_stream = torch.cuda.Stream()
+        def call():
+            block(video, audio_args)
+            if block.audio_stream is not None:  # join the audio stream (the model does after its last block)
+                torch.cuda.current_stream().wait_stream(block.audio_stream)
+
+        call()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            call()
+        g.replay()
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(3):
+            t0 = time.perf_counter()
+            for _ in range(replays):
+                g.replay()
+            torch.cuda.synchronize()
+            best = min(best, (time.perf_counter() - t0) / replays * 1e3)
+        res[name] = {"ms": round(best, 3), "video_tokens": st.video_tokens, "audio_tokens": st.audio_tokens,
+                     "text_tokens": s, "weights": "bf16", "sigma": 0.5, "timing": "hip-graph replay"}
+        del g, m, st, block
+        torch.cuda.empty_cache()
+    return res
+
+
 def guided_step_ms(model, args, ta: int, s: int) -> dict:
     """ms per guided step of the CFG/STG loop (av_pipeline.py:625-757): the
     positive, negative-prompt and STG-perturbed transformer passes stacked
@@ -556,6 +620,9 @@ def main(argv=None):
         out["guided_step"] = guided_step_ms(model, args, ta, s)
     del model, state
     torch.cuda.empty_cache()
+    if not args.no_gemm_shapes:
+        print("# one block (bf16): video and AV", file=sys.stderr, flush=True)
+        out["per_block"] = per_block_leg(torch, args, ta, s)
     if not args.no_gemm_shapes:
         print("# projection GEMM shapes at M=3456", file=sys.stderr, flush=True)
         out["gemm_shapes"] = {fmt: gemm_shapes(torch, fmt) for fmt in ("int8", "mxfp8")}
