@@ -56,24 +56,29 @@ __device__ __forceinline__ void load8f(const float* p, float* out) {
 // ---------------------------------------------------------------------------
 // AdaLN: out = bf16(rms(x) * (1 + scale) + shift)
 // VPL = vectors (8 bf16) per lane = C / 512.
-template <int VPL>
-__global__ __launch_bounds__(kRowBlock) void adaln_kernel(
+// THREADS: workgroup size.  Every workgroup first copies the modulation rows
+// (2 x C fp32) into LDS, so a launch of few rows uses large workgroups (fewer
+// copies per row); a launch of many rows, small ones (more workgroups
+// resident per CU).
+template <int VPL, int THREADS>
+__global__ __launch_bounds__(THREADS) void adaln_kernel(
     const bf16* __restrict__ x, int64_t x_stride, const float* __restrict__ scale,
     const float* __restrict__ shift, bf16* out, int64_t out_stride, int64_t rows,
     float eps, int flags) {
   constexpr int C = VPL * 512;
+  constexpr int WAVES = THREADS / kWave;
   // 1 + scale and shift of the whole row live in LDS (shared by the block's
   // waves) rather than in registers: ~100 fewer VGPRs per lane, twice the
   // waves in flight per SIMD.
   __shared__ __attribute__((aligned(16))) float s_onep[C], s_shift[C];
-  for (int i = threadIdx.x; i < C; i += kRowBlock) {
+  for (int i = threadIdx.x; i < C; i += THREADS) {
     s_onep[i] = 1.0f + scale[i];
     s_shift[i] = shift[i];
   }
   __syncthreads();
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t wave0 = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-  const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
+  const int64_t wave0 = (int64_t)blockIdx.x * WAVES + (threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * WAVES;
   const float inv_c = 1.0f / (float)C;
   const bool round_norm = (flags & LTX_ADALN_ROUND_NORM) != 0;
   const bool no_norm = (flags & LTX_ADALN_NO_NORM) != 0;
@@ -221,21 +226,24 @@ __device__ __forceinline__ void qknorm_rope_row(bf16* row, const float* w_lds, c
   }
 }
 
-template <int PPL, int HALF_VECS>
-__global__ __launch_bounds__(kRowBlock) void qknorm_rope_kernel(
+// THREADS: workgroup size, chosen per launch as for adaln_kernel (each
+// workgroup copies both norm weight rows into LDS first).
+template <int PPL, int HALF_VECS, int THREADS>
+__global__ __launch_bounds__(THREADS) void qknorm_rope_kernel(
     bf16* q, int64_t q_stride, int64_t rows_q, const float* __restrict__ wq,
     const float* cos_q, const float* sin_q, bf16* k, int64_t k_stride, int64_t rows_k,
     const float* __restrict__ wk, const float* cos_k, const float* sin_k, float eps) {
   constexpr int D = PPL * 1024;
+  constexpr int WAVES = THREADS / kWave;
   __shared__ float w_lds[2 * D];
-  for (int i = threadIdx.x; i < D; i += kRowBlock) {
+  for (int i = threadIdx.x; i < D; i += THREADS) {
     w_lds[i] = rows_q > 0 ? wq[i] : 0.0f;
     w_lds[D + i] = rows_k > 0 ? wk[i] : 0.0f;
   }
   __syncthreads();
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t wave0 = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-  const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
+  const int64_t wave0 = (int64_t)blockIdx.x * WAVES + (threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * WAVES;
   const int64_t rows = rows_q > rows_k ? rows_q : rows_k;
   const int64_t half = D / 2;
   const bool shared_table = (cos_q == cos_k) && (sin_q == sin_k);
@@ -429,8 +437,11 @@ static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; 
 // second pass behind a wave's stores).
 constexpr int64_t kMaxStreamRowBlocks = 4096;
 
-static inline int row_grid(int64_t rows, int64_t cap = kMaxRowBlocks) {
-  int64_t blocks = (rows + kWavesPerBlock - 1) / kWavesPerBlock;
+// Row launches of at most this many rows use the large-workgroup forms.
+constexpr int64_t kFewRows = 8192;
+
+static inline int row_grid(int64_t rows, int64_t cap = kMaxRowBlocks, int waves = kWavesPerBlock) {
+  int64_t blocks = (rows + waves - 1) / waves;
   if (blocks > cap) blocks = cap;
   if (blocks < 1) blocks = 1;
   return (int)blocks;
@@ -464,14 +475,20 @@ extern "C" int ltx_adaln_norm_fused_bf16(const void* x, int64_t x_stride, const 
   hipStream_t s = (hipStream_t)stream;
   const bf16* xp = (const bf16*)x;
   bf16* op = (bf16*)out;
-  const int grid = row_grid(rows, kMaxStreamRowBlocks);
+  // few rows: 16-wave workgroups (one LDS copy of the modulation per 16 rows)
+  const bool few = rows <= kFewRows;
+  const int grid = few ? row_grid(rows, kMaxStreamRowBlocks, 16) : row_grid(rows, kMaxStreamRowBlocks);
+#define LTX_ADALN_LAUNCH(V)                                                                                   \
+  (few ? (adaln_kernel<V, 1024><<<grid, 1024, 0, s>>>(xp, x_stride, scale, shift, op, out_stride, rows, eps, flags)) \
+       : (adaln_kernel<V, kRowBlock><<<grid, kRowBlock, 0, s>>>(xp, x_stride, scale, shift, op, out_stride, rows, eps, flags)))
   switch (C / 512) {
-    case 1: adaln_kernel<1><<<grid, kRowBlock, 0, s>>>(xp, x_stride, scale, shift, op, out_stride, rows, eps, flags); break;
-    case 2: adaln_kernel<2><<<grid, kRowBlock, 0, s>>>(xp, x_stride, scale, shift, op, out_stride, rows, eps, flags); break;
-    case 4: adaln_kernel<4><<<grid, kRowBlock, 0, s>>>(xp, x_stride, scale, shift, op, out_stride, rows, eps, flags); break;
-    case 8: adaln_kernel<8><<<grid, kRowBlock, 0, s>>>(xp, x_stride, scale, shift, op, out_stride, rows, eps, flags); break;
+    case 1: LTX_ADALN_LAUNCH(1); break;
+    case 2: LTX_ADALN_LAUNCH(2); break;
+    case 4: LTX_ADALN_LAUNCH(4); break;
+    case 8: LTX_ADALN_LAUNCH(8); break;
     default: return LTX_ERR_UNSUPPORTED;
   }
+#undef LTX_ADALN_LAUNCH
   return ltx_launch_status();
 }
 
@@ -519,13 +536,17 @@ extern "C" int ltx_qknorm_rope_bf16(void* q, int64_t q_stride, int64_t rows_q, c
   const int64_t rows = rows_q > rows_k ? rows_q : rows_k;
   if (rows == 0) return LTX_OK;
   hipStream_t s = (hipStream_t)stream;
-  const int grid = row_grid(rows);
+  // few rows: 8-wave workgroups (one LDS copy of the norm weights per 8 rows)
+  const bool few = rows <= kFewRows;
+  const int grid = few ? row_grid(rows, kMaxRowBlocks, 8) : row_grid(rows);
   bf16* qp = (bf16*)q;
   bf16* kp = (bf16*)k;
-#define LTX_QK_LAUNCH(PPL, HV)                                                              \
-  qknorm_rope_kernel<PPL, HV><<<grid, kRowBlock, 0, s>>>(qp, q_stride, rows_q, wq, cos_q,   \
-                                                        sin_q, kp, k_stride, rows_k, wk,    \
-                                                        cos_k, sin_k, eps)
+#define LTX_QK_LAUNCH(PPL, HV)                                                                          \
+  (few ? (qknorm_rope_kernel<PPL, HV, 512><<<grid, 512, 0, s>>>(qp, q_stride, rows_q, wq, cos_q, sin_q, kp,   \
+                                                               k_stride, rows_k, wk, cos_k, sin_k, eps))      \
+       : (qknorm_rope_kernel<PPL, HV, kRowBlock><<<grid, kRowBlock, 0, s>>>(qp, q_stride, rows_q, wq, cos_q,   \
+                                                                           sin_q, kp, k_stride, rows_k, wk,   \
+                                                                           cos_k, sin_k, eps)))
   const int ppl = (int)(D / 1024);
   if (head_dim == 128) {
     switch (ppl) {
