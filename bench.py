@@ -26,17 +26,20 @@ Prints ONE JSON line.  Besides ms/step and tokens/s it carries:
                 x4, FF up 4096->16384, FF down 16384->4096) in int8 W8A16 and
                 MXFP8, each launch replayed from a HIP graph: ms, TFLOP/s and
                 fraction of the bf16 MFMA peak (the MFMAs are bf16);
-  fused_ops     HBM GB/s of adaln_norm_fused / gated_add_fused at the
-                reference's test shape (T=14640, C=4096) and at 1296 tokens
+  fused_ops     HBM GB/s of the row kernels (AdaLN, gated add, QK-norm +
+                RoPE) at the reference's test shape (T=14640, C=4096), at the
+                step's 3456 video rows (768x512x65) and at 1296 rows
                 (512x288x65), inputs and outputs rotating through >= 1.5 GB
                 (no Infinity-Cache reuse), launches replayed from a HIP graph
                 (kernel time, not host dispatch);
-  config5       ms per step of the same 48-block model at 768x512x121 (6144
-                video + 121 audio + 256 text tokens), the eight distilled
-                steps replayed as HIP graphs;
-  guided_step   ms per step of the CFG/STG guided loop (three transformer
-                passes: positive, negative prompt, STG-perturbed; CFG-star and
-                STG guidance; Euler), eager launches;
+  clip_768x512x121  ms per step of the same 48-block model at 768x512x121
+                (6144 video + 121 audio + 256 text tokens), the eight
+                distilled steps replayed as HIP graphs;
+  guided_step   ms per step of the CFG/STG guided loop (positive, negative
+                prompt and STG-perturbed passes stacked into one forward;
+                CFG-star and STG guidance; Euler), each step a HIP graph;
+  per_block     one bf16 video block and one AV block at 768x512x65, AdaLN
+                rows from the timestep MLPs at sigma 0.5, graph replay;
   cpu_baseline  the oracle (CPU restatement of the reference block) timed on
                 this host for one AV block at the same shapes (1 warmup + 5
                 timed runs; mean and p50), x48.
@@ -80,7 +83,7 @@ def parse_args(argv=None):
                     help="also time this many CFG-star + STG guided steps (3 passes each, eager); 0 skips")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-fused-bench", action="store_true")
-    ap.add_argument("--no-config5", action="store_true", help="skip the 768x512x121 leg")
+    ap.add_argument("--no-clip-768x512x121", action="store_true", help="skip the 768x512x121 leg")
     ap.add_argument("--no-gemm-shapes", action="store_true", help="skip the per-shape GEMM leg")
     ap.add_argument("--cpu-runs", type=int, default=5, help="timed oracle block runs after one warmup")
     ap.add_argument("--counter-workload", choices=["ff-up", "ff-up-vs-library", "copy", "fused-ops"], default=None,
@@ -380,7 +383,7 @@ def gemm_shapes(torch, fmt: str, m: int = 3456) -> dict:
     return res
 
 
-def config5_leg(model, torch, steps_timed: int = 16) -> dict:
+def clip_768x512x121_leg(model, torch, steps_timed: int = 16) -> dict:
     """ms per step at 768x512x121: 6144 video + 121 audio + 256 text tokens,
     the eight distilled steps captured as HIP graphs, one full warmup pass,
     then ``steps_timed`` steps."""
@@ -613,9 +616,9 @@ def main(argv=None):
         "gemm_step": gemm_step,
     }
     del graphs
-    if not args.no_config5 and args.layers == 48:
-        print("# config 5: 768x512x121 graphs", file=sys.stderr, flush=True)
-        out["config5"] = config5_leg(model, torch)
+    if not args.no_clip_768x512x121 and args.layers == 48:
+        print("# 768x512x121: 48-block MXFP8 step graphs", file=sys.stderr, flush=True)
+        out["clip_768x512x121"] = clip_768x512x121_leg(model, torch)
     if args.guided_steps > 0:
         out["guided_step"] = guided_step_ms(model, args, ta, s)
     del model, state
@@ -629,7 +632,8 @@ def main(argv=None):
     if not args.no_fused_bench:
         print("# fused ops", file=sys.stderr, flush=True)
         out["fused_ops"] = fused_op_bandwidth(torch)
-        out["fused_ops"]["config1_T1296"] = fused_op_bandwidth(torch, T=1296)
+        out["fused_ops"]["T3456_768x512x65"] = fused_op_bandwidth(torch, T=3456)
+        out["fused_ops"]["T1296_512x288x65"] = fused_op_bandwidth(torch, T=1296)
     if not args.no_cpu_baseline:
         sys.path.insert(0, str(ROOT))
         print("# cpu baseline (oracle block on host cores) ...", file=sys.stderr, flush=True)

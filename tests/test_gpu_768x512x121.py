@@ -6,12 +6,12 @@ counts.
   reach): every step captured as a HIP graph and replayed in sequence; the
   latents stay finite, the graph replays equal the eager steps bit for bit
   and the concurrent audio stream equals the serial order bit for bit.
-* Oracle at config-5 token counts: one full-width MXFP8 AV block at
+* Oracle at these token counts: one full-width MXFP8 AV block at
   6144 + 121 tokens (normwise max relative error <= 1e-2, cosine >= 0.999
   per stream), and all eight steps of a 4-block full-width MXFP8 model on a
-  384-token grid (per-step latent cosine >= 0.999, the north-star gate).
+  384-token grid (per-step latent cosine >= 0.999).
 
-The audio length follows config 5 as written (121 tokens; the reference's
+The audio length follows the workload as written (121 tokens; the reference's
 formula gives 127 at 24 fps, ``components.patchifiers.audio_latent_frames``).
 Reference: pipelines/av_pipeline.py:899-1146, components/schedulers.py:98.
 """
@@ -29,11 +29,11 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def test_config5_48_blocks_graph_replay_and_streams_bit_identical():
+def test_768x512x121_48_blocks_graph_replay_and_streams_bit_identical():
     from ltx_amd.model.transformer.model import LTXModel
     from ltx_amd.pipeline import DenoiseState, denoise_step
 
-    print("config 5: 48-block MXFP8, 6144 + 121 + 256 tokens, 8 steps", flush=True)
+    print("768x512x121: 48-block MXFP8, 6144 + 121 + 256 tokens, 8 steps", flush=True)
     model = LTXModel(num_layers=48, weight_format="mxfp8", seed=0)
     st = DenoiseState(model, height=512, width=768, frames=121, text_tokens=256, audio_frames=121, seed=0)
     assert (st.video_tokens, st.audio_tokens) == (6144, 121)
@@ -93,22 +93,22 @@ def test_config5_48_blocks_graph_replay_and_streams_bit_identical():
     del graphs
 
 
-def test_config5_av_block_mxfp8_6144_plus_121_vs_oracle():
+def test_768x512x121_av_block_mxfp8_6144_plus_121_vs_oracle():
     from test_gpu_block import _gate, _run
 
-    print("config 5 block: MXFP8 AV block at 6144 + 121 tokens vs oracle", flush=True)
+    print("768x512x121 block: MXFP8 AV block at 6144 + 121 tokens vs oracle", flush=True)
     gv, rv, ga, ra = _run("mxfp8", (16, 16, 24), 121, seed=5)
-    _gate(gv, rv, "config-5 MXFP8 block video")
-    _gate(ga, ra, "config-5 MXFP8 block audio")
+    _gate(gv, rv, "768x512x121 MXFP8 block video")
+    _gate(ga, ra, "768x512x121 MXFP8 block audio")
 
 
-def test_config5_eight_steps_four_blocks_vs_oracle():
+def test_768x512x121_eight_steps_four_blocks_vs_oracle():
     from test_gpu_model import _model_weights
 
     from ltx_amd.model.transformer.model import LTXModel
     from ltx_amd.pipeline import DenoiseState, denoise
 
-    print("config 5 trajectory: 4-block MXFP8, 384 video tokens, 8 steps vs oracle", flush=True)
+    print("768x512x121 trajectory: 4-block MXFP8, 384 video tokens, 8 steps vs oracle", flush=True)
     model = LTXModel(num_layers=4, weight_format="mxfp8", seed=21)
     st = DenoiseState(model, height=256, width=384, frames=25, text_tokens=256, audio_frames=26, seed=7)
     assert st.video_tokens == 4 * 8 * 12

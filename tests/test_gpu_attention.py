@@ -2,7 +2,7 @@
 
 Tolerance: P is rounded to bf16 before the second product (as the
 reference's STEEL kernel does) while the oracle keeps fp32, so outputs agree
-to bf16 precision: normwise max relative error <= 1e-2 (north-star gate) and
+to bf16 precision: normwise max relative error <= 1e-2 (the bf16 tolerance gate) and
 cosine >= 0.9999.
 """
 

@@ -3,10 +3,13 @@
 Configs: the video block at 3456 tokens with 256 text tokens, and the joint
 AV block (3456 video + 68 audio tokens), random-init bf16 weights
 ~N(0, 0.02), AdaLN rows from a sigma-0.5 timestep-like draw.  Gate: the
-north-star bf16 tolerance -- normwise max relative error <= 1e-2 against the
+bf16 tolerance -- normwise max relative error <= 1e-2 against the
 fp32 oracle -- plus cosine >= 0.999 on each stream.  Also the int8 and MXFP8
 weight formats (oracle fed the decoded weights) and the block's contract
 (inputs untouched, disabled modality passed through, perturbation skip).
+Last, the 768x512x65 workload through a one-block model whose AdaLN rows
+come from its own timestep MLPs at sigma 0.5: rows and velocities against
+the oracle.
 """
 
 from __future__ import annotations
@@ -148,3 +151,55 @@ def test_block_contract_passthrough_and_skip():
     vo3, _ = blk(video, None, perturbations=create_batched_stg_config(1, blocks=[4]))
     torch.cuda.synchronize()
     assert not torch.equal(vo2.x, vo3.x)
+
+
+def test_one_block_model_at_768x512x65_sigma_half_timestep_rows():
+    """The 768x512x65 workload (3456 video + 68 audio + 256 text tokens) with
+    AdaLN rows produced by the model's own timestep MLPs at sigma 0.5
+    (model.py:160-187, :1344-1486): a one-block bf16 model, its 16 + 16
+    modulation rows against the oracle's MLPs + tables, then both velocities
+    (patchify, block, output heads) against ``oracle.block.model_velocity``."""
+    from _weights import mlp_weights
+    from ltx_amd.kernels import gemm
+    from ltx_amd.model.transformer.model import LTXModel
+    from ltx_amd.pipeline import DenoiseState
+
+    print("one-block bf16 model, 768x512x65, sigma 0.5", flush=True)
+    m = LTXModel(num_layers=1, weight_format="bf16", seed=4)
+    st = DenoiseState(m, height=512, width=768, frames=65, text_tokens=256, seed=6)
+    assert (st.video_tokens, st.audio_tokens) == (3456, 68)
+    pes = m.rope(st.video_positions, st.audio_positions)
+    sig = torch.full((1,), 0.5, device=DEV)
+    vv, av = m.velocity(st.video_latent, st.video_context, sig, pes, st.audio_latent, st.audio_context)
+    torch.cuda.synchronize()
+
+    def lw(w):
+        return gemm.dequantize(w).float().cpu(), w.bias.float().cpu()
+
+    MW = {"patchify": lw(m.patchify_proj), "audio_patchify": lw(m.audio_patchify_proj),
+          "mlps_v": [mlp_weights(x) for x in (m.adaln_single, m.prompt_adaln_single,
+                                              m.av_ca_video_scale_shift_adaln_single, m.av_ca_a2v_gate_adaln_single)],
+          "mlps_a": [mlp_weights(x) for x in (m.audio_adaln_single, m.audio_prompt_adaln_single,
+                                              m.av_ca_audio_scale_shift_adaln_single, m.av_ca_v2a_gate_adaln_single)],
+          "tables_v": m.video_tables.float().cpu(), "tables_a": m.audio_tables.float().cpu(),
+          "blocks": [block_weights(m.transformer_blocks[0])],
+          "sst_out_v": m.scale_shift_table.float().cpu(), "proj_out_v": lw(m.proj_out),
+          "sst_out_a": m.audio_scale_shift_table.float().cpu(), "proj_out_a": lw(m.audio_proj_out)}
+    # the modulation rows the block consumed: table + [9 | 2 | 4 | 1] MLP rows
+    for key, mlps, d, got in (("v", MW["mlps_v"], 4096, m._ada_v[0]), ("a", MW["mlps_a"], 2048, m._ada_a[0])):
+        rows = torch.cat([ob.adaln_mlp(mlps[0], 500.0)[0], ob.adaln_mlp(mlps[1], 500.0)[0],
+                          ob.adaln_mlp(mlps[2], 500.0)[0], ob.adaln_mlp(mlps[3], 500.0)[0]]).view(16, d)
+        want = (MW[f"tables_{key}"][0] + rows).numpy()
+        rel = max_rel_err(got.cpu().numpy(), want)
+        print(f"{key} AdaLN rows: max_rel_err={rel:.3e}", flush=True)
+        assert rel <= 1e-4, key
+    vpos, apos = st.video_positions, st.audio_positions
+    opes = tuple(tuple(torch.from_numpy(a) for a in p) for p in (
+        orope.rope_tables(vpos, 4096, 32, orope.VIDEO_MAX_POS),
+        orope.rope_tables(vpos[:, 0:1], 2048, 32, orope.AUDIO_MAX_POS),
+        orope.rope_tables(apos, 2048, 32, orope.AUDIO_MAX_POS),
+        orope.rope_tables(apos[:, 0:1], 2048, 32, orope.AUDIO_MAX_POS)))
+    rv, ra = ob.model_velocity(MW, st.video_latent.float().cpu(), st.audio_latent.float().cpu(),
+                               st.video_context.float().cpu(), st.audio_context.float().cpu(), 0.5, opes)
+    _gate(vv.float().cpu().numpy(), rv.numpy(), "768x512x65 video velocity")
+    _gate(av.float().cpu().numpy(), ra.numpy(), "768x512x65 audio velocity")

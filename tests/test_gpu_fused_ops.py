@@ -3,7 +3,7 @@
 Tolerances: each output is one bf16 rounding of an fp32 expression, so the
 kernel may differ from the float64 oracle by at most 1 bf16 ulp where the
 fp32 evaluation order moves a value across a rounding boundary; the
-north-star gate (max relative error <= 1e-2, cosine >= 0.9999 as in the
+bf16 tolerance gate (max relative error <= 1e-2, cosine >= 0.9999 as in the
 reference's tests/test_fused_ops.py:72) is checked as well.
 """
 

@@ -4,7 +4,7 @@
 * In-GEMM dequantisation: bit-exact, shown with A = identity, for which
   C = I @ W'^T is exactly the decoded weight transposed.
 * GEMM + epilogues: bf16 tolerance against the fp32-accumulating oracle --
-  normwise max relative error <= 1e-2 (the north-star bf16 gate), cosine >=
+  normwise max relative error <= 1e-2 (the bf16 tolerance gate), cosine >=
   0.9999 and >= 90 % of outputs bit-identical (the remainder differ by the
   fp32 summation order moving a value across a bf16 rounding boundary).
 """

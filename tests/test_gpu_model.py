@@ -2,7 +2,7 @@
 
 A 2-block model at the full widths (video 4096 / audio 2048, 32 heads) on a
 small latent grid (2x4x6 video tokens, 12 audio tokens, 16 text tokens) so
-the CPU oracle finishes in seconds.  Gate (north star): per-step latent
+the CPU oracle finishes in seconds.  Gate: per-step latent
 cosine >= 0.999 over all 8 steps, for video and audio.  The full-size run
 (48 blocks, 3456 + 68 tokens) is exercised by bench.py and smoke().
 """
