@@ -373,10 +373,18 @@ int ltx_swap_axes(const void* in, int64_t A, int64_t B, int64_t R, int elem_byte
  * pipelines/common.py:242-252).
  * Q (Tq, H*head_dim), K (Tk, H*head_dim), O (Tq, H*head_dim): token-major
  * rows with row strides q_rs/k_rs/o_rs (elements), head h at columns
- * [h*head_dim, (h+1)*head_dim).  V is passed pre-transposed as Vt (H,
- * head_dim, tk_pad), produced by ltx_attn_transpose_v_bf16.  gate: bf16 (Tq, H)
- * with row stride gate_rs, or NULL.  head_dim in {64, 128}.
+ * [h*head_dim, (h+1)*head_dim).  gate: bf16 (Tq, H) with row stride gate_rs,
+ * or NULL.  head_dim in {64, 128}.
+ * ltx_flash_attn_v_bf16 reads V (Tk, H*head_dim) token-major with row stride
+ * v_rs, like Q and K (the projection output as written; the kernel transposes
+ * V fragments on their way out of LDS).  ltx_flash_attn_bf16 takes V
+ * pre-transposed as Vt (H, head_dim, tk_pad), produced by
+ * ltx_attn_transpose_v_bf16; both give bit-identical results.
  */
+int ltx_flash_attn_v_bf16(const void* Q, int64_t q_rs, const void* K, int64_t k_rs,
+                          const void* V, int64_t v_rs, void* O, int64_t o_rs,
+                          const void* gate, int64_t gate_rs, int64_t Tq, int64_t Tk,
+                          int64_t H, int64_t head_dim, float scale, void* stream);
 int64_t ltx_attn_vt_padded_len(int64_t Tk);
 int ltx_attn_transpose_v_bf16(const void* V, int64_t v_rs, int64_t Tk, int64_t H,
                               int64_t head_dim, void* Vt, int64_t tk_pad, void* stream);
@@ -393,9 +401,15 @@ int ltx_flash_attn_bf16(const void* Q, int64_t q_rs, const void* K, int64_t k_rs
  * fp32 sums only).  workspace: device memory of at least
  * ltx_attn_splitkv_workspace_bytes(Tq, H, head_dim, splits) bytes, 16-byte
  * aligned, owned by the caller; concurrent calls need separate workspaces.
- * 1 <= splits <= 256.  Same reference call site as ltx_flash_attn_bf16.
+ * 1 <= splits <= 256.  Same reference call site as ltx_flash_attn_bf16; the
+ * _v_ form reads token-major V as ltx_flash_attn_v_bf16 does.
  */
 int64_t ltx_attn_splitkv_workspace_bytes(int64_t Tq, int64_t H, int64_t head_dim, int64_t splits);
+int ltx_flash_attn_splitkv_v_bf16(const void* Q, int64_t q_rs, const void* K, int64_t k_rs,
+                                  const void* V, int64_t v_rs, void* O, int64_t o_rs,
+                                  const void* gate, int64_t gate_rs, int64_t Tq, int64_t Tk,
+                                  int64_t H, int64_t head_dim, float scale, int64_t splits,
+                                  void* workspace, int64_t workspace_bytes, void* stream);
 int ltx_flash_attn_splitkv_bf16(const void* Q, int64_t q_rs, const void* K, int64_t k_rs,
                                 const void* Vt, int64_t tk_pad, void* O, int64_t o_rs,
                                 const void* gate, int64_t gate_rs, int64_t Tq, int64_t Tk,

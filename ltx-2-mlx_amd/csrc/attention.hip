@@ -61,7 +61,18 @@ __host__ __device__ __forceinline__ int vt_position(int j) {
   return 8 * h + 4 * hi8 + e4;
 }
 
-template <int DH, int WAVES>
+// 16-byte chunk XOR of key row r of a row-major V stage in LDS (DH * 2 bytes
+// per row).  The transposing fragment reads of one instruction cover, per
+// 32-lane half, four rows 16j + 8rr + 4hh + e (e = 0..3) at the same 64-byte
+// column range; the XOR spreads them over all 64 banks: rows e = 0..3 take
+// chunk groups c ^ 4e (256-byte rows), and with 128-byte rows (two rows per
+// bank sweep) rows e and e + 2 take c and c ^ 4.
+template <int DH>
+__host__ __device__ __forceinline__ int vrow_swz(int r) {
+  return DH == 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1);
+}
+
+template <int DH, int WAVES, bool VROW = false>
 struct AttnCfg {
   static constexpr int THREADS = 64 * WAVES;
   static constexpr int QT = 32 * WAVES;    // queries per workgroup
@@ -69,8 +80,9 @@ struct AttnCfg {
   static constexpr int DTILES = DH / 32;   // 32-row tiles of O^T
   static constexpr int K_ROWB = DH * 2;    // bytes per K row in LDS
   static constexpr int K_BYTES = kAttnKB * K_ROWB;
-  static constexpr int V_ROWB = kAttnKB * 2;  // 128 B per Vt row (64 keys)
-  static constexpr int V_BYTES = DH * V_ROWB;
+  // V stage: Vt rows of 128 B (64 keys) or, row-major, 64 key rows of DH * 2 B
+  static constexpr int V_ROWB = VROW ? DH * 2 : kAttnKB * 2;
+  static constexpr int V_BYTES = kAttnKB * DH * 2;
   static constexpr int STAGE = K_BYTES + V_BYTES;
   // per-lane DMA instructions per stage (a wave instruction moves 1 KiB)
   static constexpr int K_DMA = K_BYTES / 1024 / WAVES;
@@ -109,12 +121,15 @@ struct AttnSched {
   }
 };
 
-template <int DH, bool GATED, int WAVES, bool SPLIT>
+// VROW: V is read row-major (Tk rows of stride v_ld elements, head h at
+// columns h*DH ..) and its P.V fragments come from transposing LDS reads;
+// otherwise V arrives as Vt (H, DH, v_ld = Tk_pad) from transpose_v_kernel.
+template <int DH, bool GATED, int WAVES, bool SPLIT, bool VROW>
 __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
     const bf16* __restrict__ Q, int64_t q_rs, const bf16* __restrict__ K, int64_t k_rs,
-    const bf16* __restrict__ Vt, int64_t tk_pad, bf16* __restrict__ O, int64_t o_rs,
+    const bf16* __restrict__ V, int64_t v_ld, bf16* __restrict__ O, int64_t o_rs,
     const bf16* __restrict__ G, int64_t g_rs, int Tq, int Tk, int H, float scale_log2, SplitOut so) {
-  using Cfg = AttnCfg<DH, WAVES>;
+  using Cfg = AttnCfg<DH, WAVES, VROW>;
   constexpr int kAttnQ = Cfg::QT;
   constexpr int DSTEPS = Cfg::DSTEPS, DTILES = Cfg::DTILES;
   constexpr int K_ROWB = Cfg::K_ROWB, K_BYTES = Cfg::K_BYTES, V_ROWB = Cfg::V_ROWB;
@@ -145,7 +160,7 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
   const int q0 = (work % qtiles) * kAttnQ + wave * 32;
 
   const bf16* Kh = K + (int64_t)head * DH;
-  const bf16* Vh = Vt + (int64_t)head * DH * tk_pad;
+  const bf16* Vh = VROW ? V + (int64_t)head * DH : V + (int64_t)head * DH * v_ld;
 
   // ---- Q^T fragments: lane holds Q[q][dstep*16 + hh*8 .. +8] for its query
   bf16x8 qf[DSTEPS];
@@ -171,13 +186,23 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
     k_row[i] = r;
     k_src[i] = (const char*)(Kh) + chunk * 16;
   }
-  // Vt: rows of 128 B (64 keys), 8 rows per block.
+  // Vt: rows of 128 B (64 keys), 8 rows per block.  Row-major V: key rows
+  // like K's, chunks XORed by vrow_swz.
   const char* v_src[V_DMA];
+  int v_row[V_DMA];
 #pragma unroll
   for (int i = 0; i < V_DMA; ++i) {
-    const int r = 8 * (WAVES * i + wave) + (lane >> 3);
-    const int chunk = (lane & 7) ^ ((r >> 1) & 7);
-    v_src[i] = (const char*)(Vh + (int64_t)r * tk_pad) + chunk * 16;
+    if constexpr (VROW) {
+      const int r = K_ROWS_PER * (WAVES * i + wave) + lane / K_CH;
+      const int chunk = (lane % K_CH) ^ vrow_swz<DH>(r);
+      v_row[i] = r;
+      v_src[i] = (const char*)(Vh) + chunk * 16;
+    } else {
+      const int r = 8 * (WAVES * i + wave) + (lane >> 3);
+      const int chunk = (lane & 7) ^ ((r >> 1) & 7);
+      v_row[i] = r;
+      v_src[i] = (const char*)(Vh + (int64_t)r * v_ld) + chunk * 16;
+    }
   }
 
   const int nblocks_all = (Tk + kAttnKB - 1) / kAttnKB;
@@ -205,11 +230,23 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
       }
     }
   };
+  const char* v_blk0[V_DMA];
+#pragma unroll
+  for (int i = 0; i < V_DMA; ++i) v_blk0[i] = VROW ? v_src[i] + (int64_t)v_row[i] * v_ld * 2 : v_src[i];
+  const int64_t v_step = VROW ? (int64_t)kAttnKB * v_ld * 2 : (int64_t)kAttnKB * 2;
   auto issue_v = [&](int kb, int buf) {
     char* Vs = Vs0 + buf * V_BYTES;
+    if (!VROW || (kb + 1) * kAttnKB <= Tk) {
 #pragma unroll
-    for (int i = 0; i < V_DMA; ++i)
-      adma16(v_src[i] + (int64_t)kb * kAttnKB * 2, Vs + (WAVES * i + wave) * 1024);
+      for (int i = 0; i < V_DMA; ++i) adma16(v_blk0[i] + kb * v_step, Vs + (WAVES * i + wave) * 1024);
+    } else {  // last, partial block: rows past Tk repeat row Tk-1 (their P is 0)
+#pragma unroll
+      for (int i = 0; i < V_DMA; ++i) {
+        int key = kb * kAttnKB + v_row[i];
+        key = key < Tk ? key : Tk - 1;
+        adma16(v_src[i] + (int64_t)key * v_ld * 2, Vs + (WAVES * i + wave) * 1024);
+      }
+    }
   };
 
   // Loop-invariant fragment-read offsets; ring buffer, 32-row sub-block and
@@ -220,8 +257,37 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
   int k_addr[DSTEPS], v_addr[4];
 #pragma unroll
   for (int ds = 0; ds < DSTEPS; ++ds) k_addr[ds] = l32 * K_ROWB + (((2 * ds + hh) ^ k_swz) * 16);
+  if constexpr (!VROW) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) v_addr[j] = l32 * V_ROWB + (((2 * j + hh) ^ v_swz) * 16);
+    for (int j = 0; j < 4; ++j) v_addr[j] = l32 * V_ROWB + (((2 * j + hh) ^ v_swz) * 16);
+  } else {
+    // Transposing reads (ds_read_b64_tr_b16): in each 16-lane group, lane i
+    // receives element i % 4 of the 8 bytes that lane 4e + i / 4 addressed,
+    // as its element e.  Lane 16g + 4e + q of a P.V fragment (j, t)
+    // addresses 4 columns 32t + 16(g % 2) + 4q of key row 16j + 8rr + 4hh + e
+    // (rr = 0, 1: the fragment's two reads), so lane (d, hh) receives keys
+    // 16j + 8rr + 4hh + 0..3 of column d -- the P^T key order of its
+    // elements 4rr..4rr+3.  v_addr[t]: the lane's byte offset for rr = j = 0.
+    const int g = lane >> 4, e = (lane >> 2) & 3, q = lane & 3;
+#pragma unroll
+    for (int t = 0; t < DTILES; ++t) {
+      const int chunk = (4 * t + 2 * (g & 1) + (q >> 1)) ^ vrow_swz<DH>(4 * hh + e);
+      v_addr[t] = (4 * hh + e) * V_ROWB + chunk * 16 + 8 * (q & 1);
+    }
+  }
+  // P.V fragment (j, t) of the Vt / V stage at Vb
+  auto read_v = [&](const char* Vb, int j, int t) -> bf16x8 {
+    if constexpr (!VROW) {
+      return *reinterpret_cast<const bf16x8*>(Vb + t * 32 * V_ROWB + v_addr[j]);
+    } else {
+      typedef short v4s __attribute__((ext_vector_type(4)));
+      typedef __attribute__((address_space(3))) v4s* lds_v4s;
+      const char* base = Vb + v_addr[t] + 16 * j * V_ROWB;
+      const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(base));
+      const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(base + 8 * V_ROWB));
+      return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+  };
 
   f32x16 acc[DTILES];
 #pragma unroll
@@ -302,8 +368,7 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
         read_k(P, kn);
       } else if (EXP && kn >= NQ) {
         const int n = kn - NQ;  // first PF Vt fragments of half 2
-        vf[n / DTILES][n % DTILES] =
-            *reinterpret_cast<const bf16x8*>(Vb + (n % DTILES) * 32 * V_ROWB + v_addr[n / DTILES]);
+        vf[n / DTILES][n % DTILES] = read_v(Vb, n / DTILES, n % DTILES);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -359,9 +424,7 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
       }
       __builtin_amdgcn_sched_barrier(0);
       const int nn = n + PF;
-      if (PV && nn < NP)
-        vf[nn / DTILES][nn % DTILES] =
-            *reinterpret_cast<const bf16x8*>(Vb + (nn % DTILES) * 32 * V_ROWB + v_addr[nn / DTILES]);
+      if (PV && nn < NP) vf[nn / DTILES][nn % DTILES] = read_v(Vb, nn / DTILES, nn % DTILES);
       if (NEW && nn == NP) {
         __builtin_amdgcn_sched_barrier(0);
         sync_stage();
@@ -583,37 +646,41 @@ extern "C" int ltx_attn_transpose_v_bf16(const void* V, int64_t v_rs, int64_t Tk
   return ltx_launch_status();
 }
 
-static int attn_check(const void* Q, int64_t q_rs, const void* K, int64_t k_rs, const void* Vt,
-                      int64_t tk_pad, const void* O, int64_t o_rs, const void* gate, int64_t gate_rs,
-                      int64_t Tq, int64_t Tk, int64_t H, int64_t head_dim, float scale) {
-  if (!Q || !K || !Vt || !O || Tq < 0 || Tk <= 0 || H <= 0) return LTX_ERR_INVALID_ARG;
+static int attn_check(const void* Q, int64_t q_rs, const void* K, int64_t k_rs, const void* O, int64_t o_rs,
+                      const void* gate, int64_t gate_rs, int64_t Tq, int64_t Tk, int64_t H, int64_t head_dim,
+                      float scale) {
+  if (!Q || !K || !O || Tq < 0 || Tk <= 0 || H <= 0) return LTX_ERR_INVALID_ARG;
   if (head_dim != 64 && head_dim != 128) return LTX_ERR_UNSUPPORTED;
-  if (tk_pad < ltx_attn_vt_padded_len(Tk) || tk_pad % 64) return LTX_ERR_INVALID_ARG;
   if (q_rs < H * head_dim || k_rs < H * head_dim || o_rs < H * head_dim) return LTX_ERR_INVALID_ARG;
   if (gate && gate_rs < H) return LTX_ERR_INVALID_ARG;
   if (!(scale > 0.0f)) return LTX_ERR_INVALID_ARG;  // the running max is taken before scaling
-  if (!al16a(Q) || !al16a(K) || !al16a(Vt) || !al16a(O) || q_rs % 8 || k_rs % 8 || o_rs % 8)
-    return LTX_ERR_ALIGNMENT;
+  if (!al16a(Q) || !al16a(K) || !al16a(O) || q_rs % 8 || k_rs % 8 || o_rs % 8) return LTX_ERR_ALIGNMENT;
   if (Tq > INT32_MAX || Tk > INT32_MAX) return LTX_ERR_UNSUPPORTED;
   return LTX_OK;
 }
+// V operand: Vt (H, dh, tk_pad) or row-major V (Tk rows of stride v_rs)
+static int attn_check_vt(const void* Vt, int64_t tk_pad, int64_t Tk) {
+  if (!Vt || tk_pad < ltx_attn_vt_padded_len(Tk) || tk_pad % 64) return LTX_ERR_INVALID_ARG;
+  return al16a(Vt) ? LTX_OK : LTX_ERR_ALIGNMENT;
+}
+static int attn_check_v(const void* V, int64_t v_rs, int64_t H, int64_t head_dim) {
+  if (!V || v_rs < H * head_dim) return LTX_ERR_INVALID_ARG;
+  return (al16a(V) && v_rs % 8 == 0) ? LTX_OK : LTX_ERR_ALIGNMENT;
+}
 
-extern "C" int ltx_flash_attn_bf16(const void* Q, int64_t q_rs, const void* K, int64_t k_rs,
-                                   const void* Vt, int64_t tk_pad, void* O, int64_t o_rs,
-                                   const void* gate, int64_t gate_rs, int64_t Tq, int64_t Tk,
-                                   int64_t H, int64_t head_dim, float scale, void* stream) {
-  int st = attn_check(Q, q_rs, K, k_rs, Vt, tk_pad, O, o_rs, gate, gate_rs, Tq, Tk, H, head_dim, scale);
-  if (st != LTX_OK) return st;
+template <bool VROW>
+static int launch_attn(const void* Q, int64_t q_rs, const void* K, int64_t k_rs, const void* V, int64_t v_ld,
+                       void* O, int64_t o_rs, const void* gate, int64_t gate_rs, int64_t Tq, int64_t Tk,
+                       int64_t H, int64_t head_dim, float scale, hipStream_t s) {
   if (Tq == 0) return LTX_OK;
   constexpr int QT = AttnCfg<64, kAttnWaves>::QT;
   const int64_t nwg = (Tq + QT - 1) / QT * H;
   if (nwg > INT32_MAX) return LTX_ERR_UNSUPPORTED;
   const float scale_log2 = scale * 1.4426950408889634f;
-  hipStream_t s = (hipStream_t)stream;
   const SplitOut none{nullptr, nullptr, nullptr, 1};
 #define LTX_FA(DH, G)                                                                              \
-  flash_attn_kernel<DH, G, kAttnWaves, false><<<(int)nwg, 64 * kAttnWaves, 0, s>>>(                \
-      (const bf16*)Q, q_rs, (const bf16*)K, k_rs, (const bf16*)Vt, tk_pad, (bf16*)O, o_rs,          \
+  flash_attn_kernel<DH, G, kAttnWaves, false, VROW><<<(int)nwg, 64 * kAttnWaves, 0, s>>>(          \
+      (const bf16*)Q, q_rs, (const bf16*)K, k_rs, (const bf16*)V, v_ld, (bf16*)O, o_rs,             \
       (const bf16*)gate, gate_rs, (int)Tq, (int)Tk, (int)H, scale_log2, none)
   if (head_dim == 128) {
     if (gate) LTX_FA(128, true); else LTX_FA(128, false);
@@ -624,19 +691,39 @@ extern "C" int ltx_flash_attn_bf16(const void* Q, int64_t q_rs, const void* K, i
   return ltx_launch_status();
 }
 
+extern "C" int ltx_flash_attn_bf16(const void* Q, int64_t q_rs, const void* K, int64_t k_rs,
+                                   const void* Vt, int64_t tk_pad, void* O, int64_t o_rs,
+                                   const void* gate, int64_t gate_rs, int64_t Tq, int64_t Tk,
+                                   int64_t H, int64_t head_dim, float scale, void* stream) {
+  int st = attn_check(Q, q_rs, K, k_rs, O, o_rs, gate, gate_rs, Tq, Tk, H, head_dim, scale);
+  if (st == LTX_OK) st = attn_check_vt(Vt, tk_pad, Tk);
+  if (st != LTX_OK) return st;
+  return launch_attn<false>(Q, q_rs, K, k_rs, Vt, tk_pad, O, o_rs, gate, gate_rs, Tq, Tk, H, head_dim, scale,
+                            (hipStream_t)stream);
+}
+
+extern "C" int ltx_flash_attn_v_bf16(const void* Q, int64_t q_rs, const void* K, int64_t k_rs, const void* V,
+                                     int64_t v_rs, void* O, int64_t o_rs, const void* gate, int64_t gate_rs,
+                                     int64_t Tq, int64_t Tk, int64_t H, int64_t head_dim, float scale,
+                                     void* stream) {
+  int st = attn_check(Q, q_rs, K, k_rs, O, o_rs, gate, gate_rs, Tq, Tk, H, head_dim, scale);
+  if (st == LTX_OK) st = attn_check_v(V, v_rs, H, head_dim);
+  if (st != LTX_OK) return st;
+  return launch_attn<true>(Q, q_rs, K, k_rs, V, v_rs, O, o_rs, gate, gate_rs, Tq, Tk, H, head_dim, scale,
+                           (hipStream_t)stream);
+}
+
 extern "C" int64_t ltx_attn_splitkv_workspace_bytes(int64_t Tq, int64_t H, int64_t head_dim, int64_t splits) {
   if (Tq < 0 || H <= 0 || head_dim <= 0 || splits <= 0) return -1;
   const int64_t rows = splits * Tq * H;
   return rows * head_dim * 4 + 2 * ((rows * 4 + 255) / 256 * 256);
 }
 
-extern "C" int ltx_flash_attn_splitkv_bf16(const void* Q, int64_t q_rs, const void* K, int64_t k_rs,
-                                           const void* Vt, int64_t tk_pad, void* O, int64_t o_rs,
-                                           const void* gate, int64_t gate_rs, int64_t Tq, int64_t Tk,
-                                           int64_t H, int64_t head_dim, float scale, int64_t splits,
-                                           void* workspace, int64_t workspace_bytes, void* stream) {
-  int st = attn_check(Q, q_rs, K, k_rs, Vt, tk_pad, O, o_rs, gate, gate_rs, Tq, Tk, H, head_dim, scale);
-  if (st != LTX_OK) return st;
+template <bool VROW>
+static int launch_attn_splitkv(const void* Q, int64_t q_rs, const void* K, int64_t k_rs, const void* V,
+                               int64_t v_ld, void* O, int64_t o_rs, const void* gate, int64_t gate_rs,
+                               int64_t Tq, int64_t Tk, int64_t H, int64_t head_dim, float scale,
+                               int64_t splits, void* workspace, int64_t workspace_bytes, hipStream_t s) {
   if (splits < 1 || splits > 256 || !workspace) return LTX_ERR_INVALID_ARG;
   if (workspace_bytes < ltx_attn_splitkv_workspace_bytes(Tq, H, head_dim, splits)) return LTX_ERR_INVALID_ARG;
   if (!al16a(workspace)) return LTX_ERR_ALIGNMENT;
@@ -649,13 +736,12 @@ extern "C" int ltx_flash_attn_splitkv_bf16(const void* Q, int64_t q_rs, const vo
   const SplitOut so{(float*)workspace, (float*)((char*)workspace + m_off), (float*)((char*)workspace + l_off),
                     (int)splits};
   const float scale_log2 = scale * 1.4426950408889634f;
-  hipStream_t s = (hipStream_t)stream;
   const int64_t cthreads = Tq * H * (head_dim / 8);
   const int cblocks = (int)((cthreads + 255) / 256);
 #define LTX_FAS(DH, G)                                                                              \
   do {                                                                                              \
-    flash_attn_kernel<DH, false, kAttnSplitWaves, true><<<(int)nwg, 64 * kAttnSplitWaves, 0, s>>>(  \
-        (const bf16*)Q, q_rs, (const bf16*)K, k_rs, (const bf16*)Vt, tk_pad, nullptr, 0, nullptr,   \
+    flash_attn_kernel<DH, false, kAttnSplitWaves, true, VROW><<<(int)nwg, 64 * kAttnSplitWaves, 0, s>>>( \
+        (const bf16*)Q, q_rs, (const bf16*)K, k_rs, (const bf16*)V, v_ld, nullptr, 0, nullptr,      \
         0, (int)Tq, (int)Tk, (int)H, scale_log2, so);                                               \
     attn_combine_kernel<DH, G><<<cblocks, 256, 0, s>>>(so, (bf16*)O, o_rs, (const bf16*)gate,       \
                                                        gate_rs, (int)Tq, (int)H);                    \
@@ -667,6 +753,30 @@ extern "C" int ltx_flash_attn_splitkv_bf16(const void* Q, int64_t q_rs, const vo
   }
 #undef LTX_FAS
   return ltx_launch_status();
+}
+
+extern "C" int ltx_flash_attn_splitkv_bf16(const void* Q, int64_t q_rs, const void* K, int64_t k_rs,
+                                           const void* Vt, int64_t tk_pad, void* O, int64_t o_rs,
+                                           const void* gate, int64_t gate_rs, int64_t Tq, int64_t Tk,
+                                           int64_t H, int64_t head_dim, float scale, int64_t splits,
+                                           void* workspace, int64_t workspace_bytes, void* stream) {
+  int st = attn_check(Q, q_rs, K, k_rs, O, o_rs, gate, gate_rs, Tq, Tk, H, head_dim, scale);
+  if (st == LTX_OK) st = attn_check_vt(Vt, tk_pad, Tk);
+  if (st != LTX_OK) return st;
+  return launch_attn_splitkv<false>(Q, q_rs, K, k_rs, Vt, tk_pad, O, o_rs, gate, gate_rs, Tq, Tk, H, head_dim,
+                                    scale, splits, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+extern "C" int ltx_flash_attn_splitkv_v_bf16(const void* Q, int64_t q_rs, const void* K, int64_t k_rs,
+                                             const void* V, int64_t v_rs, void* O, int64_t o_rs,
+                                             const void* gate, int64_t gate_rs, int64_t Tq, int64_t Tk,
+                                             int64_t H, int64_t head_dim, float scale, int64_t splits,
+                                             void* workspace, int64_t workspace_bytes, void* stream) {
+  int st = attn_check(Q, q_rs, K, k_rs, O, o_rs, gate, gate_rs, Tq, Tk, H, head_dim, scale);
+  if (st == LTX_OK) st = attn_check_v(V, v_rs, H, head_dim);
+  if (st != LTX_OK) return st;
+  return launch_attn_splitkv<true>(Q, q_rs, K, k_rs, V, v_rs, O, o_rs, gate, gate_rs, Tq, Tk, H, head_dim,
+                                   scale, splits, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 // ---- split-KV attention without allocation --------------------------------

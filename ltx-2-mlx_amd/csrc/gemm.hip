@@ -872,6 +872,10 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   tile_coords((int)blockIdx.x, (int)gridDim.x, p.tiles_m, p.tiles_n, tmi, tni);
   const int m0 = tmi * Cfg::BM, n0 = tni * BN;
   const int KT = p.K / Cfg::BK;
+  // a wave whose 128 x 64 sub-tile lies wholly past M or N (the last row or
+  // column of tiles) reads no fragments and issues no MFMAs: it still moves
+  // its share of every stage and meets every barrier
+  const bool live = m0 + wm * WM < p.M && n0 + wn * WN < p.N;
 
   float* col_lds = reinterpret_cast<float*>(lds + Cfg::LDS_BYTES);
 
@@ -1092,13 +1096,13 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
     // memory cluster
     if (oct_start) dma_scales((kt >> 3) + 1);
     dma_stage(kt + 2 < KT ? kt + 2 : KT - 1, (BUF + 2) % kG8Stages);
-    read_stage(kt, bufc);
+    if (live) read_stage(kt, bufc);
     wait_lgkmcnt0();
     if (grp == 1) wait_vmcnt<VM_DMA>();
     barrier_nofence();
     // compute cluster
     __builtin_amdgcn_s_setprio(1);
-    compute_stage(kt);
+    if (live) compute_stage(kt);
     __builtin_amdgcn_s_setprio(0);
     if (grp == 0) {
       if (oct_start) wait_vmcnt<VM_DMA + VM_SCALES>();

@@ -57,6 +57,10 @@ SIGNATURES: dict[str, list] = {
                                     _f32, _i64, _vp, _i64, _vp],
     "ltx_flash_attn_splitkv_noalloc_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64,
                                             _i64, _i64, _f32, _i64, _vp],
+    "ltx_flash_attn_v_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _f32,
+                              _vp],
+    "ltx_flash_attn_splitkv_v_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64,
+                                      _i64, _f32, _i64, _vp, _i64, _vp],
     "ltx_broadcast_add_f32": [_vp, _vp, _vp, _i64, _i64, _vp],
     "ltx_x0_from_velocity_f32": [_vp, _vp, _f32, _vp, _i64, _vp],
     "ltx_guidance_f32": [_vp, _vp, _vp, _vp, _f32, _f32, _f32, _vp, _vp, _vp, _i64, _int, _vp],

@@ -58,11 +58,13 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor | None, he
                     splits: int | None = None) -> torch.Tensor:
     """softmax(q k^T * scale) v per head, optionally times a per-head gate.
 
-    q (Tq, H*dh), k/v (Tk, H*dh) bf16 row views; ``vt`` may carry V already
-    transposed by :func:`transpose_v`.  gate: bf16 (Tq, H) or None.  Returns
-    (Tq, H*dh) bf16 (written into ``out`` when given).  ``splits`` forces the
-    number of key ranges (default :func:`kv_splits`); more than one runs the
-    split-KV kernel pair with a workspace from the torch allocator.
+    q (Tq, H*dh), k/v (Tk, H*dh) bf16 row views; the kernel reads V in that
+    layout (transposing LDS reads).  ``vt`` instead passes V already
+    transposed by :func:`transpose_v` (then ``v`` is unused).  gate: bf16
+    (Tq, H) or None.  Returns (Tq, H*dh) bf16 (written into ``out`` when
+    given).  ``splits`` forces the number of key ranges (default
+    :func:`kv_splits`); more than one runs the split-KV kernel pair with a
+    workspace from the torch allocator.
     """
     d = q.shape[-1]
     dh = d // heads
@@ -73,8 +75,12 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor | None, he
     tq = q.numel() // d
     tk = k.numel() // d
     if vt is None:
-        vt = transpose_v(v, heads)
-    tkp = vt.shape[-1]
+        vv, vs = _lib.row_view(v, d)
+        if v.numel() // d != tk:
+            raise ValueError(f"v has {v.numel() // d} rows, k {tk}")
+        vptr, vld, sfx = _lib.ptr(vv), vs, "_v"
+    else:
+        vptr, vld, sfx = _lib.ptr(vt), vt.shape[-1], ""
     if out is None:
         out = torch.empty((tq, d), dtype=torch.bfloat16, device=q.device)
     ov, os_ = _lib.row_view(out, d)
@@ -92,11 +98,11 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor | None, he
     if splits > 1:
         nbytes = _lib.lib().ltx_attn_splitkv_workspace_bytes(tq, heads, dh, splits)
         ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
-        _lib.call("ltx_flash_attn_splitkv_bf16", _lib.ptr(qv), qs, _lib.ptr(kv), ks, _lib.ptr(vt), tkp,
+        _lib.call(f"ltx_flash_attn_splitkv{sfx}_bf16", _lib.ptr(qv), qs, _lib.ptr(kv), ks, vptr, vld,
                   ov.data_ptr(), os_, gptr, gs, tq, tk, heads, dh, float(scale), splits, ws.data_ptr(), nbytes,
                   _lib.stream_of(q), detail=f"Tq={tq} Tk={tk} H={heads} dh={dh} splits={splits}")
         return out
-    _lib.call("ltx_flash_attn_bf16", _lib.ptr(qv), qs, _lib.ptr(kv), ks, _lib.ptr(vt), tkp, ov.data_ptr(), os_,
+    _lib.call(f"ltx_flash_attn{sfx}_bf16", _lib.ptr(qv), qs, _lib.ptr(kv), ks, vptr, vld, ov.data_ptr(), os_,
               gptr, gs, tq, tk, heads, dh, float(scale), _lib.stream_of(q),
               detail=f"Tq={tq} Tk={tk} H={heads} dh={dh}")
     return out

@@ -9,8 +9,8 @@ fused into as few GEMMs as the data flow allows:
   get the 2*sigmoid epilogue in the same launch);
 * cross-attention: [Wq; Wg] on the query input and [Wk; Wv] on the context.
 
-QK-norm + RoPE run in place on the fused output, V is transposed into the
-attention kernel's layout, the head gate is applied inside the attention
+QK-norm + RoPE run in place on the fused output, the attention kernel reads
+V where the projection wrote it, the head gate is applied inside the attention
 kernel, and ``to_out`` is left to the caller so it can fuse the block's
 residual update into its epilogue.
 """
@@ -57,7 +57,7 @@ class Attention:
         context: (passes*Tk, context_dim) bf16 for cross-attention, sequence
         p's keys in rows [p*Tk, (p+1)*Tk).  pe / k_pe: token-major (cos, sin)
         tables of one sequence, or None.  The projections run once over all
-        rows; QK-norm + RoPE, V's transpose and the attention run per sequence.
+        rows; QK-norm + RoPE and the attention run per sequence.
         """
         inner, heads = self.inner_dim, self.heads
         gate_cols = heads if self.gated else 0
@@ -77,8 +77,7 @@ class Attention:
                 k_tab = None
         if passes == 1:
             qknorm_rope_(q, self.q_norm, pe, k, self.k_norm, k_tab, heads, self.norm_eps)
-            vt = attn_k.transpose_v(v, heads)
-            return attn_k.flash_attention(q, k, None, heads, vt=vt, gate=g)
+            return attn_k.flash_attention(q, k, v, heads, gate=g)
         tq, tk = q.shape[0] // passes, k.shape[0] // passes
         if tq * passes != q.shape[0] or tk * passes != k.shape[0]:
             raise ValueError(f"{q.shape[0]} query / {k.shape[0]} key rows do not split into {passes} passes")
@@ -87,8 +86,7 @@ class Attention:
             qp, kp, vp = q[p * tq:(p + 1) * tq], k[p * tk:(p + 1) * tk], v[p * tk:(p + 1) * tk]
             gp = None if g is None else g[p * tq:(p + 1) * tq]
             qknorm_rope_(qp, self.q_norm, pe, kp, self.k_norm, k_tab, heads, self.norm_eps)
-            vt = attn_k.transpose_v(vp, heads)
-            attn_k.flash_attention(qp, kp, None, heads, vt=vt, gate=gp, out=out[p * tq:(p + 1) * tq])
+            attn_k.flash_attention(qp, kp, vp, heads, gate=gp, out=out[p * tq:(p + 1) * tq])
         return out
 
     def __call__(self, x: torch.Tensor, context: torch.Tensor | None = None, mask=None,

@@ -79,6 +79,28 @@ def test_flash_attention_matches_oracle(tq, tk, H, dh):
     assert cos_sim(got, ref) >= 0.9999
 
 
+@pytest.mark.parametrize("tq,tk,H,dh", CASES)
+def test_row_major_v_equals_transposed_v(tq, tk, H, dh):
+    """The kernel reading V token-major through transposing LDS reads feeds the
+    P.V products the same operands in the same order as the Vt form: outputs
+    are bit-identical, single pass and split-KV, V strided inside a fused
+    [V | K | Q] buffer (ragged last key blocks included)."""
+    from ltx_amd.kernels import attention as A
+
+    rng = np.random.default_rng(tq * 3 + tk)
+    D = H * dh
+    q = _t(_bf(rng, (tq, D), 2.0))
+    kv = _t(_bf(rng, (tk, 2 * D + 16)))
+    k, v = kv[:, D:2 * D], kv[:, :D]
+    g = _t(bf16r(rng.uniform(0, 2, (tq, H)).astype(np.float32)))
+    vt = A.transpose_v(v, H)
+    for splits in (1, 4):
+        a = A.flash_attention(q, k, v, H, gate=g, splits=splits)
+        b = A.flash_attention(q, k, None, H, vt=vt, gate=g, splits=splits)
+        torch.cuda.synchronize()
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), f"splits={splits}"
+
+
 def test_flash_attention_gate_and_strided_qkv():
     """q/k/v as column blocks of one fused projection output; gate fused."""
     from ltx_amd.kernels import attention as A

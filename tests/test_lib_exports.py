@@ -62,6 +62,15 @@ def test_argument_validation_without_gpu():
     assert lib.ltx_adaln_norm_fused_bf16(None, 4096, 16, 16, 16, 4096, 4, 4096, 1e-6, 0, None) == -1
     assert lib.ltx_gemm_bf16(16, 96, 16, 96, None, 16, 64, 4, 64, 96, 0, None, 0, None, 64, None) == -2
     assert lib.ltx_flash_attn_bf16(16, 4096, 16, 4096, 16, 64, 16, 4096, None, 0, 4, 4, 32, 96, 0.1, None) == -2
+    # token-major V: head_dim 96 unsupported, V row stride below H*dh invalid,
+    # misaligned V / odd stride rejected -- all before any launch
+    assert lib.ltx_flash_attn_v_bf16(16, 4096, 16, 4096, 16, 4096, 16, 4096, None, 0, 4, 4, 32, 96, 0.1, None) == -2
+    assert lib.ltx_flash_attn_v_bf16(16, 4096, 16, 4096, 16, 2048, 16, 4096, None, 0, 4, 4, 32, 128, 0.1,
+                                     None) == -1
+    assert lib.ltx_flash_attn_v_bf16(16, 4096, 16, 4096, 24, 4096, 16, 4096, None, 0, 4, 4, 32, 128, 0.1,
+                                     None) == -4
+    assert lib.ltx_flash_attn_splitkv_v_bf16(16, 4096, 16, 4096, 16, 4100, 16, 4096, None, 0, 4, 4, 32, 128, 0.1,
+                                             4, 16, 1 << 20, None) == -4
     # zero rows is a no-op success
     assert lib.ltx_adaln_norm_fused_bf16(16, 4096, 16, 16, 16, 4096, 0, 4096, 1e-6, 0, None) == 0
     # FP8 checkpoint dequant: null codes -> invalid, fp16 output -> unsupported,
