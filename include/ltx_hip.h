@@ -117,6 +117,28 @@ int ltx_qknorm_rope_bf16(void* q, int64_t q_stride, int64_t rows_q, const float*
                          int64_t head_dim, float eps, void* stream);
 
 /*
+ * ltx_qknorm_rope_bf16 with tables factored over the position axes (same
+ * reference call site; the reference builds its per-token tables from
+ * per-axis frequencies, rope.py:92-336).  Each table column depends on one
+ * position axis only, so cos_q / sin_q hold tab_rows_q stacked rows -- a few
+ * per axis -- and idx_q (rows_q, axes_q) int32 selects the token's row of
+ * every axis; the kernel combines them as
+ *   cos = cos_q[idx[t,0]] * cos_q[idx[t,1]] * ...,
+ *   sin = sin_q[idx[t,0]] + sin_q[idx[t,1]] + ...   (fp32, axis order),
+ * a column's foreign-axis rows holding exactly 1 and -0, which reproduces the
+ * per-token table bit for bit while its bytes stay in cache.  idx NULL means
+ * row t of a per-token table (as ltx_qknorm_rope_bf16); 1 <= axes <= 3;
+ * indices outside [0, tab_rows) are clamped.  Same for the k side.
+ */
+int ltx_qknorm_rope_axes_bf16(void* q, int64_t q_stride, int64_t rows_q, const float* wq,
+                              const float* cos_q, const float* sin_q, const int32_t* idx_q,
+                              int64_t axes_q, int64_t tab_rows_q, void* k, int64_t k_stride,
+                              int64_t rows_k, const float* wk, const float* cos_k,
+                              const float* sin_k, const int32_t* idx_k, int64_t axes_k,
+                              int64_t tab_rows_k, int64_t D, int64_t head_dim, float eps,
+                              void* stream);
+
+/*
  * Output head modulation (model.py:1312-1342):
  *   ss     = bf16(table[0:2, :] + emb[:])           (shift row 0, scale row 1)
  *   n      = bf16(LayerNorm(x, no affine, eps))

@@ -177,10 +177,21 @@ __global__ __launch_bounds__(kRowBlock) void gated_add_kernel(
 // consecutive table entries [8p, 8p+8) of the token's (D/2)-wide table row, so
 // each lane reads its own cos/sin with two 16-byte loads per table.  The norm
 // weights live in LDS (read once per workgroup).
+//
+// A token's table row may also be factored over position axes: n rows of
+// stacked per-axis tables whose entries combine as cos = c_0 * c_1 * ...,
+// sin = s_0 + s_1 + ...  Each column belongs to one axis; every other axis
+// holds exactly 1 and -0 there, so the combination reproduces that axis'
+// entry bit for bit (x * 1 = x and x + -0 = x for every float x).
+struct RopeRows {
+  const float* c[3];
+  const float* s[3];
+  int n;  // 0: no RoPE
+};
+
 template <int PPL, int HALF_VECS>
-__device__ __forceinline__ void qknorm_rope_row(bf16* row, const float* w_lds, const float* cosr,
-                                                const float* sinr, float eps, int lane,
-                                                float (&cs)[PPL][8], float (&sn)[PPL][8],
+__device__ __forceinline__ void qknorm_rope_row(bf16* row, const float* w_lds, const RopeRows& tr, float eps,
+                                                int lane, float (&cs)[PPL][8], float (&sn)[PPL][8],
                                                 bool load_table) {
   constexpr int D = PPL * 1024;
   float a[PPL][8], b[PPL][8];
@@ -191,9 +202,22 @@ __device__ __forceinline__ void qknorm_rope_row(bf16* row, const float* w_lds, c
     v1[j] = (p / HALF_VECS) * (2 * HALF_VECS) + (p % HALF_VECS);
     load8(row + v1[j] * 8, a[j]);
     load8(row + (v1[j] + HALF_VECS) * 8, b[j]);
-    if (load_table && cosr != nullptr) {
-      load8f(cosr + p * 8, cs[j]);
-      load8f(sinr + p * 8, sn[j]);
+    if (load_table && tr.n > 0) {
+      load8f(tr.c[0] + p * 8, cs[j]);
+      load8f(tr.s[0] + p * 8, sn[j]);
+#pragma unroll
+      for (int ax = 1; ax < 3; ++ax) {
+        if (ax < tr.n) {
+          float c2[8], s2[8];
+          load8f(tr.c[ax] + p * 8, c2);
+          load8f(tr.s[ax] + p * 8, s2);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            cs[j][i] *= c2[i];
+            sn[j][i] += s2[i];
+          }
+        }
+      }
     }
   }
   float ss = 0.0f;
@@ -213,7 +237,7 @@ __device__ __forceinline__ void qknorm_rope_row(bf16* row, const float* w_lds, c
     for (int i = 0; i < 8; ++i) {
       const float x1 = round_bf(a[j][i] * inv * wa[i]);
       const float x2 = round_bf(b[j][i] * inv * wb[i]);
-      if (cosr != nullptr) {
+      if (tr.n > 0) {
         oa[i] = x1 * cs[j][i] - x2 * sn[j][i];
         ob[i] = x1 * sn[j][i] + x2 * cs[j][i];
       } else {
@@ -228,11 +252,37 @@ __device__ __forceinline__ void qknorm_rope_row(bf16* row, const float* w_lds, c
 
 // THREADS: workgroup size, chosen per launch as for adaln_kernel (each
 // workgroup copies both norm weight rows into LDS first).
+// Table of one operand: per-token rows (idx null: row t of cos / sin), or
+// `axes` factored rows per token, idx[t * axes + a] into the stacked tables of
+// `tab_rows` rows (indices clamped into range); cos null: no RoPE.
+struct RopeTable {
+  const float* cos;
+  const float* sin;
+  const int* idx;
+  int axes;
+  int64_t tab_rows;
+};
+
+__device__ __forceinline__ RopeRows rope_rows(const RopeTable& t, int64_t tok, int64_t half) {
+  RopeRows r;
+  r.n = t.cos == nullptr ? 0 : (t.idx == nullptr ? 1 : t.axes);
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    int64_t row = tok;
+    if (t.idx != nullptr && a < t.axes) {
+      row = t.idx[tok * t.axes + a];
+      row = row < 0 ? 0 : (row < t.tab_rows ? row : t.tab_rows - 1);
+    }
+    r.c[a] = t.cos + row * half;
+    r.s[a] = t.sin + row * half;
+  }
+  return r;
+}
+
 template <int PPL, int HALF_VECS, int THREADS>
 __global__ __launch_bounds__(THREADS) void qknorm_rope_kernel(
-    bf16* q, int64_t q_stride, int64_t rows_q, const float* __restrict__ wq,
-    const float* cos_q, const float* sin_q, bf16* k, int64_t k_stride, int64_t rows_k,
-    const float* __restrict__ wk, const float* cos_k, const float* sin_k, float eps) {
+    bf16* q, int64_t q_stride, int64_t rows_q, const float* __restrict__ wq, RopeTable tq, bf16* k,
+    int64_t k_stride, int64_t rows_k, const float* __restrict__ wk, RopeTable tk, float eps) {
   constexpr int D = PPL * 1024;
   constexpr int WAVES = THREADS / kWave;
   __shared__ float w_lds[2 * D];
@@ -246,21 +296,16 @@ __global__ __launch_bounds__(THREADS) void qknorm_rope_kernel(
   const int64_t nwaves = (int64_t)gridDim.x * WAVES;
   const int64_t rows = rows_q > rows_k ? rows_q : rows_k;
   const int64_t half = D / 2;
-  const bool shared_table = (cos_q == cos_k) && (sin_q == sin_k);
+  const bool shared_table = tq.cos == tk.cos && tq.sin == tk.sin && tq.idx == tk.idx && tq.axes == tk.axes;
   float cs[PPL][8], sn[PPL][8];
   for (int64_t t = wave0; t < rows; t += nwaves) {
     bool have_table = false;
     if (t < rows_q) {
-      qknorm_rope_row<PPL, HALF_VECS>(q + t * q_stride, w_lds,
-                                      cos_q ? cos_q + t * half : nullptr,
-                                      sin_q ? sin_q + t * half : nullptr, eps, lane, cs, sn,
-                                      true);
+      qknorm_rope_row<PPL, HALF_VECS>(q + t * q_stride, w_lds, rope_rows(tq, t, half), eps, lane, cs, sn, true);
       have_table = true;
     }
     if (t < rows_k) {
-      qknorm_rope_row<PPL, HALF_VECS>(k + t * k_stride, w_lds + D,
-                                      cos_k ? cos_k + t * half : nullptr,
-                                      sin_k ? sin_k + t * half : nullptr, eps, lane, cs, sn,
+      qknorm_rope_row<PPL, HALF_VECS>(k + t * k_stride, w_lds + D, rope_rows(tk, t, half), eps, lane, cs, sn,
                                       !(have_table && shared_table));
     }
   }
@@ -518,20 +563,21 @@ extern "C" int ltx_gated_add_fused_bf16(const void* residual, int64_t residual_s
   return ltx_launch_status();
 }
 
-extern "C" int ltx_qknorm_rope_bf16(void* q, int64_t q_stride, int64_t rows_q, const float* wq,
-                                    const float* cos_q, const float* sin_q, void* k,
-                                    int64_t k_stride, int64_t rows_k, const float* wk,
-                                    const float* cos_k, const float* sin_k, int64_t D,
-                                    int64_t head_dim, float eps, void* stream) {
+static int qknorm_rope_launch(void* q, int64_t q_stride, int64_t rows_q, const float* wq, RopeTable tq,
+                              void* k, int64_t k_stride, int64_t rows_k, const float* wk, RopeTable tk,
+                              int64_t D, int64_t head_dim, float eps, void* stream) {
   if (rows_q < 0 || rows_k < 0) return LTX_ERR_INVALID_ARG;
   if (rows_q > 0 && (!q || !wq || q_stride < D)) return LTX_ERR_INVALID_ARG;
   if (rows_k > 0 && (!k || !wk || k_stride < D)) return LTX_ERR_INVALID_ARG;
-  if ((cos_q == nullptr) != (sin_q == nullptr) || (cos_k == nullptr) != (sin_k == nullptr))
-    return LTX_ERR_INVALID_ARG;
+  for (const RopeTable* t : {&tq, &tk}) {
+    if ((t->cos == nullptr) != (t->sin == nullptr)) return LTX_ERR_INVALID_ARG;
+    if (t->idx != nullptr && (t->cos == nullptr || t->axes < 1 || t->axes > 3 || t->tab_rows < 1))
+      return LTX_ERR_INVALID_ARG;
+  }
   if (D <= 0 || D % 1024 != 0 || D > 4096) return LTX_ERR_UNSUPPORTED;
   if (head_dim != 64 && head_dim != 128) return LTX_ERR_UNSUPPORTED;
-  if ((rows_q > 0 && (!aligned16(q) || q_stride % 8 || (cos_q && (!aligned16(cos_q) || !aligned16(sin_q))))) ||
-      (rows_k > 0 && (!aligned16(k) || k_stride % 8 || (cos_k && (!aligned16(cos_k) || !aligned16(sin_k))))))
+  if ((rows_q > 0 && (!aligned16(q) || q_stride % 8 || (tq.cos && (!aligned16(tq.cos) || !aligned16(tq.sin))))) ||
+      (rows_k > 0 && (!aligned16(k) || k_stride % 8 || (tk.cos && (!aligned16(tk.cos) || !aligned16(tk.sin))))))
     return LTX_ERR_ALIGNMENT;
   const int64_t rows = rows_q > rows_k ? rows_q : rows_k;
   if (rows == 0) return LTX_OK;
@@ -542,11 +588,10 @@ extern "C" int ltx_qknorm_rope_bf16(void* q, int64_t q_stride, int64_t rows_q, c
   bf16* qp = (bf16*)q;
   bf16* kp = (bf16*)k;
 #define LTX_QK_LAUNCH(PPL, HV)                                                                          \
-  (few ? (qknorm_rope_kernel<PPL, HV, 512><<<grid, 512, 0, s>>>(qp, q_stride, rows_q, wq, cos_q, sin_q, kp,   \
-                                                               k_stride, rows_k, wk, cos_k, sin_k, eps))      \
-       : (qknorm_rope_kernel<PPL, HV, kRowBlock><<<grid, kRowBlock, 0, s>>>(qp, q_stride, rows_q, wq, cos_q,   \
-                                                                           sin_q, kp, k_stride, rows_k, wk,   \
-                                                                           cos_k, sin_k, eps)))
+  (few ? (qknorm_rope_kernel<PPL, HV, 512><<<grid, 512, 0, s>>>(qp, q_stride, rows_q, wq, tq, kp, k_stride,   \
+                                                               rows_k, wk, tk, eps))                          \
+       : (qknorm_rope_kernel<PPL, HV, kRowBlock><<<grid, kRowBlock, 0, s>>>(qp, q_stride, rows_q, wq, tq, kp, \
+                                                                           k_stride, rows_k, wk, tk, eps)))
   const int ppl = (int)(D / 1024);
   if (head_dim == 128) {
     switch (ppl) {
@@ -565,6 +610,28 @@ extern "C" int ltx_qknorm_rope_bf16(void* q, int64_t q_stride, int64_t rows_q, c
   }
 #undef LTX_QK_LAUNCH
   return ltx_launch_status();
+}
+
+extern "C" int ltx_qknorm_rope_bf16(void* q, int64_t q_stride, int64_t rows_q, const float* wq,
+                                    const float* cos_q, const float* sin_q, void* k,
+                                    int64_t k_stride, int64_t rows_k, const float* wk,
+                                    const float* cos_k, const float* sin_k, int64_t D,
+                                    int64_t head_dim, float eps, void* stream) {
+  const RopeTable tq{cos_q, sin_q, nullptr, 1, 0}, tk{cos_k, sin_k, nullptr, 1, 0};
+  return qknorm_rope_launch(q, q_stride, rows_q, wq, tq, k, k_stride, rows_k, wk, tk, D, head_dim, eps, stream);
+}
+
+extern "C" int ltx_qknorm_rope_axes_bf16(void* q, int64_t q_stride, int64_t rows_q, const float* wq,
+                                         const float* cos_q, const float* sin_q, const int32_t* idx_q,
+                                         int64_t axes_q, int64_t tab_rows_q, void* k, int64_t k_stride,
+                                         int64_t rows_k, const float* wk, const float* cos_k,
+                                         const float* sin_k, const int32_t* idx_k, int64_t axes_k,
+                                         int64_t tab_rows_k, int64_t D, int64_t head_dim, float eps,
+                                         void* stream) {
+  if (axes_q < 1 || axes_q > 3 || axes_k < 1 || axes_k > 3) return LTX_ERR_INVALID_ARG;
+  const RopeTable tq{cos_q, sin_q, idx_q, (int)axes_q, tab_rows_q};
+  const RopeTable tk{cos_k, sin_k, idx_k, (int)axes_k, tab_rows_k};
+  return qknorm_rope_launch(q, q_stride, rows_q, wq, tq, k, k_stride, rows_k, wk, tk, D, head_dim, eps, stream);
 }
 
 extern "C" int ltx_output_norm_modulate_bf16(const void* x, int64_t x_stride, const float* table,

@@ -56,7 +56,8 @@ class Attention:
         Tq tokens stacked by rows (the batched passes of a guided step);
         context: (passes*Tk, context_dim) bf16 for cross-attention, sequence
         p's keys in rows [p*Tk, (p+1)*Tk).  pe / k_pe: token-major (cos, sin)
-        tables of one sequence, or None.  The projections run once over all
+        tables of one sequence (or their factored (cos, sin, idx) form), or
+        None.  The projections run once over all
         rows; QK-norm + RoPE and the attention run per sequence.
         """
         inner, heads = self.inner_dim, self.heads

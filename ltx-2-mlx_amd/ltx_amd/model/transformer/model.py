@@ -147,8 +147,9 @@ class LTXModel:
         return n + sum(m.nbytes() for m in mlps)
 
     def rope(self, video_positions: np.ndarray, audio_positions: np.ndarray | None):
-        """Token-major RoPE tables for a stage: (video self, video cross, audio
-        self, audio cross).
+        """RoPE tables for a stage: (video self, video cross, audio self, audio
+        cross), each token-major (cos, sin) or its factored (cos, sin, idx)
+        form (``rope.factor_tables_np``; ``rope.expand_tables`` restores it).
 
         Tables are built once per distinct set of positions and reused across
         the steps of a stage.  The cache key is a digest of the full position
@@ -163,13 +164,17 @@ class LTXModel:
         hit = self._rope_cache.pop(key, None)
         if hit is None:
             dev = self.device
-            vpe = rope_tables(video_positions, self.video_dim, VIDEO_MAX_POS, dev)
+            # factored over the position axes where that is smaller (video:
+            # a few rows per frame / row / column instead of one per token)
+            vpe = rope_tables(video_positions, self.video_dim, VIDEO_MAX_POS, dev, factored=True)
             vxpe = ape = axpe = None
             if audio_positions is not None and self.audio_config is not None:
                 # cross PE: temporal axis only, dim = audio inner dim (model.py:392-416)
-                vxpe = rope_tables(video_positions[:, 0:1], self.audio_dim, (AUDIO_CROSS_PE_MAX_POS,), dev)
-                ape = rope_tables(audio_positions, self.audio_dim, AUDIO_MAX_POS, dev)
-                axpe = rope_tables(audio_positions[:, 0:1], self.audio_dim, (AUDIO_CROSS_PE_MAX_POS,), dev)
+                vxpe = rope_tables(video_positions[:, 0:1], self.audio_dim, (AUDIO_CROSS_PE_MAX_POS,), dev,
+                                   factored=True)
+                ape = rope_tables(audio_positions, self.audio_dim, AUDIO_MAX_POS, dev, factored=True)
+                axpe = rope_tables(audio_positions[:, 0:1], self.audio_dim, (AUDIO_CROSS_PE_MAX_POS,), dev,
+                                   factored=True)
             hit = (vpe, vxpe, ape, axpe)
         self._rope_cache[key] = hit  # re-inserted: most recently used last
         while len(self._rope_cache) > ROPE_CACHE_ENTRIES:

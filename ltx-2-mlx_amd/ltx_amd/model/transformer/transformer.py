@@ -82,8 +82,9 @@ class TransformerArgs:
     """Arguments passed to transformer blocks (transformer.py:125-157).
 
     ``positional_embeddings`` / ``cross_positional_embeddings`` hold
-    token-major (cos, sin) fp32 tables (T, D/2); reference-layout (1, H, T,
-    dh/2) tables are accepted and converted.  ``timesteps`` is (B, 1, 9, D),
+    token-major (cos, sin) fp32 tables (T, D/2) or their factored (cos, sin,
+    idx) form (``rope.factor_tables_np``); reference-layout (1, H, T, dh/2)
+    tables are accepted and converted.  ``timesteps`` is (B, 1, 9, D),
     ``prompt_timestep`` (B, 1, 2, D), ``cross_scale_shift_timestep`` (B, 1, 4,
     D) and ``cross_gate_timestep`` (B, 1, 1, D), all fp32.
     """
@@ -105,9 +106,10 @@ class TransformerArgs:
 
 
 def _tables(pe):
-    """Accept token-major (T, D/2) or reference (1, H, T, dh/2) tables."""
-    if pe is None:
-        return None
+    """Accept token-major (T, D/2) tables, their factored (cos, sin, idx) form
+    or reference (1, H, T, dh/2) tables."""
+    if pe is None or len(pe) == 3:
+        return pe
     cos, sin = pe
     if cos.dim() == 4:
         from ...kernels.rope_ops import tables_from_reference_layout

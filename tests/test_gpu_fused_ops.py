@@ -194,6 +194,51 @@ def test_qknorm_rope_audio_self_and_cross():
     _qk_case(68, 3456, 2048, 32, atab, vx, seed=3)  # V2A
 
 
+def test_qknorm_rope_factored_tables_bit_identical():
+    """Tables factored over the position axes (stacked per-axis rows + a row
+    index per token and axis) give the same bits as the per-token tables:
+    video self-attention (3 axes, Q and K in one fused buffer, shared table),
+    A2V / V2A (time-only video tables, 1 axis, against per-token audio
+    tables), and 768x512x121's 6144 tokens."""
+    from ltx_amd.kernels.rope_ops import qknorm_rope_
+    from ltx_amd.model.transformer import rope as prope
+
+    def dev(tab):
+        return tuple(torch.from_numpy(np.ascontiguousarray(a)).to(DEV) for a in tab)
+
+    def factored(pos, dim, mp):
+        full = prope.rope_tables_np(pos, dim, mp)
+        return dev(full), dev(prope.factor_tables_np(pos, *full))
+
+    def run(tq, tk, d, variants, seed):
+        rng = np.random.default_rng(seed)
+        buf = _t(_bf(rng, (max(tq, tk), 3 * d), 3.0))
+        wq = _t(rng.uniform(0.5, 1.5, d).astype(np.float32), torch.float32)
+        wk = _t(rng.uniform(0.5, 1.5, d).astype(np.float32), torch.float32)
+        outs = []
+        for pq, pk in variants:
+            b = buf.clone()
+            qknorm_rope_(b[:tq, :d], wq, pq, b[:tk, d:2 * d], wk, pk, 32)
+            outs.append(b)
+        torch.cuda.synchronize()
+        assert not torch.equal(outs[0], buf)
+        for o in outs[1:]:
+            assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16))
+
+    for grid in ((9, 16, 24), (16, 16, 24)):
+        vpos = orope.video_positions(*grid, fps=24.0)
+        t = int(np.prod(grid))
+        full, fac = factored(vpos, 4096, orope.VIDEO_MAX_POS)
+        assert fac[2].shape == (t, 3)
+        run(t, t, 4096, [(full, full), (fac, fac)], seed=grid[0])
+        xfull, xfac = factored(vpos[:, 0:1], 2048, orope.AUDIO_MAX_POS)
+        assert xfac[2].shape == (t, 1)
+        apos = orope.audio_positions(68)
+        atab = dev(prope.rope_tables_np(apos, 2048, orope.AUDIO_MAX_POS))
+        run(t, 68, 2048, [(xfull, atab), (xfac, atab)], seed=grid[0] + 1)  # A2V
+        run(68, t, 2048, [(atab, xfull), (atab, xfac)], seed=grid[0] + 2)  # V2A
+
+
 def test_qknorm_no_rope_text():
     _qk_case(3456, 256, 4096, 32, None, None, seed=4)
     _qk_case(68, 256, 2048, 32, None, None, seed=5)

@@ -11,7 +11,8 @@ import torch
 
 from ltx_amd.model.transformer import model as model_mod
 from ltx_amd.model.transformer.model import LTXModel
-from ltx_amd.model.transformer.rope import audio_positions, rope_tables_np, video_positions, VIDEO_MAX_POS
+from ltx_amd.model.transformer.rope import (VIDEO_MAX_POS, audio_positions, expand_tables, rope_tables_np,
+                                           video_positions)
 
 
 def _stub_model(video_dim=256, audio_dim=64):
@@ -31,10 +32,13 @@ def test_same_shape_same_prefix_positions_get_their_own_tables():
     apos = audio_positions(68)
     pl = m.rope(land, apos)
     pp = m.rope(port, apos)
-    assert not torch.equal(pl[0][0], pp[0][0])
+    assert not torch.equal(expand_tables(pl[0])[0], expand_tables(pp[0])[0])
     for pos, pe in ((land, pl), (port, pp)):
         cos, sin = rope_tables_np(pos, m.video_dim, VIDEO_MAX_POS)
-        assert np.array_equal(pe[0][0].numpy(), cos) and np.array_equal(pe[0][1].numpy(), sin)
+        assert len(pe[0]) == 3  # factored over (frame, row, column)
+        c, s = expand_tables(pe[0])
+        assert np.array_equal(c.numpy().view(np.uint32), cos.view(np.uint32))
+        assert np.array_equal(s.numpy().view(np.uint32), sin.view(np.uint32))
     # a repeated call returns the cached objects
     assert m.rope(land, apos)[0][0] is pl[0][0]
 

@@ -80,3 +80,64 @@ def test_product_tables_match_oracle_bitwise():
         pc, ps = prope.rope_tables_np(pos, dim, mp)
         np.testing.assert_array_equal(pc, oc)
         np.testing.assert_array_equal(ps, os_)
+
+
+def test_factored_tables_expand_to_the_oracle_tables_bitwise():
+    """The per-axis factored form (a few rows per frame / row / column and a
+    row index per token) recombines -- products of cos, sums of sin, in the
+    kernel's axis order -- into the oracle's per-token tables bit for bit:
+    768x512x65 landscape and portrait, 768x512x121, a tiny grid, and the
+    time-only cross-attention tables."""
+    from ltx_amd.model.transformer import rope as prope
+
+    for grid, dim, axes in (((9, 16, 24), 4096, 3), ((9, 24, 16), 4096, 3), ((16, 16, 24), 4096, 3),
+                            ((2, 4, 6), 4096, 3), ((9, 16, 24), 2048, 1), ((16, 16, 24), 2048, 1)):
+        pos = r.video_positions(*grid, 24.0)
+        if axes == 1:
+            pos = pos[:, 0:1]
+        mp = r.VIDEO_MAX_POS if axes == 3 else r.AUDIO_MAX_POS
+        oc, os_ = r.rope_tables(pos, dim, 32, mp)
+        f = prope.factor_tables_np(pos, *prope.rope_tables_np(pos, dim, mp))
+        assert f is not None
+        cos_f, sin_f, idx = f
+        assert idx.shape == (np.prod(grid), axes)
+        assert cos_f.shape[0] == (sum(grid) if axes == 3 else grid[0])
+        c, s = prope.expand_tables_np(cos_f, sin_f, idx)
+        assert np.array_equal(c.view(np.uint32), oc.view(np.uint32))
+        assert np.array_equal(s.view(np.uint32), os_.view(np.uint32))
+    # every token distinct on its one axis (audio): nothing to factor
+    apos = r.audio_positions(68)
+    assert prope.factor_tables_np(apos, *prope.rope_tables_np(apos, 2048, r.AUDIO_MAX_POS)) is None
+
+
+def test_factored_identity_entries_keep_signed_zeros():
+    """Foreign-axis entries must be exactly 1 (cos) and -0 (sin): -0 + x = x for
+    every x, +0 would turn a -0 sin into +0.  A 2-axis table on a 2x3 grid with
+    signed zeros planted in both axes' columns survives factoring bit for bit,
+    and the same form with +0 identities does not."""
+    from ltx_amd.model.transformer import rope as prope
+
+    g = np.random.default_rng(3)
+    ny, nx, half, pad = 2, 3, 7, 1  # columns: pad, then axes 0, 1 alternating
+    yy, xx = np.meshgrid(np.arange(ny), np.arange(nx), indexing="ij")
+    t = ny * nx
+    pos = np.zeros((1, 2, t, 2), np.float32)
+    pos[0, 0, :, 0], pos[0, 1, :, 0] = yy.reshape(-1), xx.reshape(-1)
+    pos[..., 1] = pos[..., 0] + 1
+    vals = {a: g.standard_normal((n, half)).astype(np.float32) for a, n in ((0, ny), (1, nx))}
+    vals[0][0, 1], vals[1][2, 2], vals[0][1, 0] = -0.0, -0.0, 0.0
+    col_axis = np.r_[0, np.arange(half - pad) % 2]
+    cos, sin = np.empty((t, half), np.float32), np.empty((t, half), np.float32)
+    for tok in range(t):
+        for c in range(half):
+            a = col_axis[c]
+            coord = (yy.reshape(-1) if a == 0 else xx.reshape(-1))[tok]
+            cos[tok, c] = vals[a][coord, c] * 0.5
+            sin[tok, c] = vals[a][coord, c]
+    cos_f, sin_f, idx = prope.factor_tables_np(pos, cos, sin)
+    c, s = prope.expand_tables_np(cos_f, sin_f, idx)
+    assert np.array_equal(s.view(np.uint32), sin.view(np.uint32))
+    assert np.array_equal(c.view(np.uint32), cos.view(np.uint32))
+    plus = np.where(np.signbit(sin_f) & (sin_f == 0), np.float32(0.0), sin_f)
+    _, s_plus = prope.expand_tables_np(cos_f, plus, idx)
+    assert not np.array_equal(s_plus.view(np.uint32), sin.view(np.uint32))
