@@ -48,10 +48,16 @@ constexpr int kNumXcdAttn = 8;
 constexpr float kLazyMax = 8.0f;         // log2 headroom before the max is raised
 
 typedef __attribute__((address_space(3))) void* lds_ptr_a;
-typedef __attribute__((address_space(1))) const void* gbl_ptr_a;
 
-__device__ __forceinline__ void adma16(const void* src, char* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds((gbl_ptr_a)src, (lds_ptr_a)lds_wave_base, 16, 0, 0);
+// 16 bytes per lane from base + voff + soff to LDS at lds_dst + 16 * lane: a
+// buffer load with the lds modifier; offsets at or past num_records load
+// zeros.  The descriptor (untyped, 32-bit data format) is built from
+// wave-uniform values, so it lives in scalar registers.
+__device__ __forceinline__ void attn_dma16(const void* base, int num_records, uint32_t voff, int soff,
+                                           char* lds_dst) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, num_records, 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_a)lds_dst, 16, voff, soff, 0, 0);
 }
 
 // Position of key j (0..15 within its 16-key group) in the permuted Vt row:
@@ -139,10 +145,13 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
   constexpr int EPS = 32 / NQ;    // softmax elements per S^T slot
   constexpr int PF = 4;           // fragment reads in flight ahead of their MFMA
   static_assert(NQ >= PF && NP >= PF && 32 % NQ == 0, "slot schedule");
-  // K ring (2 x K_BYTES) followed by the Vt ring (2 x V_BYTES)
-  __shared__ __attribute__((aligned(1024))) char lds[2 * (K_BYTES + V_BYTES)];
+  // K ring (RING x K_BYTES) followed by the V ring (RING x V_BYTES): a ring of
+  // 4 lets the workgroup synchronise every other key block (the split-KV
+  // tiles, two workgroups per CU, keep 2)
+  constexpr int RING = SPLIT ? 2 : 4;
+  __shared__ __attribute__((aligned(1024))) char lds[RING * (K_BYTES + V_BYTES)];
   char* const Ks0 = lds;
-  char* const Vs0 = lds + 2 * K_BYTES;
+  char* const Vs0 = lds + RING * K_BYTES;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hh = lane >> 5, l32 = lane & 31;
@@ -173,35 +182,37 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
   }
 
   // ---- DMA sources.  Wave instruction i fills the 1 KiB LDS block
-  // WAVES*i + wave.  K: 1024/K_ROWB rows per block.
+  // WAVES*i + wave.  K: 1024/K_ROWB rows per block.  Buffer loads: a
+  // descriptor per operand (scalar registers) whose record count ends at the
+  // last key row of this head, one 32-bit per-lane offset, and the block's
+  // advance as the scalar offset.  Rows past Tk in the last block lie past
+  // the record count and load as zeros (their scores are masked, their P is
+  // 0).
   constexpr int K_ROWS_PER = 1024 / K_ROWB;      // 4 (dh 128) or 8 (dh 64)
   constexpr int K_CH = K_ROWB / 16;               // 16-byte chunks per row
-  const char* k_src[K_DMA];
-  int k_row[K_DMA];
+  const int k_records = (int)((int64_t)(Tk - 1) * k_rs * 2 + DH * 2);
+  uint32_t k_voff[K_DMA];
 #pragma unroll
   for (int i = 0; i < K_DMA; ++i) {
     const int r = K_ROWS_PER * (WAVES * i + wave) + lane / K_CH;
     const int slot = lane % K_CH;
     const int chunk = (K_CH == 16) ? (slot ^ (r & 15)) : (slot ^ ((r >> 1) & 7));
-    k_row[i] = r;
-    k_src[i] = (const char*)(Kh) + chunk * 16;
+    k_voff[i] = (uint32_t)(r * k_rs * 2 + chunk * 16);
   }
   // Vt: rows of 128 B (64 keys), 8 rows per block.  Row-major V: key rows
   // like K's, chunks XORed by vrow_swz.
-  const char* v_src[V_DMA];
-  int v_row[V_DMA];
+  const int v_records = VROW ? (int)((int64_t)(Tk - 1) * v_ld * 2 + DH * 2) : (int)(DH * v_ld * 2);
+  uint32_t v_voff[V_DMA];
 #pragma unroll
   for (int i = 0; i < V_DMA; ++i) {
     if constexpr (VROW) {
       const int r = K_ROWS_PER * (WAVES * i + wave) + lane / K_CH;
       const int chunk = (lane % K_CH) ^ vrow_swz<DH>(r);
-      v_row[i] = r;
-      v_src[i] = (const char*)(Vh) + chunk * 16;
+      v_voff[i] = (uint32_t)(r * v_ld * 2 + chunk * 16);
     } else {
       const int r = 8 * (WAVES * i + wave) + (lane >> 3);
       const int chunk = (lane & 7) ^ ((r >> 1) & 7);
-      v_row[i] = r;
-      v_src[i] = (const char*)(Vh + (int64_t)r * v_ld) + chunk * 16;
+      v_voff[i] = (uint32_t)(r * v_ld * 2 + chunk * 16);
     }
   }
 
@@ -211,42 +222,17 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
   const int kb0 = split * per_split;
   const int kb1 = (kb0 + per_split) < nblocks_all ? (kb0 + per_split) : nblocks_all;
   const int nb = kb1 > kb0 ? kb1 - kb0 : 0;
-  // K row k_row[i] of key block 0; a block advances every row by k_step bytes
-  const char* k_blk0[K_DMA];
-#pragma unroll
-  for (int i = 0; i < K_DMA; ++i) k_blk0[i] = k_src[i] + (int64_t)k_row[i] * k_rs * 2;
-  const int64_t k_step = (int64_t)kAttnKB * k_rs * 2;
+  const int k_step = (int)(kAttnKB * k_rs * 2);
+  const int v_step = VROW ? (int)(kAttnKB * v_ld * 2) : kAttnKB * 2;
   auto issue_k = [&](int kb, int buf) {
     char* Ks = Ks0 + buf * K_BYTES;
-    if ((kb + 1) * kAttnKB <= Tk) {
 #pragma unroll
-      for (int i = 0; i < K_DMA; ++i) adma16(k_blk0[i] + kb * k_step, Ks + (WAVES * i + wave) * 1024);
-    } else {  // last, partial block: rows past Tk repeat row Tk-1 (their scores are masked)
-#pragma unroll
-      for (int i = 0; i < K_DMA; ++i) {
-        int key = kb * kAttnKB + k_row[i];
-        key = key < Tk ? key : Tk - 1;
-        adma16(k_src[i] + (int64_t)key * k_rs * 2, Ks + (WAVES * i + wave) * 1024);
-      }
-    }
+    for (int i = 0; i < K_DMA; ++i) attn_dma16(Kh, k_records, k_voff[i], kb * k_step, Ks + (WAVES * i + wave) * 1024);
   };
-  const char* v_blk0[V_DMA];
-#pragma unroll
-  for (int i = 0; i < V_DMA; ++i) v_blk0[i] = VROW ? v_src[i] + (int64_t)v_row[i] * v_ld * 2 : v_src[i];
-  const int64_t v_step = VROW ? (int64_t)kAttnKB * v_ld * 2 : (int64_t)kAttnKB * 2;
   auto issue_v = [&](int kb, int buf) {
     char* Vs = Vs0 + buf * V_BYTES;
-    if (!VROW || (kb + 1) * kAttnKB <= Tk) {
 #pragma unroll
-      for (int i = 0; i < V_DMA; ++i) adma16(v_blk0[i] + kb * v_step, Vs + (WAVES * i + wave) * 1024);
-    } else {  // last, partial block: rows past Tk repeat row Tk-1 (their P is 0)
-#pragma unroll
-      for (int i = 0; i < V_DMA; ++i) {
-        int key = kb * kAttnKB + v_row[i];
-        key = key < Tk ? key : Tk - 1;
-        adma16(v_src[i] + (int64_t)key * v_ld * 2, Vs + (WAVES * i + wave) * 1024);
-      }
-    }
+    for (int i = 0; i < V_DMA; ++i) attn_dma16(Vh, v_records, v_voff[i], kb * v_step, Vs + (WAVES * i + wave) * 1024);
   };
 
   // Loop-invariant fragment-read offsets; ring buffer, 32-row sub-block and
@@ -259,7 +245,7 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
   for (int ds = 0; ds < DSTEPS; ++ds) k_addr[ds] = l32 * K_ROWB + (((2 * ds + hh) ^ k_swz) * 16);
   if constexpr (!VROW) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) v_addr[j] = l32 * V_ROWB + (((2 * j + hh) ^ v_swz) * 16);
+    for (int j = 0; j < 4; ++j) v_addr[j] = RING * K_BYTES + l32 * V_ROWB + (((2 * j + hh) ^ v_swz) * 16);
   } else {
     // Transposing reads (ds_read_b64_tr_b16): in each 16-lane group, lane i
     // receives element i % 4 of the 8 bytes that lane 4e + i / 4 addressed,
@@ -272,17 +258,19 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
 #pragma unroll
     for (int t = 0; t < DTILES; ++t) {
       const int chunk = (4 * t + 2 * (g & 1) + (q >> 1)) ^ vrow_swz<DH>(4 * hh + e);
-      v_addr[t] = (4 * hh + e) * V_ROWB + chunk * 16 + 8 * (q & 1);
+      v_addr[t] = RING * K_BYTES + (4 * hh + e) * V_ROWB + chunk * 16 + 8 * (q & 1);
     }
   }
-  // P.V fragment (j, t) of the Vt / V stage at Vb
-  auto read_v = [&](const char* Vb, int j, int t) -> bf16x8 {
+  // P.V fragment (j, t) of the Vt / V stage in ring slot `slot`.  v_addr holds
+  // LDS byte offsets from the start of the array, V ring base included, so
+  // every slot / fragment offset fits a read's 16-bit immediate.
+  auto read_v = [&](int slot, int j, int t) -> bf16x8 {
     if constexpr (!VROW) {
-      return *reinterpret_cast<const bf16x8*>(Vb + t * 32 * V_ROWB + v_addr[j]);
+      return *reinterpret_cast<const bf16x8*>(lds + v_addr[j] + slot * V_BYTES + t * 32 * V_ROWB);
     } else {
       typedef short v4s __attribute__((ext_vector_type(4)));
       typedef __attribute__((address_space(3))) v4s* lds_v4s;
-      const char* base = Vb + v_addr[t] + 16 * j * V_ROWB;
+      const char* base = lds + v_addr[t] + slot * V_BYTES + 16 * j * V_ROWB;
       const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(base));
       const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(base + 8 * V_ROWB));
       return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
@@ -344,13 +332,15 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
     kf[k >> 1][k & 1] =
         *reinterpret_cast<const bf16x8*>(Ks0 + buf * K_BYTES + (k & 1) * 32 * K_ROWB + k_addr[k >> 1]);
   };
-  // Half 1 of iteration b (parity P): S^T of block b from K buffer P into
-  // s[P] (its first PF K fragments already in flight); remaining exps of
-  // block b-1 (s[1-P]); first Vt reads of half 2.
-  auto half1 = [&](auto pc, auto qkc, auto expc) {
-    constexpr int P = decltype(pc)::value;
+  // Iteration b runs with Q = b % RING (compile-time): block b sits in ring
+  // slot Q of K and V, its S^T in s[P], P = b & 1.
+  // Half 1 of iteration b: S^T of block b from K slot Q into s[P] (its first
+  // PF K fragments already in flight); remaining exps of block b-1 (s[1-P]);
+  // first V reads of half 2 (block b-1, slot Q-1).
+  auto half1 = [&](auto qc, auto qkc, auto expc) {
+    constexpr int Q = decltype(qc)::value, P = Q & 1;
     constexpr bool QK = decltype(qkc)::value, EXP = decltype(expc)::value;
-    const char* Vb = Vs0 + (1 - P) * V_BYTES;
+    constexpr int VSLOT = (Q + RING - 1) % RING;
     if (QK) {
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb)
@@ -365,10 +355,10 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
       if (EXP) do_exps(std::integral_constant<int, 1 - P>(), NP + k);
       const int kn = k + PF;
       if (QK && kn < NQ) {
-        read_k(P, kn);
+        read_k(Q, kn);
       } else if (EXP && kn >= NQ) {
         const int n = kn - NQ;  // first PF Vt fragments of half 2
-        vf[n / DTILES][n % DTILES] = read_v(Vb, n / DTILES, n % DTILES);
+        vf[n / DTILES][n % DTILES] = read_v(VSLOT, n / DTILES, n % DTILES);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -394,18 +384,22 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
   };
-  // Half 2 of iteration b (parity P): P.V of block b-1 from Vt buffer 1-P;
-  // row max of block b (s[P]), the running-max update, first exps of block b.
-  // The running max (log2 domain) is raised only when a block's max exceeds
-  // it by more than 2^kLazyMax; O^T is rescaled just before the next P.V.
-  // Stage sync (NEW only), once this wave has issued its last Vt read of the
-  // half: K_{b+1} and Vt_b become resident, every wave is done with K_b and
-  // Vt_{b-1}, whose buffers then receive K_{b+2} and Vt_{b+1}; the remaining
-  // slots read the first K fragments of block b+1.
-  auto half2 = [&](auto pc, auto pvc, auto newc, int b) {
-    constexpr int P = decltype(pc)::value;
+  // Half 2 of iteration b: P.V of block b-1 from V slot Q-1; row max of
+  // block b (s[P]), the running-max update, first exps of block b.  The
+  // running max (log2 domain) is raised only when a block's max exceeds it by
+  // more than 2^kLazyMax; O^T is rescaled just before the next P.V.
+  // Stage sync (NEW only), once this wave has issued its last V read of the
+  // half: every wave is done with K_b and V_{b-1} (and all older blocks), and
+  // every load issued before it is resident.  RING 2 syncs every iteration
+  // and then loads K_{b+2} and V_{b+1} into the slots just freed.  RING 4
+  // syncs at b = 0, loading K_2, K_3, V_1, V_2, and at every odd b, loading
+  // K_{b+3}, K_{b+4}, V_{b+2}, V_{b+3} into the slots of K_{b-1}, K_b,
+  // V_{b-2}, V_{b-1}: each block is loaded before the sync that precedes its
+  // first read.  The remaining slots read the first K fragments of block b+1.
+  auto half2 = [&](auto qc, auto pvc, auto newc, int b) {
+    constexpr int Q = decltype(qc)::value, P = Q & 1;
     constexpr bool PV = decltype(pvc)::value, NEW = decltype(newc)::value;
-    const char* Vb = Vs0 + (1 - P) * V_BYTES;
+    constexpr int VSLOT = (Q + RING - 1) % RING;
     const int kb = kb0 + b;
     if (PV && __any(alpha_pend != 1.0f)) {
 #pragma unroll
@@ -413,7 +407,7 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[t][e] *= alpha_pend;
     }
-    if (NEW) mask_tail(pc, kb);
+    if (NEW) mask_tail(std::integral_constant<int, P>(), kb);
     float mx = -INFINITY;
 #pragma unroll
     for (int n = 0; n < NP; ++n) {
@@ -424,15 +418,29 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
       }
       __builtin_amdgcn_sched_barrier(0);
       const int nn = n + PF;
-      if (PV && nn < NP) vf[nn / DTILES][nn % DTILES] = read_v(Vb, nn / DTILES, nn % DTILES);
+      if (PV && nn < NP) vf[nn / DTILES][nn % DTILES] = read_v(VSLOT, nn / DTILES, nn % DTILES);
       if (NEW && nn == NP) {
         __builtin_amdgcn_sched_barrier(0);
-        sync_stage();
-        if (b + 2 < nb) issue_k(kb + 2, P);
-        if (b + 1 < nb) issue_v(kb + 1, 1 - P);
+        if constexpr (RING == 2) {
+          sync_stage();
+          if (b + 2 < nb) issue_k(kb + 2, Q);
+          if (b + 1 < nb) issue_v(kb + 1, (Q + 1) % RING);
+        } else if constexpr ((Q & 1) == 1) {
+          sync_stage();
+          if (b + 3 < nb) issue_k(kb + 3, (Q + 3) % RING);
+          if (b + 4 < nb) issue_k(kb + 4, Q);
+          if (b + 2 < nb) issue_v(kb + 2, (Q + 2) % RING);
+          if (b + 3 < nb) issue_v(kb + 3, (Q + 3) % RING);
+        } else if (b == 0) {
+          sync_stage();
+          if (2 < nb) issue_k(kb0 + 2, 2);
+          if (3 < nb) issue_k(kb0 + 3, 3);
+          if (1 < nb) issue_v(kb0 + 1, 1);
+          if (2 < nb) issue_v(kb0 + 2, 2);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
-      if (NEW && nn >= NP && b + 1 < nb) read_k(1 - P, nn - NP);
+      if (NEW && nn >= NP && b + 1 < nb) read_k((Q + 1) % RING, nn - NP);
       if (NEW) {
         if (n < Sch::F) {
 #pragma unroll
@@ -450,7 +458,7 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
           alpha_pend = alpha;
           neg_m = -m_run;
         } else {
-          do_exps(pc, n);
+          do_exps(std::integral_constant<int, P>(), n);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -458,12 +466,19 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2 % RING>;
+  using I3 = std::integral_constant<int, 3 % RING>;
   using BT = std::integral_constant<bool, true>;
   using BF = std::integral_constant<bool, false>;
-  // iteration b in [1, nb) with parity P = b & 1
-  auto body = [&](auto pc, int b) {
-    half1(pc, BT(), BT());
-    half2(pc, BT(), BT(), b);
+  // iteration b in [1, nb), Q = b % RING
+  auto body = [&](auto qc, int b) {
+    half1(qc, BT(), BT());
+    half2(qc, BT(), BT(), b);
+  };
+  // drain (iteration nb): last exps and P.V of block nb-1
+  auto drain = [&](auto qc) {
+    half1(qc, BF(), BT());
+    half2(qc, BT(), BF(), 0);
   };
 
   if (nb > 0) {
@@ -476,17 +491,31 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
     half1(I0(), BT(), BF());
     half2(I0(), BF(), BT(), 0);
     int b = 1;
-    for (; b + 1 < nb; b += 2) {
-      body(I1(), b);
-      body(I0(), b + 1);
+    if constexpr (RING == 2) {
+      for (; b + 1 < nb; b += 2) {
+        body(I1(), b);
+        body(I0(), b + 1);
+      }
+      if (b < nb) body(I1(), b);
+      if (nb & 1) drain(I1()); else drain(I0());
+    } else {
+      for (; b + 3 < nb; b += 4) {
+        body(I1(), b);
+        body(I2(), b + 1);
+        body(I3(), b + 2);
+        body(I0(), b + 3);
+      }
+      // b % 4 == 1 here; up to three more iterations
+      if (b < nb) body(I1(), b++);
+      if (b < nb) body(I2(), b++);
+      if (b < nb) body(I3(), b++);
+      switch (nb % 4) {
+        case 0: drain(I0()); break;
+        case 1: drain(I1()); break;
+        case 2: drain(I2()); break;
+        default: drain(I3()); break;
+      }
     }
-    if (b < nb) body(I1(), b);
-    // drain (iteration nb): last exps and P.V of block nb-1
-    auto drain = [&](auto pc) {
-      half1(pc, BF(), BT());
-      half2(pc, BT(), BF(), 0);
-    };
-    if (nb & 1) drain(I1()); else drain(I0());
   }
 
   const int q = q0 + l32;
@@ -656,15 +685,19 @@ static int attn_check(const void* Q, int64_t q_rs, const void* K, int64_t k_rs, 
   if (!(scale > 0.0f)) return LTX_ERR_INVALID_ARG;  // the running max is taken before scaling
   if (!al16a(Q) || !al16a(K) || !al16a(O) || q_rs % 8 || k_rs % 8 || o_rs % 8) return LTX_ERR_ALIGNMENT;
   if (Tq > INT32_MAX || Tk > INT32_MAX) return LTX_ERR_UNSUPPORTED;
+  // K (and token-major V) are addressed by 32-bit buffer offsets
+  if ((Tk + 64) * k_rs * 2 > INT32_MAX) return LTX_ERR_UNSUPPORTED;
   return LTX_OK;
 }
 // V operand: Vt (H, dh, tk_pad) or row-major V (Tk rows of stride v_rs)
 static int attn_check_vt(const void* Vt, int64_t tk_pad, int64_t Tk) {
   if (!Vt || tk_pad < ltx_attn_vt_padded_len(Tk) || tk_pad % 64) return LTX_ERR_INVALID_ARG;
+  if (128 * tk_pad * 2 > INT32_MAX) return LTX_ERR_UNSUPPORTED;
   return al16a(Vt) ? LTX_OK : LTX_ERR_ALIGNMENT;
 }
-static int attn_check_v(const void* V, int64_t v_rs, int64_t H, int64_t head_dim) {
+static int attn_check_v(const void* V, int64_t v_rs, int64_t Tk, int64_t H, int64_t head_dim) {
   if (!V || v_rs < H * head_dim) return LTX_ERR_INVALID_ARG;
+  if ((Tk + 64) * v_rs * 2 > INT32_MAX) return LTX_ERR_UNSUPPORTED;
   return (al16a(V) && v_rs % 8 == 0) ? LTX_OK : LTX_ERR_ALIGNMENT;
 }
 
@@ -707,7 +740,7 @@ extern "C" int ltx_flash_attn_v_bf16(const void* Q, int64_t q_rs, const void* K,
                                      int64_t Tq, int64_t Tk, int64_t H, int64_t head_dim, float scale,
                                      void* stream) {
   int st = attn_check(Q, q_rs, K, k_rs, O, o_rs, gate, gate_rs, Tq, Tk, H, head_dim, scale);
-  if (st == LTX_OK) st = attn_check_v(V, v_rs, H, head_dim);
+  if (st == LTX_OK) st = attn_check_v(V, v_rs, Tk, H, head_dim);
   if (st != LTX_OK) return st;
   return launch_attn<true>(Q, q_rs, K, k_rs, V, v_rs, O, o_rs, gate, gate_rs, Tq, Tk, H, head_dim, scale,
                            (hipStream_t)stream);
@@ -773,7 +806,7 @@ extern "C" int ltx_flash_attn_splitkv_v_bf16(const void* Q, int64_t q_rs, const 
                                              int64_t H, int64_t head_dim, float scale, int64_t splits,
                                              void* workspace, int64_t workspace_bytes, void* stream) {
   int st = attn_check(Q, q_rs, K, k_rs, O, o_rs, gate, gate_rs, Tq, Tk, H, head_dim, scale);
-  if (st == LTX_OK) st = attn_check_v(V, v_rs, H, head_dim);
+  if (st == LTX_OK) st = attn_check_v(V, v_rs, Tk, H, head_dim);
   if (st != LTX_OK) return st;
   return launch_attn_splitkv<true>(Q, q_rs, K, k_rs, V, v_rs, O, o_rs, gate, gate_rs, Tq, Tk, H, head_dim,
                                    scale, splits, workspace, workspace_bytes, (hipStream_t)stream);
