@@ -11,23 +11,25 @@
 //
 // Layouts (token-major, as produced by the projections):
 //   Q: (Tq, H*dh) with row stride q_rs; K: (Tk, H*dh) with row stride k_rs;
-//   V is consumed pre-transposed by ltx_attn_transpose_v_bf16 into
-//   Vt (H, dh, Tk_pad), Tk_pad = ceil(Tk/64)*64, zero-padded, with the keys of
-//   every 16-key group permuted so that each lane's 8 keys of a P.V fragment
-//   are contiguous (see vt_position).
+//   V either token-major like K (its P.V fragments come from transposing LDS
+//   reads) or pre-transposed by ltx_attn_transpose_v_bf16 into Vt (H, dh,
+//   Tk_pad), Tk_pad = ceil(Tk/64)*64, zero-padded, with the keys of every
+//   16-key group permuted so that each lane's 8 keys of a P.V fragment are
+//   contiguous (see vt_position).  Both forms give the same bits.
 //
 // Kernel structure: one workgroup = 8 waves = 256 queries of one head; each
 // wave owns 32 queries and two waves share a SIMD.  Scores are computed
 // transposed, S^T = K Q^T, with v_mfma_f32_32x32x16_bf16: each lane then
 // holds one query's scores in registers, so the row max / row sum are
 // lane-local plus one cross-half exchange (v_permlane32_swap), and P^T feeds
-// the P.V MFMA straight from registers (O^T += Vt . P^T).  K and Vt stream
-// through LDS in 64-key stages by direct global->LDS DMA, double buffered.
+// the P.V MFMA straight from registers (O^T += Vt . P^T).  K and V stream
+// through LDS in 64-key stages by direct global->LDS buffer loads, in rings
+// of 4 stages (a workgroup sync every other stage; 2 for the split-KV tiles).
 // Key blocks are software-pipelined inside each wave, because VALU work only
 // overlaps the issuing wave's own MFMAs: the softmax of block b is cut into
 // one piece per MFMA slot (row max, running-max update, then exp2 / row sum
 // / bf16 pack) spread over the P.V MFMAs of block b-1 and the S^T MFMAs of
-// block b+1.  The stage barrier sits after a wave's last Vt read of a P.V
+// block b+1.  The stage barrier sits after a wave's last V read of a P.V
 // half, so the K fragments of the next block are read behind the remaining
 // MFMAs.  The running max is raised only when a block's max exceeds it by
 // more than 2^8 (P then stays <= 256, exact in fp32 and bf16-relative as any
