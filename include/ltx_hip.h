@@ -78,6 +78,19 @@ int ltx_adaln_norm_fused_bf16(const void* x, int64_t x_stride, const float* scal
                               int64_t rows, int64_t C, float eps, int flags,
                               void* stream);
 
+/*
+ * Two modulations of one row norm: out as ltx_adaln_norm_fused_bf16 with
+ * (scale, shift), out2 with (scale2, shift2), each row read once.  The
+ * reference's block modulates the same pre-cross-attention norm of a stream
+ * twice, for its A2V and its V2A input (transformer.py:535-564); bit-identical
+ * to two ltx_adaln_norm_fused_bf16 calls.  out2 row stride out2_stride.
+ */
+int ltx_adaln_norm_fused2_bf16(const void* x, int64_t x_stride, const float* scale,
+                               const float* shift, void* out, int64_t out_stride,
+                               const float* scale2, const float* shift2, void* out2,
+                               int64_t out2_stride, int64_t rows, int64_t C, float eps,
+                               int flags, void* stream);
+
 /* ---- flags for ltx_gated_add_fused_bf16 ----------------------------------- */
 /* Round branch*gate to bf16 before the add: `x + (attn_out*gate).astype(bf16)`
  * of the text cross-attention (transformer.py:387, :484). */

@@ -46,6 +46,13 @@ int main(int argc, char** argv) {
   EXPECT(ltx_adaln_norm_fused_bf16(d, 3584, fd, fd, d, 3584, 4, 3584, 1e-6f, 0, nullptr), LTX_ERR_UNSUPPORTED);
   EXPECT(ltx_adaln_norm_fused_bf16(m, 4096, fd, fd, d, 4096, 4, 4096, 1e-6f, 0, nullptr), LTX_ERR_ALIGNMENT);
   EXPECT(ltx_adaln_norm_fused_bf16(d, 4096, fd, fd, d, 4096, 0, 4096, 1e-6f, 0, nullptr), LTX_OK);
+  EXPECT(ltx_adaln_norm_fused2_bf16(d, 4096, fd, fd, d, 4096, fd, fd, nullptr, 4096, 4, 4096, 1e-6f, 0, nullptr),
+         LTX_ERR_INVALID_ARG);
+  EXPECT(ltx_adaln_norm_fused2_bf16(d, 4096, fd, fd, d, 4096, fd, nullptr, d, 4096, 4, 4096, 1e-6f, 0, nullptr),
+         LTX_ERR_INVALID_ARG);
+  EXPECT(ltx_adaln_norm_fused2_bf16(d, 4096, fd, fd, d, 4096, fd, fd, m, 4096, 4, 4096, 1e-6f, 0, nullptr),
+         LTX_ERR_ALIGNMENT);
+  EXPECT(ltx_adaln_norm_fused2_bf16(d, 4096, fd, fd, d, 4096, fd, fd, d, 4096, 0, 4096, 1e-6f, 0, nullptr), LTX_OK);
   EXPECT(ltx_gated_add_fused_bf16(nullptr, 4096, d, 4096, fd, d, 4096, 4, 4096, 0, nullptr), LTX_ERR_INVALID_ARG);
   EXPECT(ltx_gated_add_fused_bf16(d, 4096, d, 4096, fd, d, 4096, 4, 1000, 0, nullptr), LTX_ERR_UNSUPPORTED);
   EXPECT(ltx_gated_add_fused_bf16(d, 4096, d, 4096, fd, d, 4096, 0, 4096, 0, nullptr), LTX_OK);

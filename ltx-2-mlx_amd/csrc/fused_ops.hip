@@ -60,20 +60,26 @@ __device__ __forceinline__ void load8f(const float* p, float* out) {
 // (2 x C fp32) into LDS, so a launch of few rows uses large workgroups (fewer
 // copies per row); a launch of many rows, small ones (more workgroups
 // resident per CU).
-template <int VPL, int THREADS>
+// NOUT = 2: one read of each row, two modulations of the same norm (scale2,
+// shift2 into out2) -- the A2V and V2A inputs of one stream.
+template <int VPL, int THREADS, int NOUT = 1>
 __global__ __launch_bounds__(THREADS) void adaln_kernel(
     const bf16* __restrict__ x, int64_t x_stride, const float* __restrict__ scale,
-    const float* __restrict__ shift, bf16* out, int64_t out_stride, int64_t rows,
-    float eps, int flags) {
+    const float* __restrict__ shift, bf16* out, int64_t out_stride, const float* __restrict__ scale2,
+    const float* __restrict__ shift2, bf16* out2, int64_t out2_stride, int64_t rows, float eps, int flags) {
   constexpr int C = VPL * 512;
   constexpr int WAVES = THREADS / kWave;
   // 1 + scale and shift of the whole row live in LDS (shared by the block's
   // waves) rather than in registers: ~100 fewer VGPRs per lane, twice the
   // waves in flight per SIMD.
-  __shared__ __attribute__((aligned(16))) float s_onep[C], s_shift[C];
+  __shared__ __attribute__((aligned(16))) float s_onep[NOUT][C], s_shift[NOUT][C];
   for (int i = threadIdx.x; i < C; i += THREADS) {
-    s_onep[i] = 1.0f + scale[i];
-    s_shift[i] = shift[i];
+    s_onep[0][i] = 1.0f + scale[i];
+    s_shift[0][i] = shift[i];
+    if constexpr (NOUT == 2) {
+      s_onep[NOUT - 1][i] = 1.0f + scale2[i];
+      s_shift[NOUT - 1][i] = shift2[i];
+    }
   }
   __syncthreads();
   const int lane = threadIdx.x & (kWave - 1);
@@ -88,8 +94,6 @@ __global__ __launch_bounds__(THREADS) void adaln_kernel(
     // they would pin the modulation in registers again).
     int z;
     asm volatile("v_mov_b32 %0, 0" : "=v"(z));
-    const float* onep = s_onep + z;
-    const float* shp = s_shift + z;
     const bf16* xr = x + r * x_stride;
     // the row stays packed (bf16) in registers and is widened where used:
     // half the VGPRs of a float copy, more rows in flight per SIMD
@@ -110,20 +114,25 @@ __global__ __launch_bounds__(THREADS) void adaln_kernel(
       ss = wave_sum(ss);
       inv = rsqrt_rn(ss * inv_c + eps);
     }
-    bf16* orow = out + r * out_stride;
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-      const int c0 = (lane + j * kWave) * 8;
-      float op[8], sh[8], o[8];
-      load8f(onep + c0, op);
-      load8f(shp + c0, sh);
+    for (int k = 0; k < NOUT; ++k) {
+      const float* onep = s_onep[k] + z;
+      const float* shp = s_shift[k] + z;
+      bf16* orow = k == 0 ? out + r * out_stride : out2 + r * out2_stride;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float n = (float)xv[j][i] * inv;
-        if (round_norm) n = round_bf(n);
-        o[i] = n * op[i] + sh[i];
+      for (int j = 0; j < VPL; ++j) {
+        const int c0 = (lane + j * kWave) * 8;
+        float op[8], sh[8], o[8];
+        load8f(onep + c0, op);
+        load8f(shp + c0, sh);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float n = (float)xv[j][i] * inv;
+          if (round_norm) n = round_bf(n);
+          o[i] = n * op[i] + sh[i];
+        }
+        store8_stream(orow + c0, o);
       }
-      store8_stream(orow + c0, o);
     }
   }
 }
@@ -506,26 +515,30 @@ extern "C" const char* ltx_status_string(int status) {
 
 extern "C" int ltx_version(void) { return 100; }
 
-extern "C" int ltx_adaln_norm_fused_bf16(const void* x, int64_t x_stride, const float* scale,
-                                         const float* shift, void* out, int64_t out_stride,
-                                         int64_t rows, int64_t C, float eps, int flags,
-                                         void* stream) {
-  if (rows < 0 || !x || !scale || !shift || !out) return LTX_ERR_INVALID_ARG;
+static int adaln_launch(const void* x, int64_t x_stride, const float* scale, const float* shift, void* out,
+                        int64_t out_stride, const float* scale2, const float* shift2, void* out2,
+                        int64_t out2_stride, int64_t rows, int64_t C, float eps, int flags, void* stream) {
+  const bool dual = out2 != nullptr;
+  if (rows < 0 || !x || !scale || !shift || !out || (dual && (!scale2 || !shift2))) return LTX_ERR_INVALID_ARG;
   if (C <= 0 || C % 512 != 0 || C > 4096) return LTX_ERR_UNSUPPORTED;
-  if (x_stride < C || out_stride < C) return LTX_ERR_INVALID_ARG;
-  if (!aligned16(x) || !aligned16(out) || !aligned16(scale) || !aligned16(shift) ||
-      x_stride % 8 || out_stride % 8)
+  if (x_stride < C || out_stride < C || (dual && out2_stride < C)) return LTX_ERR_INVALID_ARG;
+  if (!aligned16(x) || !aligned16(out) || !aligned16(scale) || !aligned16(shift) || x_stride % 8 ||
+      out_stride % 8 || (dual && (!aligned16(out2) || !aligned16(scale2) || !aligned16(shift2) || out2_stride % 8)))
     return LTX_ERR_ALIGNMENT;
   if (rows == 0) return LTX_OK;
   hipStream_t s = (hipStream_t)stream;
   const bf16* xp = (const bf16*)x;
   bf16* op = (bf16*)out;
+  bf16* op2 = (bf16*)out2;
   // few rows: 16-wave workgroups (one LDS copy of the modulation per 16 rows)
   const bool few = rows <= kFewRows;
   const int grid = few ? row_grid(rows, kMaxStreamRowBlocks, 16) : row_grid(rows, kMaxStreamRowBlocks);
+#define LTX_ADALN_ARGS xp, x_stride, scale, shift, op, out_stride, scale2, shift2, op2, out2_stride, rows, eps, flags
 #define LTX_ADALN_LAUNCH(V)                                                                                   \
-  (few ? (adaln_kernel<V, 1024><<<grid, 1024, 0, s>>>(xp, x_stride, scale, shift, op, out_stride, rows, eps, flags)) \
-       : (adaln_kernel<V, kRowBlock><<<grid, kRowBlock, 0, s>>>(xp, x_stride, scale, shift, op, out_stride, rows, eps, flags)))
+  (dual ? (few ? (adaln_kernel<V, 1024, 2><<<grid, 1024, 0, s>>>(LTX_ADALN_ARGS))                             \
+               : (adaln_kernel<V, kRowBlock, 2><<<grid, kRowBlock, 0, s>>>(LTX_ADALN_ARGS)))                    \
+        : (few ? (adaln_kernel<V, 1024, 1><<<grid, 1024, 0, s>>>(LTX_ADALN_ARGS))                             \
+               : (adaln_kernel<V, kRowBlock, 1><<<grid, kRowBlock, 0, s>>>(LTX_ADALN_ARGS))))
   switch (C / 512) {
     case 1: LTX_ADALN_LAUNCH(1); break;
     case 2: LTX_ADALN_LAUNCH(2); break;
@@ -534,7 +547,26 @@ extern "C" int ltx_adaln_norm_fused_bf16(const void* x, int64_t x_stride, const 
     default: return LTX_ERR_UNSUPPORTED;
   }
 #undef LTX_ADALN_LAUNCH
+#undef LTX_ADALN_ARGS
   return ltx_launch_status();
+}
+
+extern "C" int ltx_adaln_norm_fused_bf16(const void* x, int64_t x_stride, const float* scale,
+                                         const float* shift, void* out, int64_t out_stride,
+                                         int64_t rows, int64_t C, float eps, int flags,
+                                         void* stream) {
+  return adaln_launch(x, x_stride, scale, shift, out, out_stride, nullptr, nullptr, nullptr, 0, rows, C, eps, flags,
+                      stream);
+}
+
+extern "C" int ltx_adaln_norm_fused2_bf16(const void* x, int64_t x_stride, const float* scale,
+                                          const float* shift, void* out, int64_t out_stride,
+                                          const float* scale2, const float* shift2, void* out2,
+                                          int64_t out2_stride, int64_t rows, int64_t C, float eps, int flags,
+                                          void* stream) {
+  if (!out2) return LTX_ERR_INVALID_ARG;
+  return adaln_launch(x, x_stride, scale, shift, out, out_stride, scale2, shift2, out2, out2_stride, rows, C, eps,
+                      flags, stream);
 }
 
 extern "C" int ltx_gated_add_fused_bf16(const void* residual, int64_t residual_stride,

@@ -57,6 +57,8 @@ SIGNATURES: dict[str, list] = {
                                     _f32, _i64, _vp, _i64, _vp],
     "ltx_flash_attn_splitkv_noalloc_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64,
                                             _i64, _i64, _f32, _i64, _vp],
+    "ltx_adaln_norm_fused2_bf16": [_vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _int,
+                                   _vp],
     "ltx_qknorm_rope_axes_bf16": [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _vp,
                                   _vp, _i64, _i64, _i64, _i64, _f32, _vp],
     "ltx_flash_attn_v_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _f32,

@@ -119,6 +119,19 @@ def adaln_rows(x2d: torch.Tensor, x_stride: int, scale: torch.Tensor, shift: tor
     )
 
 
+def adaln_rows2(x2d: torch.Tensor, x_stride: int, scale: torch.Tensor, shift: torch.Tensor, out2d: torch.Tensor,
+                scale2: torch.Tensor, shift2: torch.Tensor, out2_2d: torch.Tensor, rows: int, c: int, eps: float,
+                flags: int) -> None:
+    """Two modulations of one row norm (one read of x): out = AdaLN(x, scale,
+    shift), out2 = AdaLN(x, scale2, shift2), both with row stride c."""
+    _lib.call(
+        "ltx_adaln_norm_fused2_bf16",
+        _lib.ptr(x2d), x_stride, _lib.ptr(scale), _lib.ptr(shift), _lib.ptr(out2d), c, _lib.ptr(scale2),
+        _lib.ptr(shift2), _lib.ptr(out2_2d), c, rows, c, float(eps), flags, _lib.stream_of(x2d),
+        detail=f"rows={rows} C={c} (two outputs)",
+    )
+
+
 def adaln_norm_fused(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, eps: float) -> torch.Tensor:
     """Fused RMSNorm + AdaLN modulation: ``rms_norm(x) * (1+scale) + shift``.
 

@@ -127,6 +127,17 @@ def adaln(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, eps: float,
     return out
 
 
+def adaln2(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, scale2: torch.Tensor, shift2: torch.Tensor,
+           eps: float, flags: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Two AdaLN modulations of the same rows (one read of x, one norm)."""
+    t, c = x.shape
+    xv, xs = _lib.row_view(x, c)
+    out = torch.empty((t, c), dtype=torch.bfloat16, device=x.device)
+    out2 = torch.empty((t, c), dtype=torch.bfloat16, device=x.device)
+    fused_ops.adaln_rows2(xv, xs, scale, shift, out, scale2, shift2, out2, t, c, eps, flags)
+    return out, out2
+
+
 class BasicAVTransformerBlock:
     """Audio-video transformer block (transformer.py:160-674)."""
 
@@ -391,12 +402,12 @@ class BasicAVTransformerBlock:
             vpe = _tables(video.cross_positional_embeddings)
             ape = _tables(audio.cross_positional_embeddings)
             # modulated inputs of both directions from the pre-A2V streams
-            vs_a2v = adaln(v2, ada_v[ROW_SCALE_A2V], ada_v[ROW_SHIFT_A2V], eps, rn)
-            vs_v2a = adaln(v2, ada_v[ROW_SCALE_V2A], ada_v[ROW_SHIFT_V2A], eps, rn)
+            vs_a2v, vs_v2a = adaln2(v2, ada_v[ROW_SCALE_A2V], ada_v[ROW_SHIFT_A2V], ada_v[ROW_SCALE_V2A],
+                                    ada_v[ROW_SHIFT_V2A], eps, rn)
             ev_v = main.record_event() if side is not None else None
             with on_audio():
-                as_a2v = adaln(a2, ada_a[ROW_SCALE_A2V], ada_a[ROW_SHIFT_A2V], eps, rn)
-                as_v2a = adaln(a2, ada_a[ROW_SCALE_V2A], ada_a[ROW_SHIFT_V2A], eps, rn)
+                as_a2v, as_v2a = adaln2(a2, ada_a[ROW_SCALE_A2V], ada_a[ROW_SHIFT_A2V], ada_a[ROW_SCALE_V2A],
+                                        ada_a[ROW_SHIFT_V2A], eps, rn)
             if side is not None:
                 main.wait_event(side.record_event())
                 as_a2v.record_stream(main)

@@ -82,6 +82,27 @@ def test_adaln_kernel_flag_forms(flags):
     _assert_close_bf16(bf16_from_torch(out), ref)
 
 
+@pytest.mark.parametrize("T,C,flags", [(3456, 4096, 1), (68, 2048, 1), (20000, 4096, 0), (300, 4096, 2)])
+def test_adaln_two_outputs_equal_two_single_calls(T, C, flags):
+    """The two-output AdaLN (A2V and V2A inputs of one stream) equals two
+    single-output calls bit for bit (those are checked against the oracle
+    above), over the large-workgroup and the grid-stride launch forms."""
+    from ltx_amd.kernels.fused_ops import adaln_rows, adaln_rows2
+
+    rng = np.random.default_rng(T + C + flags)
+    x = _bf(rng, (T, C), 2.0)
+    s1, h1, s2, h2 = (_t(rng.standard_normal(C).astype(np.float32) * 0.1, torch.float32) for _ in range(4))
+    xt = _t(x)
+    a, b = torch.empty_like(xt), torch.empty_like(xt)
+    adaln_rows2(xt, C, s1, h1, a, s2, h2, b, T, C, 1e-6, flags)
+    ra, rb = torch.empty_like(xt), torch.empty_like(xt)
+    adaln_rows(xt, C, s1, h1, ra, C, T, C, 1e-6, flags)
+    adaln_rows(xt, C, s2, h2, rb, C, T, C, 1e-6, flags)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), ra.view(torch.int16))
+    assert torch.equal(b.view(torch.int16), rb.view(torch.int16))
+
+
 def test_adaln_special_cases_exact():
     """scale = -1 makes the output exactly bf16(shift); zero modulation gives
     the plain RMSNorm."""
