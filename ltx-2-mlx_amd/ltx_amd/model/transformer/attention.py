@@ -48,8 +48,20 @@ class Attention:
     def weights(self) -> list[gemm.LinearWeight]:
         return [w for w in (self.proj_q, self.proj_kv, self.to_out) if w is not None]
 
+    def context_kv(self, context: torch.Tensor) -> torch.Tensor:
+        """Keys and values of a cross-attention context without RoPE (the text
+        context): the [Wk; Wv] projection with K normalised in place, returned
+        as the (Tk, 2*inner) buffer that ``core(..., kv=...)`` takes.  Lets a
+        caller compute them on another stream, ahead of the queries."""
+        inner = self.inner_dim
+        kvb = gemm.linear(context, self.proj_kv)
+        k = kvb[:, :inner]
+        qknorm_rope_(k[:0], self.q_norm, None, k, self.k_norm, None, self.heads, self.norm_eps)
+        return kvb
+
     def core(self, x: torch.Tensor, context: torch.Tensor | None = None,
-             pe: tuple | None = None, k_pe: tuple | None = None, passes: int = 1) -> torch.Tensor:
+             pe: tuple | None = None, k_pe: tuple | None = None, passes: int = 1,
+             kv: torch.Tensor | None = None) -> torch.Tensor:
         """Everything up to (not including) ``to_out``; returns (passes*Tq, inner) bf16.
 
         x: (passes*Tq, query_dim) bf16 -- ``passes`` independent sequences of
@@ -58,7 +70,9 @@ class Attention:
         p's keys in rows [p*Tk, (p+1)*Tk).  pe / k_pe: token-major (cos, sin)
         tables of one sequence (or their factored (cos, sin, idx) form), or
         None.  The projections run once over all
-        rows; QK-norm + RoPE and the attention run per sequence.
+        rows; QK-norm + RoPE and the attention run per sequence.  ``kv``:
+        the context's keys and values from :meth:`context_kv` (instead of
+        ``context``; cross-attention without RoPE on the keys).
         """
         inner, heads = self.inner_dim, self.heads
         gate_cols = heads if self.gated else 0
@@ -69,15 +83,18 @@ class Attention:
             k_tab = pe
         else:
             qb = gemm.linear(x, self.proj_q, sigmoid_from=inner)
-            kvb = gemm.linear(context, self.proj_kv)
+            if kv is not None and k_pe is not None:
+                raise ValueError("precomputed keys carry no RoPE")
+            kvb = gemm.linear(context, self.proj_kv) if kv is None else kv
             q = qb[:, :inner]
             g = qb[:, inner:inner + gate_cols] if self.gated else None
             k, v = kvb[:, :inner], kvb[:, inner:]
             k_tab = pe if k_pe is None else k_pe
             if pe is None:
                 k_tab = None
+        k_done = kv is not None  # keys already normalised by context_kv
         if passes == 1:
-            qknorm_rope_(q, self.q_norm, pe, k, self.k_norm, k_tab, heads, self.norm_eps)
+            qknorm_rope_(q, self.q_norm, pe, k[:0] if k_done else k, self.k_norm, k_tab, heads, self.norm_eps)
             return attn_k.flash_attention(q, k, v, heads, gate=g)
         tq, tk = q.shape[0] // passes, k.shape[0] // passes
         if tq * passes != q.shape[0] or tk * passes != k.shape[0]:
@@ -86,7 +103,7 @@ class Attention:
         for p in range(passes):
             qp, kp, vp = q[p * tq:(p + 1) * tq], k[p * tk:(p + 1) * tk], v[p * tk:(p + 1) * tk]
             gp = None if g is None else g[p * tq:(p + 1) * tq]
-            qknorm_rope_(qp, self.q_norm, pe, kp, self.k_norm, k_tab, heads, self.norm_eps)
+            qknorm_rope_(qp, self.q_norm, pe, kp[:0] if k_done else kp, self.k_norm, k_tab, heads, self.norm_eps)
             attn_k.flash_attention(qp, kp, vp, heads, gate=gp, out=out[p * tq:(p + 1) * tq])
         return out
 

@@ -336,7 +336,20 @@ class BasicAVTransformerBlock:
                 side.wait_stream(main)
             a2.record_stream(side)
             ada_a.record_stream(side)
+            if ada_v is not None:
+                ada_v.record_stream(side)
 
+        ev_kv = kv_v = None
+        if run_vx and side is not None:
+            # the text context's keys and values do not depend on the video
+            # rows: computed on the audio stream while the video self-attention
+            # runs, off the video stream's path
+            with on_audio():
+                c, cp = ctx_rows(video, 0, npass)
+                c = adaln(c, ada_v[ROW_SCALE_KV], ada_v[ROW_SHIFT_KV], eps, _lib.ADALN_NO_NORM)
+                kv_v = (self.attn2.context_kv(c), cp)
+                ev_kv = side.record_event()
+            kv_v[0].record_stream(main)
         if run_vx:
             pe = _tables(video.positional_embeddings)
             rng = runs(keep("skip_video_self_attn"))
@@ -355,13 +368,22 @@ class BasicAVTransformerBlock:
                 v_owned = True
             mark("video self-attn")
             a = adaln(v2, ada_v[ROW_SCALE_Q], ada_v[ROW_SHIFT_Q], eps, rn)
-            c, cp = ctx_rows(video, 0, npass)
-            c = adaln(c, ada_v[ROW_SCALE_KV], ada_v[ROW_SHIFT_KV], eps, _lib.ADALN_NO_NORM)
-            if cp == npass:
-                o = self.attn2.core(a, c, passes=npass)
+            if kv_v is not None:
+                main.wait_event(ev_kv)
+                kv, cp = kv_v
+                if cp == npass:
+                    o = self.attn2.core(a, kv=kv, passes=npass)
+                else:
+                    o = torch.cat([self.attn2.core(a[p * tv:(p + 1) * tv], kv=kv) for p in range(npass)], 0) \
+                        if npass > 1 else self.attn2.core(a, kv=kv)
             else:
-                o = torch.cat([self.attn2.core(a[p * tv:(p + 1) * tv], c) for p in range(npass)], 0) \
-                    if npass > 1 else self.attn2.core(a, c)
+                c, cp = ctx_rows(video, 0, npass)
+                c = adaln(c, ada_v[ROW_SCALE_KV], ada_v[ROW_SHIFT_KV], eps, _lib.ADALN_NO_NORM)
+                if cp == npass:
+                    o = self.attn2.core(a, c, passes=npass)
+                else:
+                    o = torch.cat([self.attn2.core(a[p * tv:(p + 1) * tv], c) for p in range(npass)], 0) \
+                        if npass > 1 else self.attn2.core(a, c)
             v2 = residual_gemm(o, self.attn2.to_out, v2, v_owned, ada_v[ROW_GATE_Q], gemm.EPI_RESIDUAL_ROUND)
             v_owned = True
             mark("video text-attn")
