@@ -48,15 +48,19 @@ class Attention:
     def weights(self) -> list[gemm.LinearWeight]:
         return [w for w in (self.proj_q, self.proj_kv, self.to_out) if w is not None]
 
-    def context_kv(self, context: torch.Tensor) -> torch.Tensor:
-        """Keys and values of a cross-attention context without RoPE (the text
-        context): the [Wk; Wv] projection with K normalised in place, returned
-        as the (Tk, 2*inner) buffer that ``core(..., kv=...)`` takes.  Lets a
-        caller compute them on another stream, ahead of the queries."""
+    def context_kv(self, context: torch.Tensor, k_pe: tuple | None = None, passes: int = 1) -> torch.Tensor:
+        """Keys and values of a cross-attention context: the [Wk; Wv]
+        projection with K normalised (and rotated by ``k_pe``, the table of one
+        sequence) in place, returned as the (passes*Tk, 2*inner) buffer that
+        ``core(..., kv=...)`` takes.  Lets a caller compute them on another
+        stream, ahead of the queries."""
         inner = self.inner_dim
         kvb = gemm.linear(context, self.proj_kv)
         k = kvb[:, :inner]
-        qknorm_rope_(k[:0], self.q_norm, None, k, self.k_norm, None, self.heads, self.norm_eps)
+        tk = k.shape[0] // passes
+        for p in range(passes):
+            kp = k[p * tk:(p + 1) * tk]
+            qknorm_rope_(kp[:0], self.q_norm, None, kp, self.k_norm, k_pe, self.heads, self.norm_eps)
         return kvb
 
     def core(self, x: torch.Tensor, context: torch.Tensor | None = None,
@@ -72,7 +76,7 @@ class Attention:
         None.  The projections run once over all
         rows; QK-norm + RoPE and the attention run per sequence.  ``kv``:
         the context's keys and values from :meth:`context_kv` (instead of
-        ``context``; cross-attention without RoPE on the keys).
+        ``context``; its keys are already normalised and rotated).
         """
         inner, heads = self.inner_dim, self.heads
         gate_cols = heads if self.gated else 0
@@ -83,8 +87,6 @@ class Attention:
             k_tab = pe
         else:
             qb = gemm.linear(x, self.proj_q, sigmoid_from=inner)
-            if kv is not None and k_pe is not None:
-                raise ValueError("precomputed keys carry no RoPE")
             kvb = gemm.linear(context, self.proj_kv) if kv is None else kv
             q = qb[:, :inner]
             g = qb[:, inner:inner + gate_cols] if self.gated else None

@@ -427,16 +427,25 @@ class BasicAVTransformerBlock:
             vs_a2v, vs_v2a = adaln2(v2, ada_v[ROW_SCALE_A2V], ada_v[ROW_SHIFT_A2V], ada_v[ROW_SCALE_V2A],
                                     ada_v[ROW_SHIFT_V2A], eps, rn)
             ev_v = main.record_event() if side is not None else None
+            rng = runs(keep("skip_a2v_cross_attn")) if run_a2v else []
+            kv_a2v = None
             with on_audio():
                 as_a2v, as_v2a = adaln2(a2, ada_a[ROW_SCALE_A2V], ada_a[ROW_SHIFT_A2V], ada_a[ROW_SCALE_V2A],
                                         ada_a[ROW_SHIFT_V2A], eps, rn)
+                if side is not None and rng == [(0, npass)]:
+                    # A2V keys / values from the audio rows, on the audio stream
+                    kv_a2v = self.audio_to_video_attn.context_kv(as_a2v, k_pe=ape, passes=npass)
             if side is not None:
                 main.wait_event(side.record_event())
                 as_a2v.record_stream(main)
                 vs_v2a.record_stream(side)
-            rng = runs(keep("skip_a2v_cross_attn")) if run_a2v else []
+                if kv_a2v is not None:
+                    kv_a2v.record_stream(main)
             if rng == [(0, npass)]:
-                o = self.audio_to_video_attn.core(vs_a2v, as_a2v, pe=vpe, k_pe=ape, passes=npass)
+                if kv_a2v is not None:
+                    o = self.audio_to_video_attn.core(vs_a2v, pe=vpe, passes=npass, kv=kv_a2v)
+                else:
+                    o = self.audio_to_video_attn.core(vs_a2v, as_a2v, pe=vpe, k_pe=ape, passes=npass)
                 v2 = residual_gemm(o, self.audio_to_video_attn.to_out, v2, v_owned, ada_v[ROW_GATE_AV],
                                    gemm.EPI_RESIDUAL)
                 v_owned = True
