@@ -421,19 +421,25 @@ __global__ void timestep_embedding_kernel(const float* values, int64_t count, fl
   out[idx] = c < half ? cosf(arg) : sinf(arg);
 }
 
-// GEMV: each wave computes ROWS_PER_WAVE outputs for every batch entry;
-// x is staged in LDS once per workgroup.
-constexpr int kGemvRowsPerWave = 4;
+// GEMV: each wave computes kGemvRowsPerWave outputs for every batch entry;
+// x is staged in LDS once per workgroup (batch * K floats of dynamic LDS, so
+// small batches leave room for many workgroups per CU).  A wave first issues
+// every weight load of its rows (KIT 16-byte loads per lane and row, K <=
+// 512 * KIT), then accumulates them in k order: one round trip to memory per
+// wave instead of one per 512 columns.  Lane l accumulates columns l*8 + i +
+// 512 j in the order j, i; the wave sum closes the row.
+constexpr int kGemvRowsPerWave = 2;
 constexpr int kGemvMaxK = 4096;
 constexpr int kGemvMaxBatch = 4;
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 
+template <int KIT>
 __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, int batch,
                                                    int K, const bf16* __restrict__ W,
                                                    const float* __restrict__ bias,
                                                    float* __restrict__ y, int64_t N, int flags) {
-  __shared__ float xs[kGemvMaxBatch * kGemvMaxK];
+  extern __shared__ float xs[];  // batch * K
   for (int i = threadIdx.x; i < batch * K; i += blockDim.x) {
     float v = x[i];
     if (flags & LTX_GEMV_SILU_INPUT) v = silu(v);
@@ -443,18 +449,30 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t wave = (int64_t)blockIdx.x * (blockDim.x / kWave) + (threadIdx.x >> 6);
   const int64_t n0 = wave * kGemvRowsPerWave;
+  bf16x8 wv[kGemvRowsPerWave][KIT];
+#pragma unroll
+  for (int rr = 0; rr < kGemvRowsPerWave; ++rr) {
+    const int64_t n = n0 + rr < N ? n0 + rr : N - 1;
+#pragma unroll
+    for (int j = 0; j < KIT; ++j) {
+      const int k0 = lane * 8 + j * kWave * 8;
+      if (k0 < K) wv[rr][j] = *reinterpret_cast<const bf16x8*>(W + n * (int64_t)K + k0);
+    }
+  }
+#pragma unroll
   for (int rr = 0; rr < kGemvRowsPerWave; ++rr) {
     const int64_t n = n0 + rr;
     if (n >= N) break;
     float acc[kGemvMaxBatch] = {0.f, 0.f, 0.f, 0.f};
-    const bf16* wr = W + n * (int64_t)K;
-    for (int k0 = lane * 8; k0 < K; k0 += kWave * 8) {
-      float wv[8];
-      load8(wr + k0, wv);
-      for (int b = 0; b < batch; ++b) {
-        const float* xb = xs + b * K + k0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[b] = fmaf(wv[i], xb[i], acc[b]);
+    for (int j = 0; j < KIT; ++j) {
+      const int k0 = lane * 8 + j * kWave * 8;
+      if (k0 < K) {
+        for (int b = 0; b < batch; ++b) {
+          const float* xb = xs + b * K + k0;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[b] = fmaf((float)wv[rr][j][i], xb[i], acc[b]);
+        }
       }
     }
     for (int b = 0; b < batch; ++b) {
@@ -722,8 +740,18 @@ extern "C" int ltx_gemv_f32_bf16w(const float* x, int64_t batch, int64_t K, cons
   if (batch == 0 || N == 0) return LTX_OK;
   const int64_t waves = (N + kGemvRowsPerWave - 1) / kGemvRowsPerWave;
   const int64_t blocks = (waves + 3) / 4;
-  gemv_kernel<<<(int)blocks, 256, 0, (hipStream_t)stream>>>(x, (int)batch, (int)K,
-                                                            (const bf16*)W, bias, y, N, flags);
+  if (blocks > INT32_MAX) return LTX_ERR_UNSUPPORTED;
+  const size_t lds = (size_t)batch * K * sizeof(float);
+  hipStream_t s = (hipStream_t)stream;
+  const bf16* w = (const bf16*)W;
+  if (K <= 512)
+    gemv_kernel<1><<<(int)blocks, 256, lds, s>>>(x, (int)batch, (int)K, w, bias, y, N, flags);
+  else if (K <= 1024)
+    gemv_kernel<2><<<(int)blocks, 256, lds, s>>>(x, (int)batch, (int)K, w, bias, y, N, flags);
+  else if (K <= 2048)
+    gemv_kernel<4><<<(int)blocks, 256, lds, s>>>(x, (int)batch, (int)K, w, bias, y, N, flags);
+  else
+    gemv_kernel<8><<<(int)blocks, 256, lds, s>>>(x, (int)batch, (int)K, w, bias, y, N, flags);
   return ltx_launch_status();
 }
 
