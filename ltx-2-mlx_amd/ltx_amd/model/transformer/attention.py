@@ -65,7 +65,7 @@ class Attention:
 
     def core(self, x: torch.Tensor, context: torch.Tensor | None = None,
              pe: tuple | None = None, k_pe: tuple | None = None, passes: int = 1,
-             kv: torch.Tensor | None = None) -> torch.Tensor:
+             kv: torch.Tensor | None = None, kv_ready=None) -> torch.Tensor:
         """Everything up to (not including) ``to_out``; returns (passes*Tq, inner) bf16.
 
         x: (passes*Tq, query_dim) bf16 -- ``passes`` independent sequences of
@@ -76,7 +76,9 @@ class Attention:
         None.  The projections run once over all
         rows; QK-norm + RoPE and the attention run per sequence.  ``kv``:
         the context's keys and values from :meth:`context_kv` (instead of
-        ``context``; its keys are already normalised and rotated).
+        ``context``; its keys are already normalised and rotated);
+        ``kv_ready``: an event the current stream waits for before the first
+        read of ``kv`` (after the query projection and norm).
         """
         inner, heads = self.inner_dim, self.heads
         gate_cols = heads if self.gated else 0
@@ -97,11 +99,15 @@ class Attention:
         k_done = kv is not None  # keys already normalised by context_kv
         if passes == 1:
             qknorm_rope_(q, self.q_norm, pe, k[:0] if k_done else k, self.k_norm, k_tab, heads, self.norm_eps)
+            if kv_ready is not None:
+                torch.cuda.current_stream().wait_event(kv_ready)
             return attn_k.flash_attention(q, k, v, heads, gate=g)
         tq, tk = q.shape[0] // passes, k.shape[0] // passes
         if tq * passes != q.shape[0] or tk * passes != k.shape[0]:
             raise ValueError(f"{q.shape[0]} query / {k.shape[0]} key rows do not split into {passes} passes")
         out = torch.empty((q.shape[0], inner), dtype=torch.bfloat16, device=q.device)
+        if kv_ready is not None:
+            torch.cuda.current_stream().wait_event(kv_ready)
         for p in range(passes):
             qp, kp, vp = q[p * tq:(p + 1) * tq], k[p * tk:(p + 1) * tk], v[p * tk:(p + 1) * tk]
             gp = None if g is None else g[p * tq:(p + 1) * tq]

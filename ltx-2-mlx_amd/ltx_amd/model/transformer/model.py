@@ -17,8 +17,6 @@ the distilled text-to-video+audio path:
 
 from __future__ import annotations
 
-import contextlib
-
 import hashlib
 from dataclasses import dataclass
 
@@ -231,34 +229,29 @@ class LTXModel:
         def stacked(x):  # (T, C) -> (passes, T, C)
             return x if passes == 1 else x.unsqueeze(0).expand(passes, *x.shape).contiguous()
 
-        # the audio stream's work overlaps the video stream's on a second HIP
-        # stream: forked here (its preprocessing -- patchify, timestep MLPs,
-        # modulation rows -- runs beside the video's), joined before the heads
-        side = None
-        if run_audio and self.concurrent_audio:
-            if self._audio_stream is None:
-                self._audio_stream = torch.cuda.Stream(device=video_latent.device)  # default priority
-            side = self._audio_stream
-            side.wait_stream(torch.cuda.current_stream())
-
         # preprocess
         vx = stacked(gemm.linear(video_latent, self.patchify_proj))
         self._timestep_rows(sigma_dev, sigma_dev, video=True)
+        stream = _lib.stream_of(vx)
         _lib.call("ltx_broadcast_add_f32", self.video_tables.data_ptr(), self._temb_v.data_ptr(),
-                  self._ada_v.data_ptr(), self.num_layers, ADA_ROWS * self.video_dim, _lib.stream_of(vx))
+                  self._ada_v.data_ptr(), self.num_layers, ADA_ROWS * self.video_dim, stream)
         video = TransformerArgs(x=vx, context=video_context, timesteps=self._temb_v[:9], positional_embeddings=vpe,
                                 cross_positional_embeddings=vxpe)
         audio = None
         if run_audio:
-            with torch.cuda.stream(side) if side is not None else contextlib.nullcontext():
-                ax = stacked(gemm.linear(audio_latent, self.audio_patchify_proj))
-                self._timestep_rows(sigma_dev, sigma_dev, video=False)
-                _lib.call("ltx_broadcast_add_f32", self.audio_tables.data_ptr(), self._temb_a.data_ptr(),
-                          self._ada_a.data_ptr(), self.num_layers, ADA_ROWS * self.audio_dim, _lib.stream_of(ax))
+            ax = stacked(gemm.linear(audio_latent, self.audio_patchify_proj))
+            self._timestep_rows(sigma_dev, sigma_dev, video=False)
+            _lib.call("ltx_broadcast_add_f32", self.audio_tables.data_ptr(), self._temb_a.data_ptr(),
+                      self._ada_a.data_ptr(), self.num_layers, ADA_ROWS * self.audio_dim, stream)
             audio = TransformerArgs(x=ax, context=audio_context, timesteps=self._temb_a[:9],
                                     positional_embeddings=ape, cross_positional_embeddings=axpe)
-        # blocks (block 0's audio work also waits for the video preprocessing:
-        # the audio stream computes the video text context's keys)
+        # blocks; the audio stream's work overlaps the video stream's on a
+        # second HIP stream (forked once here, joined before the heads)
+        side = None
+        if run_audio and self.concurrent_audio:
+            if self._audio_stream is None:
+                self._audio_stream = torch.cuda.Stream(device=vx.device)  # default priority
+            side = self._audio_stream
         for i, block in enumerate(self.transformer_blocks):
             block.ada_rows_video = self._ada_v[i]
             block.ada_rows_audio = self._ada_a[i] if run_audio else None

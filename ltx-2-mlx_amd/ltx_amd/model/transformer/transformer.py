@@ -369,13 +369,13 @@ class BasicAVTransformerBlock:
             mark("video self-attn")
             a = adaln(v2, ada_v[ROW_SCALE_Q], ada_v[ROW_SHIFT_Q], eps, rn)
             if kv_v is not None:
-                main.wait_event(ev_kv)
                 kv, cp = kv_v
                 if cp == npass:
-                    o = self.attn2.core(a, kv=kv, passes=npass)
+                    o = self.attn2.core(a, kv=kv, passes=npass, kv_ready=ev_kv)
                 else:
-                    o = torch.cat([self.attn2.core(a[p * tv:(p + 1) * tv], kv=kv) for p in range(npass)], 0) \
-                        if npass > 1 else self.attn2.core(a, kv=kv)
+                    o = torch.cat([self.attn2.core(a[p * tv:(p + 1) * tv], kv=kv, kv_ready=ev_kv)
+                                   for p in range(npass)], 0) if npass > 1 else \
+                        self.attn2.core(a, kv=kv, kv_ready=ev_kv)
             else:
                 c, cp = ctx_rows(video, 0, npass)
                 c = adaln(c, ada_v[ROW_SCALE_KV], ada_v[ROW_SHIFT_KV], eps, _lib.ADALN_NO_NORM)
@@ -435,15 +435,18 @@ class BasicAVTransformerBlock:
                 if side is not None and rng == [(0, npass)]:
                     # A2V keys / values from the audio rows, on the audio stream
                     kv_a2v = self.audio_to_video_attn.context_kv(as_a2v, k_pe=ape, passes=npass)
+            ev_a = None
             if side is not None:
-                main.wait_event(side.record_event())
-                as_a2v.record_stream(main)
+                ev_a = side.record_event()
                 vs_v2a.record_stream(side)
                 if kv_a2v is not None:
                     kv_a2v.record_stream(main)
+                else:
+                    main.wait_event(ev_a)
+                    as_a2v.record_stream(main)
             if rng == [(0, npass)]:
                 if kv_a2v is not None:
-                    o = self.audio_to_video_attn.core(vs_a2v, pe=vpe, passes=npass, kv=kv_a2v)
+                    o = self.audio_to_video_attn.core(vs_a2v, pe=vpe, passes=npass, kv=kv_a2v, kv_ready=ev_a)
                 else:
                     o = self.audio_to_video_attn.core(vs_a2v, as_a2v, pe=vpe, k_pe=ape, passes=npass)
                 v2 = residual_gemm(o, self.audio_to_video_attn.to_out, v2, v_owned, ada_v[ROW_GATE_AV],
