@@ -252,11 +252,15 @@ class LTXModel:
             if self._audio_stream is None:
                 self._audio_stream = torch.cuda.Stream(device=vx.device)  # default priority
             side = self._audio_stream
-        for i, block in enumerate(self.transformer_blocks):
+        blocks = self.transformer_blocks
+        for i, block in enumerate(blocks):
             block.ada_rows_video = self._ada_v[i]
             block.ada_rows_audio = self._ada_a[i] if run_audio else None
             block.audio_stream = side
             block.audio_fork = i == 0
+            block.next_block = blocks[i + 1] if side is not None and i + 1 < len(blocks) else None
+            block._prefetched_kv = None
+        for block in blocks:
             video, audio = block(video, audio, perturbations=perturbations, profile_events=profile_events)
         if side is not None:
             torch.cuda.current_stream().wait_stream(side)

@@ -173,6 +173,11 @@ class BasicAVTransformerBlock:
         self.ada_rows_audio: torch.Tensor | None = None
         self.audio_stream: torch.cuda.Stream | None = None
         self.audio_fork = True  # the audio stream waits for the caller's stream first
+        # The next block of the same forward (set by the scheduler): its text
+        # keys / values are computed on the audio stream during this block,
+        # ahead of this block's A2V event, so that event also covers them.
+        self.next_block: "BasicAVTransformerBlock | None" = None
+        self._prefetched_kv: tuple | None = None
         self._adaln_flags = 0 if _FUSED_ADALN_ENABLED else _lib.ADALN_ROUND_NORM
 
     # -- parameters ---------------------------------------------------------
@@ -331,30 +336,63 @@ class BasicAVTransformerBlock:
         def on_audio():
             return torch.cuda.stream(side) if side is not None else contextlib.nullcontext()
 
+        # The audio stream's first kernel of a forked block must depend on the
+        # caller's stream as it is now, but be issued only after the video
+        # stream's first kernel: a HIP graph replay keeps the first-issued
+        # child of a fork on the parent's queue and moves the others to
+        # queues it shares with later branches, where the video kernels would
+        # wait behind audio work.
+        ev_fork = main.record_event() if side is not None and self.audio_fork else None
+
+        def fork_side():
+            nonlocal ev_fork
+            if ev_fork is not None:
+                side.wait_event(ev_fork)
+                ev_fork = None
+
         if side is not None:
-            if self.audio_fork:  # audio input and modulation rows come from the caller's stream
-                side.wait_stream(main)
             a2.record_stream(side)
             ada_a.record_stream(side)
             if ada_v is not None:
                 ada_v.record_stream(side)
 
         ev_kv = kv_v = None
-        if run_vx and side is not None:
+        prefetched, self._prefetched_kv = self._prefetched_kv, None
+
+        def context_kv_on_side():
             # the text context's keys and values do not depend on the video
             # rows: computed on the audio stream while the video self-attention
-            # runs, off the video stream's path
+            # runs, off the video stream's path.  The previous block of the
+            # forward computed this block's before its A2V event, which the
+            # video stream has waited for already; otherwise they are made
+            # here and joined by their own event.  The next block's are made
+            # right after, ahead of this block's A2V event.
+            nonlocal ev_kv, kv_v
             with on_audio():
+                fork_side()
                 c, cp = ctx_rows(video, 0, npass)
-                c = adaln(c, ada_v[ROW_SCALE_KV], ada_v[ROW_SHIFT_KV], eps, _lib.ADALN_NO_NORM)
-                kv_v = (self.attn2.context_kv(c), cp)
-                ev_kv = side.record_event()
-            kv_v[0].record_stream(main)
+                if prefetched is not None:
+                    kv_v = prefetched
+                else:
+                    cm = adaln(c, ada_v[ROW_SCALE_KV], ada_v[ROW_SHIFT_KV], eps, _lib.ADALN_NO_NORM)
+                    kv_v = (self.attn2.context_kv(cm), cp)
+                    ev_kv = side.record_event()
+                    kv_v[0].record_stream(main)
+                nb = self.next_block
+                if nb is not None and nb.attn2 is not None and nb.ada_rows_video is not None and \
+                        (run_a2v or run_v2a):
+                    ada_n = nb.ada_rows_video
+                    cm = adaln(c, ada_n[ROW_SCALE_KV], ada_n[ROW_SHIFT_KV], eps, _lib.ADALN_NO_NORM)
+                    nb._prefetched_kv = (nb.attn2.context_kv(cm), cp)
+                    nb._prefetched_kv[0].record_stream(main)
+
         if run_vx:
             pe = _tables(video.positional_embeddings)
             rng = runs(keep("skip_video_self_attn"))
             if rng == [(0, npass)]:
                 h = adaln(v2, ada_v[ROW_SCALE_MSA], ada_v[ROW_SHIFT_MSA], eps, flags)
+                if side is not None:
+                    context_kv_on_side()
                 o = self.attn1.core(h, pe=pe, passes=npass)
                 v2 = residual_gemm(o, self.attn1.to_out, v2, v_owned, ada_v[ROW_GATE_MSA], gemm.EPI_RESIDUAL)
                 v_owned = True
@@ -367,6 +405,8 @@ class BasicAVTransformerBlock:
                 v2 = partial_residual(v2, v_owned, tv, rng, video_self)
                 v_owned = True
             mark("video self-attn")
+            if side is not None and kv_v is None:
+                context_kv_on_side()
             a = adaln(v2, ada_v[ROW_SCALE_Q], ada_v[ROW_SHIFT_Q], eps, rn)
             if kv_v is not None:
                 kv, cp = kv_v
@@ -390,6 +430,7 @@ class BasicAVTransformerBlock:
 
         if run_ax:
             with on_audio():
+                fork_side()
                 pe = _tables(audio.positional_embeddings)
                 rng = runs(keep("skip_audio_self_attn"))
                 if rng == [(0, npass)]:
