@@ -777,7 +777,12 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
 // stage apart: while one group issues its memory cluster (LDS fragment reads
 // of a stage, its share of the direct global->LDS loads two stages ahead, the
 // scale loads), the other group's compute cluster (the stage's 32 MFMAs with
-// the weight dequantisation interleaved) keeps the SIMD's matrix pipe busy.
+// the weight dequantisation of fragments 2-7 interleaved) keeps the SIMD's
+// matrix pipe busy.  The memory cluster ends, once its fragment reads have
+// landed, by decoding the stage's E8M0 scales and dequantising fragments 0
+// and 1, so the compute cluster's first MFMAs issue right after the barrier
+// (FF up 402 -> 382 us: the dependent decode -> convert chain had left the
+// matrix pipe idle at the start of every compute cluster).
 // A workgroup barrier separates the clusters.  Both operands reach LDS by
 // global_load_lds (no staging registers, no LDS write instructions): three
 // 48 KB stages of bf16 activations (256 x 128 B) and raw weight codes
@@ -875,7 +880,9 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   // a wave whose 128 x 64 sub-tile lies wholly past M or N (the last row or
   // column of tiles) reads no fragments and issues no MFMAs: it still moves
   // its share of every stage and meets every barrier
-  const bool live = m0 + wm * WM < p.M && n0 + wn * WN < p.N;
+  // (an int from a scalar register: a bool kept across the loop becomes a lane
+  // mask whose tests cost vector instructions in every cluster)
+  const int live = __builtin_amdgcn_readfirstlane((m0 + wm * WM < p.M && n0 + wn * WN < p.N) ? 1 : 0);
 
   float* col_lds = reinterpret_cast<float*>(lds + Cfg::LDS_BYTES);
 
@@ -910,7 +917,7 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
     const int chunk = (lane & 3) ^ ((r >> 2) & 3);
     b_src[d] = (uint32_t)((int64_t)gn * p.ldb) + chunk * 16;
   }
-  auto dma_stage = [&](int kt, int buf) {
+  auto dma_stage = [&](int kt, int buf) __attribute__((always_inline)) {
     char* As = lds + buf * A_BYTES;
     char* Bs = lds + B_REGION + buf * B_BYTES;
 #pragma unroll
@@ -980,7 +987,7 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   bf16x8 fa[4][TM];  // A fragments of the stage's four k-steps
   u32x4 fb[2][TN];   // weight codes of the stage's two k-step pairs (16 per lane)
   // fragment reads of stage kt, which sits in buffer BUF (compile-time)
-  auto read_stage = [&](int kt, auto bufc) {
+  auto read_stage = [&](int kt, auto bufc) __attribute__((always_inline)) {
     constexpr int BUF = decltype(bufc)::value;
     if constexpr (BKIND == B_MXFP8) {
       const int sa = sc_read + ((kt >> 3) & 1) * Cfg::SC_OCT + ((kt & 7) >> 1) * 4;
@@ -1038,32 +1045,39 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
     return __builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]});
   };
 
-  // compute cluster of stage kt: 4 k-steps x TN weight fragments x TM MFMAs.
-  // Fragment f+1 is dequantised while the MFMAs of fragment f run (two
-  // register sets, alternating).  The scale decodes of the stage's second
-  // pair ride along with its first pair.
-  auto compute_stage = [&](int kt) {
-    float scf[2][TN];
-    auto decode = [&](int pp, int j) {
-      if constexpr (BKIND == B_MXFP8)
-        scf[pp][j] = e8m0_to_f32_valu(__builtin_amdgcn_ubfe(scw[j], 16 * (kt & 1) + 8 * pp, 8));
-      else
-        scf[pp][j] = s_i8[j];
-    };
-    constexpr int NF = 4 * TN;
-    auto frag_dequant = [&](int f) -> bf16x8 {
-      const int kk = f / TN, j = f % TN, pp = kk >> 1, s = kk & 1;
-      return dequant(fb[pp][j][2 * s], fb[pp][j][2 * s + 1], scf[pp][j]);
-    };
+  // Weight fragment f of a stage (k-step f / TN, column block f % TN) in two
+  // alternating register sets; the E8M0 scales of the stage's two k-step
+  // pairs decoded once per stage.
+  float scf[2][TN];
+  bf16x8 bq[2];
+  constexpr int NF = 4 * TN;
+  auto decode = [&](int kt, int pp, int j) {
+    if constexpr (BKIND == B_MXFP8)
+      scf[pp][j] = e8m0_to_f32_valu(__builtin_amdgcn_ubfe(scw[j], 16 * (kt & 1) + 8 * pp, 8));
+    else
+      scf[pp][j] = s_i8[j];
+  };
+  auto frag_dequant = [&](int f) -> bf16x8 {
+    const int kk = f / TN, j = f % TN, pp = kk >> 1, s = kk & 1;
+    return dequant(fb[pp][j][2 * s], fb[pp][j][2 * s + 1], scf[pp][j]);
+  };
+  // end of the memory cluster of stage kt (its fragment reads have landed):
+  // the stage's scales and fragments 0 and 1
+  auto prep_stage = [&](int kt) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < TN; ++j) decode(0, j);
-    bf16x8 bq[2];
+    for (int j = 0; j < TN; ++j) decode(kt, 0, j);
     bq[0] = frag_dequant(0);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) decode(kt, 1, j);
+    bq[1] = frag_dequant(1);
+  };
+  // compute cluster of stage kt: 4 k-steps x TN weight fragments x TM MFMAs.
+  // Fragment f+1 (f >= 1) is dequantised while the MFMAs of fragment f run.
+  auto compute_stage = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
       const int kk = f / TN, j = f % TN;
-      if (f < TN) decode(1, f);  // the second pair's scales, early
-      if (f + 1 < NF) bq[(f + 1) & 1] = frag_dequant(f + 1);
+      if (f >= 1 && f + 1 < NF) bq[(f + 1) & 1] = frag_dequant(f + 1);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bq[f & 1], fa[kk][i], acc[i][j], 0, 0, 0);
@@ -1090,21 +1104,25 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   // so every stage issues the same loads and the waits are exact.  The scales
   // of octet o+1 go out (group 0) with stage 8o's loads.
   // SUB = kt % 8 (compile-time in the unrolled loop).
-  auto stage_iter = [&](int kt, auto bufc) {
+  // The loop is compiled once per group (GRP), so the group-specific waits
+  // and scale loads are resolved at compile time.
+  auto stage_iter = [&](int kt, auto bufc, auto grpc) __attribute__((always_inline)) {
     constexpr int BUF = decltype(bufc)::value;
+    constexpr int GRP = decltype(grpc)::value;
     const bool oct_start = BKIND == B_MXFP8 && (kt & 7) == 0;
     // memory cluster
-    if (oct_start) dma_scales((kt >> 3) + 1);
+    if (GRP == 0 && oct_start) dma_scales((kt >> 3) + 1);
     dma_stage(kt + 2 < KT ? kt + 2 : KT - 1, (BUF + 2) % kG8Stages);
     if (live) read_stage(kt, bufc);
     wait_lgkmcnt0();
-    if (grp == 1) wait_vmcnt<VM_DMA>();
+    if (live) prep_stage(kt);
+    if (GRP == 1) wait_vmcnt<VM_DMA>();
     barrier_nofence();
     // compute cluster
     __builtin_amdgcn_s_setprio(1);
-    if (live) compute_stage(kt);
+    if (live) compute_stage();
     __builtin_amdgcn_s_setprio(0);
-    if (grp == 0) {
+    if (GRP == 0) {
       if (oct_start) wait_vmcnt<VM_DMA + VM_SCALES>();
       else wait_vmcnt<VM_DMA>();
     }
@@ -1113,14 +1131,18 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   typedef std::integral_constant<int, 0> B0;
   typedef std::integral_constant<int, 1> B1;
   typedef std::integral_constant<int, 2> B2;
-  int kt = 0;
-  for (; kt + 2 < KT; kt += 3) {
-    stage_iter(kt, B0{});
-    stage_iter(kt + 1, B1{});
-    stage_iter(kt + 2, B2{});
-  }
-  if (kt < KT) stage_iter(kt, B0{});
-  if (kt + 1 < KT) stage_iter(kt + 1, B1{});
+  auto main_loop = [&](auto grpc) __attribute__((always_inline)) {
+    int kt = 0;
+    for (; kt + 2 < KT; kt += 3) {
+      stage_iter(kt, B0{}, grpc);
+      stage_iter(kt + 1, B1{}, grpc);
+      stage_iter(kt + 2, B2{}, grpc);
+    }
+    if (kt < KT) stage_iter(kt, B0{}, grpc);
+    if (kt + 1 < KT) stage_iter(kt + 1, B1{}, grpc);
+  };
+  if (grp == 0) main_loop(std::integral_constant<int, 0>{});
+  else main_loop(std::integral_constant<int, 1>{});
   if (grp == 0) barrier_nofence();
   wait_vmcnt<0>();
 
