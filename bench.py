@@ -12,16 +12,21 @@ X0/Euler update.  Inputs are resident before timing starts.
 Prints ONE JSON line.  Besides ms/step and tokens/s it carries:
   roofline      the dominant kernel (video FF up-projection GEMM, M=3456,
                 K=4096, N=16384, GELU epilogue): algorithmic flops per launch /
-                its average launch time from stream events around every such
-                launch in eager steps run right after the timed region (the
-                timed region replays HIP graphs, which take no events);
+                its average launch time inside the timed replays of the
+                step graphs, from device clock stamps (ltx_device_clock_stamp)
+                captured right before and after every such launch on its
+                stream (HIP events cannot be recorded inside graphs on ROCm;
+                the timed graphs carry these 96 tiny stamp kernels per step);
                 ``traffic`` = HBM bytes per launch from the rocprofv3
                 FETCH_SIZE / WRITE_SIZE summary committed in profiles/ for
                 this kernel and weight format (null when none matches);
-  gemm_step     every GEMM launch of those eager steps timed the same way,
-                per stream: flops / summed launch time (the audio stream's
+  gemm_step     every GEMM launch of eager steps (queued behind graph
+                replays) timed with stream events around the launch, per
+                stream: flops / summed launch time (the audio stream's
                 launches overlap the video stream's, so their times include
-                sharing the chip); ff_up_mfma_pct is the roofline kernel alone;
+                sharing the chip; the host needs longer than the device to
+                enqueue an eager step, so these include host gaps);
+                ff_up_mfma_pct is the roofline kernel alone;
   gemm_shapes   the block's projection shapes at M=3456 (Q/K/V/out 4096x4096
                 x4, FF up 4096->16384, FF down 16384->4096) in int8 W8A16 and
                 MXFP8, each launch replayed from a HIP graph: ms, TFLOP/s and
@@ -293,10 +298,13 @@ def cpu_baseline(tv: int, ta: int, s: int, layers: int, grid, runs: int = 5):
                       f"MLX CPU backend is not installable here"}
 
 
-def gemm_step_profile(run_step, steps, tv, torch):
+def gemm_step_profile(run_step, steps, tv, torch, prefill=None):
     """Time every GEMM launch of ``steps`` eager steps with events recorded on
-    its own stream around the launch.  Returns (FF-up launch durations in ms,
-    per-stream summary)."""
+    its own stream around the launch.  ``prefill`` (graph replays of the step)
+    is queued first, so the device is still busy while the host enqueues the
+    eager steps: the events then bracket back-to-back kernels, as in the
+    replays, rather than gaps left by the host.  Returns (FF-up launch
+    durations in ms, per-stream summary, host enqueue ms per eager step)."""
     from ltx_amd.kernels import gemm
 
     recs = []
@@ -310,10 +318,15 @@ def gemm_step_profile(run_step, steps, tv, torch):
         else:
             recs[-1][3] = e
 
+    torch.cuda.synchronize()
+    if prefill is not None:
+        prefill()
     gemm.LAUNCH_HOOK = hook
     try:
+        t0 = time.perf_counter()
         for i in range(steps):
             run_step(i)
+        host_ms = (time.perf_counter() - t0) / steps * 1e3
         torch.cuda.synchronize()
     finally:
         gemm.LAUNCH_HOOK = None
@@ -337,7 +350,84 @@ def gemm_step_profile(run_step, steps, tv, torch):
     summary["all"] = {"gflop_per_step": round(tot[1] / steps / 1e9, 1), "ms_per_step": round(tot[2] / steps, 3),
                       "tflops": round(tot[1] / (tot[2] * 1e-3) / 1e12, 1),
                       "frac_bf16_peak": round(tot[1] / (tot[2] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
-    return ff_up, summary
+    return ff_up, summary, host_ms
+
+
+class LaunchStamps:
+    """Device clock stamps around chosen GEMM launches inside captured HIP
+    graphs.  While ``capturing(k)`` is active, every launch chosen by
+    ``select(info)`` gets a stamp kernel (ltx_device_clock_stamp) right before
+    and right after it on its stream, writing into slot range k; each replay
+    of that graph overwrites the range, so after the timed replays it holds
+    the last replay of every graph.  The counter's rate comes from two stamps
+    around a host sleep."""
+
+    CAP = 128  # stamped launches per graph
+
+    def __init__(self, torch, graphs: int, select):
+        self.torch, self.select = torch, select
+        self.slots = torch.zeros((graphs, 2 * self.CAP), dtype=torch.int64, device="cuda")
+        self.count = [0] * graphs
+        self.k, self.on = None, False
+
+    def _stamp(self, addr):
+        from ltx_amd import _lib
+
+        _lib.call("ltx_device_clock_stamp", addr, self.torch.cuda.current_stream().cuda_stream)
+
+    def hook(self, phase, info):
+        k = self.k
+        if phase == "pre":
+            self.on = bool(self.select(info))
+            if self.on:
+                if self.count[k] >= self.CAP:
+                    raise RuntimeError("too many stamped launches in one graph")
+                self._stamp(self.slots[k].data_ptr() + 16 * self.count[k])
+        elif self.on:
+            self._stamp(self.slots[k].data_ptr() + 16 * self.count[k] + 8)
+            self.count[k] += 1
+            self.on = False
+
+    def capturing(self, k):
+        import contextlib
+
+        from ltx_amd.kernels import gemm
+
+        @contextlib.contextmanager
+        def ctx():
+            self.k = k
+            gemm.LAUNCH_HOOK = self.hook
+            try:
+                yield
+            finally:
+                gemm.LAUNCH_HOOK = None
+                self.k = None
+
+        return ctx()
+
+    def ticks_per_ms(self) -> float:
+        from ltx_amd import _lib
+
+        torch = self.torch
+        r = torch.zeros(2, dtype=torch.int64, device="cuda")
+        s = torch.cuda.current_stream().cuda_stream
+        _lib.call("ltx_device_clock_stamp", r.data_ptr(), s)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        time.sleep(0.25)
+        _lib.call("ltx_device_clock_stamp", r.data_ptr() + 8, s)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        v = r.tolist()
+        return (v[1] - v[0]) / ((t1 - t0) * 1e3)
+
+    def durations_ms(self) -> list:
+        rate = self.ticks_per_ms()
+        v = self.slots.tolist()
+        out = []
+        for k, n in enumerate(self.count):
+            out += [(v[k][2 * i + 1] - v[k][2 * i]) / rate for i in range(n)]
+        return out
 
 
 def gemm_shapes(torch, fmt: str, m: int = 3456) -> dict:
@@ -563,12 +653,18 @@ def main(argv=None):
     run_step(0)
     torch.cuda.synchronize()
     graphs = None
+    from ltx_amd.kernels import gemm as _gemm
+
+    # the dominant kernel's launches (video FF up) get device clock stamps
+    # inside the captured step graphs, so its duration is read from the timed
+    # replays themselves
+    stamps = LaunchStamps(torch, nsig, lambda info: info[4] == _gemm.EPI_GELU and info[1] == tv and info[3] == 4096)
     if not args.no_graph:
         graphs = []
         pool = torch.cuda.graph_pool_handle()
         for i in range(nsig):
             g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, pool=pool):
+            with stamps.capturing(i), torch.cuda.graph(g, pool=pool):
                 run_step(i)
             graphs.append(g)
         torch.cuda.synchronize()
@@ -584,9 +680,22 @@ def main(argv=None):
     wall = time.perf_counter() - t_start
     ms = wall / args.steps * 1e3
 
-    # dominant kernel (FF up-projection GEMM) and every other GEMM, timed with
-    # stream events in eager steps
-    durs, gemm_step = gemm_step_profile(run_step, args.kernel_steps, tv, torch)
+    # dominant kernel (FF up-projection GEMM): its stamps in the last timed
+    # replay of each step graph (eager: stream events, below)
+    durs = stamps.durations_ms() if graphs else []
+
+    # every GEMM, timed with stream events in eager steps queued behind graph
+    # replays
+    def prefill():
+        for i in range(2):
+            do(i)
+
+    durs_eager, gemm_step, host_ms = gemm_step_profile(run_step, args.kernel_steps, tv, torch, prefill=prefill)
+    gemm_step["host_enqueue_ms_per_eager_step"] = round(host_ms, 1)
+    gemm_step["ff_up_us_eager_events"] = round(sum(durs_eager) / len(durs_eager) * 1e3, 1)
+    timing = "device clock stamps around each launch in the timed HIP-graph replays (last replay of each step graph)"
+    if not durs:
+        durs, timing = durs_eager, "stream events around each launch in eager steps"
     k_ms = sum(durs) / len(durs)
     k_flop = 2.0 * tv * 4096 * 16384
     achieved = k_flop / (k_ms * 1e-3) / 1e12
@@ -597,6 +706,7 @@ def main(argv=None):
                 "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic(kname, args.weights),
                 "launch_us": round(k_ms * 1e3, 1), "launches_timed": len(durs),
+                "launch_timing": timing,
                 "algorithmic_flop_per_launch": k_flop}
     flops = step_flops(tv, ta, s, args.layers)
     out = {
@@ -607,7 +717,7 @@ def main(argv=None):
         "config": {"workload": f"48-block LTX-2.3 AV denoise step at {args.width}x{args.height}x{args.frames}"
                                if args.layers == 48 else f"{args.layers}-block AV denoise step",
                    "video_tokens": tv, "audio_tokens": ta, "text_tokens": s, "blocks": args.layers,
-                   "weights": args.weights, "timing": "hip-graph replay" if graphs else "eager"},
+                   "weights": args.weights, "timing": "hip-graph replay, FF-up launches bracketed by device clock stamps" if graphs else "eager"},
         "tokens_per_s": round((tv + ta) / (ms * 1e-3), 1),
         "step_tflop": round(flops / 1e12, 2), "step_tflops_achieved": round(flops / (ms * 1e-3) / 1e12, 1),
         "ff_up_mfma_pct": round(100 * achieved / PEAK_BF16_TFLOPS, 1),

@@ -55,6 +55,14 @@ const char* ltx_status_string(int status);
 /* Library version, encoded as major*10000 + minor*100 + patch. */
 int ltx_version(void);
 
+/* Measurement aid with no counterpart in the reference: writes the GPU's
+ * constant-rate real-time counter (s_memrealtime) to dst[0] (device memory,
+ * 8-byte aligned) when the stream reaches the call; under graph capture it
+ * becomes a kernel node, so a pair of stamps times the work between them
+ * inside a replayed graph (HIP events cannot be recorded there).  Ticks per
+ * second are found by comparing two stamps with the host clock. */
+int ltx_device_clock_stamp(uint64_t* dst, void* stream);
+
 /* ---- flags for ltx_adaln_norm_fused_bf16 ---------------------------------- */
 /* Round the normalised row to bf16 before modulating: the reference's
  * `mx.fast.rms_norm(x)` (bf16 output) followed by the fp32 modulation, i.e.

@@ -40,6 +40,8 @@ int main(int argc, char** argv) {
   for (int s = -6; s <= 1; ++s) EXPECT(std::strlen(ltx_status_string(s)) > 0, 1);
   EXPECT(std::strcmp(ltx_status_string(LTX_OK), "ok"), 0);
   EXPECT(ltx_version() > 0, 1);
+  EXPECT(ltx_device_clock_stamp(nullptr, nullptr), LTX_ERR_INVALID_ARG);
+  EXPECT(ltx_device_clock_stamp(reinterpret_cast<uint64_t*>(static_cast<char*>(m) + 4), nullptr), LTX_ERR_ALIGNMENT);
 
   // row kernels
   EXPECT(ltx_adaln_norm_fused_bf16(nullptr, 4096, fd, fd, d, 4096, 4, 4096, 1e-6f, 0, nullptr), LTX_ERR_INVALID_ARG);

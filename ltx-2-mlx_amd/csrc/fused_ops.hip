@@ -533,6 +533,21 @@ extern "C" const char* ltx_status_string(int status) {
 
 extern "C" int ltx_version(void) { return 100; }
 
+// Device clock stamp: one lane writes the GPU's constant-rate real-time
+// counter into dst[0].  Stream-ordered like any kernel (and recorded as a
+// kernel node under graph capture), so two stamps bracket the work between
+// them on that stream.
+__global__ void clock_stamp_kernel(uint64_t* dst) {
+  if (threadIdx.x == 0) dst[0] = __builtin_amdgcn_s_memrealtime();
+}
+
+extern "C" int ltx_device_clock_stamp(uint64_t* dst, void* stream) {
+  if (!dst) return LTX_ERR_INVALID_ARG;
+  if (((uintptr_t)dst & 7u) != 0) return LTX_ERR_ALIGNMENT;
+  clock_stamp_kernel<<<1, 64, 0, (hipStream_t)stream>>>(dst);
+  return ltx_launch_status();
+}
+
 static int adaln_launch(const void* x, int64_t x_stride, const float* scale, const float* shift, void* out,
                         int64_t out_stride, const float* scale2, const float* shift2, void* out2,
                         int64_t out2_stride, int64_t rows, int64_t C, float eps, int flags, void* stream) {

@@ -86,6 +86,15 @@ constexpr int kNumXcd = 8;
 // a few instructions instead of the libm tanh and an IEEE division, absolute
 // error ~2e-7, far below the bf16 rounding of the result; saturates correctly
 // at +-inf.
+// bf16 rounding of two values with one conversion: the same bits as
+// round_bf on each
+__device__ __forceinline__ void round_bf2(float& x, float& y) {
+  asm("" : "+v"(x), "+v"(y));
+  const uint32_t u = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x, y}, bf16x2));
+  x = __uint_as_float(u << 16);
+  y = __uint_as_float(u & 0xffff0000u);
+}
+
 __device__ __forceinline__ float gelu_tanh(float x) {
   // 0.5 x (1 + tanh(u)) with u = sqrt(2/pi) (x + 0.044715 x^3) is
   // x sigmoid(2u) = x / (1 + 2^t), t = -2u log2(e) = x (A + B x^2):
@@ -1177,14 +1186,26 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
         const f32x4 bias4 = *reinterpret_cast<const f32x4*>(col_lds + wn * WN + nl);
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
+          // bf16 roundings two at a time (one conversion per pair)
           float y[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float a = acc[i][j][4 * g + e];
-            y[e] = (RTB ? round_bf(a) : a) + bias4[e];
-            if (EPI == LTX_GEMM_EPI_GELU) y[e] = gelu_tanh(round_bf(y[e]));
-            if (EPI == LTX_GEMM_EPI_SIGMOID2) y[e] = sigmoid2_bf(round_bf(y[e]));
-            if (SIG && gn + e >= p.sig_from) y[e] = sigmoid2_bf(round_bf(y[e]));
+          for (int e = 0; e < 4; ++e) y[e] = acc[i][j][4 * g + e];
+          if (RTB) {
+            round_bf2(y[0], y[1]);
+            round_bf2(y[2], y[3]);
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y[e] += bias4[e];
+          if (EPI == LTX_GEMM_EPI_GELU || EPI == LTX_GEMM_EPI_SIGMOID2 || SIG) {
+            float r[4] = {y[0], y[1], y[2], y[3]};
+            round_bf2(r[0], r[1]);
+            round_bf2(r[2], r[3]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              if (EPI == LTX_GEMM_EPI_GELU) y[e] = gelu_tanh(r[e]);
+              if (EPI == LTX_GEMM_EPI_SIGMOID2) y[e] = sigmoid2_bf(r[e]);
+              if (SIG && gn + e >= p.sig_from) y[e] = sigmoid2_bf(r[e]);
+            }
           }
           bf16x4 v;
 #pragma unroll

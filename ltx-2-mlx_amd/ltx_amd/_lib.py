@@ -24,6 +24,7 @@ _vp = ctypes.c_void_p
 # name -> argtypes (every function returns int status)
 SIGNATURES: dict[str, list] = {
     "ltx_version": [],
+    "ltx_device_clock_stamp": [_vp, _vp],
     "ltx_adaln_norm_fused_bf16": [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _int, _vp],
     "ltx_gated_add_fused_bf16": [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _int, _vp],
     "ltx_qknorm_rope_bf16": [

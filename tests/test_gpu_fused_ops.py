@@ -326,3 +326,42 @@ def test_timestep_embedding_and_gemv():
     torch.cuda.synchronize()
     ref = ofo.linear_f32(x, W, b, silu_in=True)
     assert max_rel_err(y.cpu().numpy(), ref) < 1e-4
+
+
+def test_device_clock_stamp_eager_and_in_graph():
+    """Stamps are stream-ordered: eager stamps around a busy kernel advance, and
+    a stamp pair captured in a HIP graph brackets the work between them on
+    every replay (later replays read later times)."""
+    from ltx_amd import _lib
+
+    st = torch.zeros(4, dtype=torch.int64, device=DEV)
+    a = torch.randn((2048, 2048), device=DEV)
+    c = torch.zeros_like(a)
+    s = torch.cuda.current_stream().cuda_stream
+    _lib.call("ltx_device_clock_stamp", st.data_ptr(), s)
+    for _ in range(20):
+        c.add_(a)
+    _lib.call("ltx_device_clock_stamp", st.data_ptr() + 8, s)
+    torch.cuda.synchronize()
+    t = st.tolist()
+    assert t[1] > t[0] > 0
+
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        cs = torch.cuda.current_stream().cuda_stream
+        _lib.call("ltx_device_clock_stamp", st.data_ptr() + 16, cs)
+        for _ in range(20):
+            c.add_(a)
+        _lib.call("ltx_device_clock_stamp", st.data_ptr() + 24, cs)
+    prev = None
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        t = st.tolist()
+        assert t[3] > t[2] > 0
+        if prev is not None:
+            assert t[2] > prev
+        prev = t[3]
+    # the stamp pair spans the twenty elementwise kernels: at least a few microseconds on
+    # the 100 MHz-class counter, far less than a second
+    assert 10 < t[3] - t[2] < 100_000_000

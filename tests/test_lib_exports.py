@@ -71,6 +71,9 @@ def test_argument_validation_without_gpu():
                                      None) == -4
     assert lib.ltx_flash_attn_splitkv_v_bf16(16, 4096, 16, 4096, 16, 4100, 16, 4096, None, 0, 4, 4, 32, 128, 0.1,
                                              4, 16, 1 << 20, None) == -4
+    # device clock stamp: null or misaligned destination rejected before any launch
+    assert lib.ltx_device_clock_stamp(None, None) == -1
+    assert lib.ltx_device_clock_stamp(12, None) == -4
     # zero rows is a no-op success
     assert lib.ltx_adaln_norm_fused_bf16(16, 4096, 16, 16, 16, 4096, 0, 4096, 1e-6, 0, None) == 0
     # FP8 checkpoint dequant: null codes -> invalid, fp16 output -> unsupported,
