@@ -198,57 +198,73 @@ struct RopeRows {
   int n;  // 0: no RoPE
 };
 
+// One row in place: its values stay in registers for the reduction; the
+// RoPE table entries of chunk j are loaded while chunk j-1 is written (the
+// first chunk's during the reduction), so at most two chunks' tables are live.
 template <int PPL, int HALF_VECS>
 __device__ __forceinline__ void qknorm_rope_row(bf16* row, const float* w_lds, const RopeRows& tr, float eps,
-                                                int lane, float (&cs)[PPL][8], float (&sn)[PPL][8],
-                                                bool load_table) {
+                                                int lane) {
   constexpr int D = PPL * 1024;
-  float a[PPL][8], b[PPL][8];
+  bf16x8 a[PPL], b[PPL];  // packed; widened where used
   int v1[PPL];
 #pragma unroll
   for (int j = 0; j < PPL; ++j) {
     const int p = lane + j * kWave;
     v1[j] = (p / HALF_VECS) * (2 * HALF_VECS) + (p % HALF_VECS);
-    load8(row + v1[j] * 8, a[j]);
-    load8(row + (v1[j] + HALF_VECS) * 8, b[j]);
-    if (load_table && tr.n > 0) {
-      load8f(tr.c[0] + p * 8, cs[j]);
-      load8f(tr.s[0] + p * 8, sn[j]);
+    a[j] = *reinterpret_cast<const bf16x8*>(row + v1[j] * 8);
+    b[j] = *reinterpret_cast<const bf16x8*>(row + (v1[j] + HALF_VECS) * 8);
+  }
+  auto load_tab = [&](int j, float (&c)[8], float (&s)[8]) {
+    const int p = lane + j * kWave;
+    load8f(tr.c[0] + p * 8, c);
+    load8f(tr.s[0] + p * 8, s);
 #pragma unroll
-      for (int ax = 1; ax < 3; ++ax) {
-        if (ax < tr.n) {
-          float c2[8], s2[8];
-          load8f(tr.c[ax] + p * 8, c2);
-          load8f(tr.s[ax] + p * 8, s2);
+    for (int ax = 1; ax < 3; ++ax) {
+      if (ax < tr.n) {
+        float c2[8], s2[8];
+        load8f(tr.c[ax] + p * 8, c2);
+        load8f(tr.s[ax] + p * 8, s2);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            cs[j][i] *= c2[i];
-            sn[j][i] += s2[i];
-          }
+        for (int i = 0; i < 8; ++i) {
+          c[i] *= c2[i];
+          s[i] += s2[i];
         }
       }
     }
-  }
+  };
+  float cs[2][8], sn[2][8];
+  if (tr.n > 0) load_tab(0, cs[0], sn[0]);
   float ss = 0.0f;
 #pragma unroll
   for (int j = 0; j < PPL; ++j)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ss = fmaf(a[j][i], a[j][i], fmaf(b[j][i], b[j][i], ss));
+    for (int i = 0; i < 8; ++i) {
+      const float fa = (float)a[j][i], fb = (float)b[j][i];
+      ss = fmaf(fa, fa, fmaf(fb, fb, ss));
+    }
   ss = wave_sum(ss);
   const float inv = rsqrt_rn(ss * (1.0f / (float)D) + eps);
 #pragma unroll
   for (int j = 0; j < PPL; ++j) {
+    // keep the table loads of chunk j+1 here (not hoisted above the
+    // reduction, which would hold every chunk's table in registers)
+    __builtin_amdgcn_sched_barrier(0);
+    if (tr.n > 0 && j + 1 < PPL) load_tab(j + 1, cs[(j + 1) & 1], sn[(j + 1) & 1]);
     float wa[8], wb[8];
     load8f(w_lds + v1[j] * 8, wa);
     load8f(w_lds + (v1[j] + HALF_VECS) * 8, wb);
     float oa[8], ob[8];
+    // re-widen the packed values here (the widened copies of the reduction
+    // are not kept alive until now)
+    bf16x8 aj = a[j], bj = b[j];
+    asm volatile("" : "+v"(aj), "+v"(bj));
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float x1 = round_bf(a[j][i] * inv * wa[i]);
-      const float x2 = round_bf(b[j][i] * inv * wb[i]);
+      const float x1 = round_bf((float)aj[i] * inv * wa[i]);
+      const float x2 = round_bf((float)bj[i] * inv * wb[i]);
       if (tr.n > 0) {
-        oa[i] = x1 * cs[j][i] - x2 * sn[j][i];
-        ob[i] = x1 * sn[j][i] + x2 * cs[j][i];
+        oa[i] = x1 * cs[j & 1][i] - x2 * sn[j & 1][i];
+        ob[i] = x1 * sn[j & 1][i] + x2 * cs[j & 1][i];
       } else {
         oa[i] = x1;
         ob[i] = x2;
@@ -288,8 +304,13 @@ __device__ __forceinline__ RopeRows rope_rows(const RopeTable& t, int64_t tok, i
   return r;
 }
 
+// One wave per row: with both operands, task 2t is Q row t and task 2t+1 is K
+// row t (a wave keeps its parity: the wave count is even), so a token's two
+// rows run side by side and its table rows are fetched once from memory and
+// once from cache.  At most 128 registers per lane (4 waves per SIMD): the
+// whole step-size launch (2 x 3456 rows) is resident at once.
 template <int PPL, int HALF_VECS, int THREADS>
-__global__ __launch_bounds__(THREADS) void qknorm_rope_kernel(
+__global__ __launch_bounds__(THREADS, 4) void qknorm_rope_kernel(
     bf16* q, int64_t q_stride, int64_t rows_q, const float* __restrict__ wq, RopeTable tq, bf16* k,
     int64_t k_stride, int64_t rows_k, const float* __restrict__ wk, RopeTable tk, float eps) {
   constexpr int D = PPL * 1024;
@@ -305,17 +326,15 @@ __global__ __launch_bounds__(THREADS) void qknorm_rope_kernel(
   const int64_t nwaves = (int64_t)gridDim.x * WAVES;
   const int64_t rows = rows_q > rows_k ? rows_q : rows_k;
   const int64_t half = D / 2;
-  const bool shared_table = tq.cos == tk.cos && tq.sin == tk.sin && tq.idx == tk.idx && tq.axes == tk.axes;
-  float cs[PPL][8], sn[PPL][8];
-  for (int64_t t = wave0; t < rows; t += nwaves) {
-    bool have_table = false;
-    if (t < rows_q) {
-      qknorm_rope_row<PPL, HALF_VECS>(q + t * q_stride, w_lds, rope_rows(tq, t, half), eps, lane, cs, sn, true);
-      have_table = true;
-    }
-    if (t < rows_k) {
-      qknorm_rope_row<PPL, HALF_VECS>(k + t * k_stride, w_lds + D, rope_rows(tk, t, half), eps, lane, cs, sn,
-                                      !(have_table && shared_table));
+  const bool both = rows_q > 0 && rows_k > 0;
+  const int64_t tasks = both ? 2 * rows : rows;
+  for (int64_t r = wave0; r < tasks; r += nwaves) {
+    const int64_t t = both ? (r >> 1) : r;
+    const bool is_k = both ? (r & 1) != 0 : rows_k > 0;
+    if (!is_k) {
+      if (t < rows_q) qknorm_rope_row<PPL, HALF_VECS>(q + t * q_stride, w_lds, rope_rows(tq, t, half), eps, lane);
+    } else if (t < rows_k) {
+      qknorm_rope_row<PPL, HALF_VECS>(k + t * k_stride, w_lds + D, rope_rows(tk, t, half), eps, lane);
     }
   }
 }
@@ -647,9 +666,10 @@ static int qknorm_rope_launch(void* q, int64_t q_stride, int64_t rows_q, const f
   const int64_t rows = rows_q > rows_k ? rows_q : rows_k;
   if (rows == 0) return LTX_OK;
   hipStream_t s = (hipStream_t)stream;
+  const int64_t tasks = (rows_q > 0 && rows_k > 0) ? 2 * rows : rows;
   // few rows: 8-wave workgroups (one LDS copy of the norm weights per 8 rows)
-  const bool few = rows <= kFewRows;
-  const int grid = few ? row_grid(rows, kMaxRowBlocks, 8) : row_grid(rows);
+  const bool few = tasks <= kFewRows;
+  const int grid = few ? row_grid(tasks, kMaxRowBlocks, 8) : row_grid(tasks);
   bf16* qp = (bf16*)q;
   bf16* kp = (bf16*)k;
 #define LTX_QK_LAUNCH(PPL, HV)                                                                          \
