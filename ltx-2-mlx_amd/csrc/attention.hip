@@ -24,7 +24,9 @@
 // lane-local plus one cross-half exchange (v_permlane32_swap), and P^T feeds
 // the P.V MFMA straight from registers (O^T += Vt . P^T).  K and V stream
 // through LDS in 64-key stages by direct global->LDS buffer loads, in rings
-// of 4 stages (a workgroup sync every other stage; 2 for the split-KV tiles).
+// of 4 stages (a workgroup sync every other stage; 2 for the split-KV tiles);
+// a key range that fits the ring (text contexts, the audio tokens) is loaded
+// whole before the first block, with one sync.
 // Key blocks are software-pipelined inside each wave, because VALU work only
 // overlaps the issuing wave's own MFMAs: the softmax of block b is cut into
 // one piece per MFMA slot (row max, running-max update, then exp2 / row sum
@@ -224,6 +226,8 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
   const int kb0 = split * per_split;
   const int kb1 = (kb0 + per_split) < nblocks_all ? (kb0 + per_split) : nblocks_all;
   const int nb = kb1 > kb0 ? kb1 - kb0 : 0;
+  // a key range that fits the K / V rings is loaded whole before the first block
+  const int pre = __builtin_amdgcn_readfirstlane(nb <= RING ? 1 : 0);
   const int k_step = (int)(kAttnKB * k_rs * 2);
   const int v_step = VROW ? (int)(kAttnKB * v_ld * 2) : kAttnKB * 2;
   auto issue_k = [&](int kb, int buf) {
@@ -421,7 +425,7 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
       __builtin_amdgcn_sched_barrier(0);
       const int nn = n + PF;
       if (PV && nn < NP) vf[nn / DTILES][nn % DTILES] = read_v(VSLOT, nn / DTILES, nn % DTILES);
-      if (NEW && nn == NP) {
+      if (NEW && nn == NP && !pre) {
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (RING == 2) {
           sync_stage();
@@ -484,10 +488,20 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
   };
 
   if (nb > 0) {
-    issue_k(kb0, 0);
-    sync_stage();
-    if (nb > 1) issue_k(kb0 + 1, 1);
-    issue_v(kb0, 0);
+    if (pre) {
+      // every key block fits the ring: all of K and V in flight at once, one
+      // sync, no further stage syncs
+      for (int i = 0; i < nb; ++i) {
+        issue_k(kb0 + i, i);
+        issue_v(kb0 + i, i);
+      }
+      sync_stage();
+    } else {
+      issue_k(kb0, 0);
+      sync_stage();
+      if (nb > 1) issue_k(kb0 + 1, 1);
+      issue_v(kb0, 0);
+    }
 #pragma unroll
     for (int k = 0; k < PF; ++k) read_k(0, k);
     half1(I0(), BT(), BF());
