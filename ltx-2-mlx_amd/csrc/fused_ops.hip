@@ -304,10 +304,9 @@ __device__ __forceinline__ RopeRows rope_rows(const RopeTable& t, int64_t tok, i
   return r;
 }
 
-// One wave per row: with both operands, task 2t is Q row t and task 2t+1 is K
-// row t (a wave keeps its parity: the wave count is even), so a token's two
-// rows run side by side and its table rows are fetched once from memory and
-// once from cache.  At most 128 registers per lane (4 waves per SIMD): the
+// One wave per row: task 2t is Q row t and task 2t+1 is K row t while both
+// operands have rows, so a token's two rows run side by side and its table
+// rows are fetched once from memory and once from cache.  At most 128 registers per lane (4 waves per SIMD): the
 // whole step-size launch (2 x 3456 rows) is resident at once.
 template <int PPL, int HALF_VECS, int THREADS>
 __global__ __launch_bounds__(THREADS, 4) void qknorm_rope_kernel(
@@ -324,13 +323,14 @@ __global__ __launch_bounds__(THREADS, 4) void qknorm_rope_kernel(
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t wave0 = (int64_t)blockIdx.x * WAVES + (threadIdx.x >> 6);
   const int64_t nwaves = (int64_t)gridDim.x * WAVES;
-  const int64_t rows = rows_q > rows_k ? rows_q : rows_k;
   const int64_t half = D / 2;
-  const bool both = rows_q > 0 && rows_k > 0;
-  const int64_t tasks = both ? 2 * rows : rows;
+  // tasks [0, 2 mn) pair the operands' rows; the rest are the larger
+  // operand's remaining rows
+  const int64_t mn = rows_q < rows_k ? rows_q : rows_k;
+  const int64_t tasks = rows_q + rows_k;
   for (int64_t r = wave0; r < tasks; r += nwaves) {
-    const int64_t t = both ? (r >> 1) : r;
-    const bool is_k = both ? (r & 1) != 0 : rows_k > 0;
+    const int64_t t = r < 2 * mn ? (r >> 1) : mn + (r - 2 * mn);
+    const bool is_k = r < 2 * mn ? (r & 1) != 0 : rows_k > rows_q;
     if (!is_k) {
       if (t < rows_q) qknorm_rope_row<PPL, HALF_VECS>(q + t * q_stride, w_lds, rope_rows(tq, t, half), eps, lane);
     } else if (t < rows_k) {
@@ -666,18 +666,19 @@ static int qknorm_rope_launch(void* q, int64_t q_stride, int64_t rows_q, const f
   const int64_t rows = rows_q > rows_k ? rows_q : rows_k;
   if (rows == 0) return LTX_OK;
   hipStream_t s = (hipStream_t)stream;
-  const int64_t tasks = (rows_q > 0 && rows_k > 0) ? 2 * rows : rows;
-  // 16-wave workgroups for launches of at most 8192 rows (the step's: all
-  // resident at once, one LDS copy of the norm weights per 16 rows), 8-wave
-  // workgroups in a grid of at most 2048 above (measured fastest for each:
-  // 3456-row Q + K 42.2 -> 39.9 us, 2 x 14640 rows 149.7 -> 142.6 us against
-  // the 4-wave workgroups)
-  const bool few = tasks <= kFewRows;
-  const int grid = few ? row_grid(tasks, kMaxRowBlocks, 16) : row_grid(tasks, kMaxRowBlocks, 8);
+  const int64_t tasks = rows_q + rows_k;
+  // 16-wave workgroups for 1024 < tasks <= 8192 (the step's 3456-row
+  // launches: all resident at once, one LDS copy of the norm weights per 16
+  // rows), 8-wave workgroups otherwise, in a grid of at most 2048 (measured
+  // fastest for each: 3456-row Q + K 42.2 -> 39.9 us, 2 x 14640 rows 149.7 ->
+  // 142.6 us against 4-wave workgroups; 68 + 68 rows 7.9 against 10.9 us in
+  // 16-wave ones)
+  const bool wide = tasks > 1024 && tasks <= kFewRows;
+  const int grid = row_grid(tasks, kMaxRowBlocks, wide ? 16 : 8);
   bf16* qp = (bf16*)q;
   bf16* kp = (bf16*)k;
 #define LTX_QK_LAUNCH(PPL, HV)                                                                            \
-  (few ? (qknorm_rope_kernel<PPL, HV, 1024><<<grid, 1024, 0, s>>>(qp, q_stride, rows_q, wq, tq, kp, k_stride,   \
+  (wide ? (qknorm_rope_kernel<PPL, HV, 1024><<<grid, 1024, 0, s>>>(qp, q_stride, rows_q, wq, tq, kp, k_stride,   \
                                                                  rows_k, wk, tk, eps))                          \
        : (qknorm_rope_kernel<PPL, HV, 512><<<grid, 512, 0, s>>>(qp, q_stride, rows_q, wq, tq, kp, k_stride,     \
                                                                rows_k, wk, tk, eps)))
