@@ -364,9 +364,9 @@ class LaunchStamps:
 
     CAP = 128  # stamped launches per graph
 
-    def __init__(self, torch, graphs: int, select):
+    def __init__(self, torch, graphs: int, select, device: str = "cuda"):
         self.torch, self.select = torch, select
-        self.slots = torch.zeros((graphs, 2 * self.CAP), dtype=torch.int64, device="cuda")
+        self.slots = torch.zeros((graphs, 2 * self.CAP), dtype=torch.int64, device=device)
         self.count = [0] * graphs
         self.k, self.on = None, False
 
@@ -421,8 +421,8 @@ class LaunchStamps:
         v = r.tolist()
         return (v[1] - v[0]) / ((t1 - t0) * 1e3)
 
-    def durations_ms(self) -> list:
-        rate = self.ticks_per_ms()
+    def durations_ms(self, rate=None) -> list:
+        rate = self.ticks_per_ms() if rate is None else rate
         v = self.slots.tolist()
         out = []
         for k, n in enumerate(self.count):

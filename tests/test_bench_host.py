@@ -53,3 +53,33 @@ def test_traffic_record_is_consistent():
         assert bench.measured_traffic(r["kernel"], r["weights"]) == r["hbm_bytes"]
         assert r["hbm_bytes"] > r["algorithmic_bytes"]
     assert bench.measured_traffic("no such kernel", "mxfp8") is None
+
+
+def test_launch_stamps_pair_the_chosen_launches():
+    """The stamp recorder brackets exactly the launches `select` chooses, in
+    per-graph slot ranges, and turns stamp pairs into durations."""
+    import torch
+
+    st = bench.LaunchStamps(torch, 2, lambda info: info[0] == "ff_up", device="cpu")
+    written = []
+
+    def fake_stamp(addr):  # records the slot a stamp kernel would write
+        written.append(addr)
+        base = st.slots.data_ptr()
+        idx = (addr - base) // 8
+        st.slots.view(-1)[idx] = 1000 * (len(written))
+
+    st._stamp = fake_stamp
+    launches = [("qkv",), ("ff_up",), ("out",), ("ff_up",)]
+    for k in range(2):
+        st.k = k
+        for info in launches:
+            st.hook("pre", info)
+            st.hook("post", info)
+    assert st.count == [2, 2]
+    row = st.slots.shape[1] * 8
+    base = st.slots.data_ptr()
+    # graph k's pairs at slots 0..3 of its row, pre before post
+    assert written == [base + k * row + o for k in range(2) for o in (0, 8, 16, 24)]
+    d = st.durations_ms(rate=1000.0)  # 1000 ticks per ms
+    assert d == [1.0, 1.0, 1.0, 1.0]
