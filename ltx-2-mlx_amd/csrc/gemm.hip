@@ -1303,10 +1303,14 @@ template <int BKIND, int EPI>
 static int launch_epi(const GemmArgs& p, int tile, hipStream_t s) {
   if (tile == 0) {
     // Large tiles when they still give most CUs a tile; 128x128 otherwise.
-    // (256x128 tiles, 5 % faster on A2V Q alone, were 0.25 ms slower per
-    // step with the audio stream sharing the CUs: explicit only.)
+    // MXFP8 takes the 8-wave kernel from 100 tiles of 256x256: the A2V query
+    // projection (3456 x 4096 -> 2048, 112 tiles) runs in 76 instead of 86 us
+    // alone, and the step gains 0.6-0.7 ms (the CUs its single round leaves
+    // free take the audio stream's work).  (256x128 tiles, 14 % faster on
+    // that projection alone, were 0.25 ms slower per step: explicit only.)
     const int64_t big = (int64_t)((p.M + 255) / 256) * ((p.N + 255) / 256);
-    tile = big >= 160 ? (BKIND == B_MXFP8 && g8_ok<BKIND>(p) ? 5 : 1) : 2;
+    const bool g8 = BKIND == B_MXFP8 && g8_ok<BKIND>(p);
+    tile = big >= 160 ? (g8 ? 5 : 1) : (big >= 100 && g8 ? 5 : 2);
   }
   if (tile == 5) {
     if constexpr (BKIND != B_BF16) {
