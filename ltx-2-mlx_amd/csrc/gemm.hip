@@ -81,11 +81,6 @@ constexpr int kEpiPartial = 16;
 constexpr int kGroupM = 4;
 constexpr int kNumXcd = 8;
 
-// GELU with the tanh approximation (feed_forward.py:8-14).  tanh(u) is
-// evaluated as 1 - 2 / (exp(2u) + 1) with the hardware exp2 and reciprocal
-// a few instructions instead of the libm tanh and an IEEE division, absolute
-// error ~2e-7, far below the bf16 rounding of the result; saturates correctly
-// at +-inf.
 // bf16 rounding of two values with one conversion: the same bits as
 // round_bf on each
 __device__ __forceinline__ void round_bf2(float& x, float& y) {
@@ -95,6 +90,11 @@ __device__ __forceinline__ void round_bf2(float& x, float& y) {
   y = __uint_as_float(u & 0xffff0000u);
 }
 
+// GELU with the tanh approximation (feed_forward.py:8-14).  tanh(u) is
+// evaluated as 1 - 2 / (exp(2u) + 1) with the hardware exp2 and reciprocal
+// a few instructions instead of the libm tanh and an IEEE division, absolute
+// error ~2e-7, far below the bf16 rounding of the result; saturates correctly
+// at +-inf.
 __device__ __forceinline__ float gelu_tanh(float x) {
   // 0.5 x (1 + tanh(u)) with u = sqrt(2/pi) (x + 0.044715 x^3) is
   // x sigmoid(2u) = x / (1 + 2^t), t = -2u log2(e) = x (A + B x^2):
