@@ -306,8 +306,9 @@ __device__ __forceinline__ RopeRows rope_rows(const RopeTable& t, int64_t tok, i
 
 // One wave per row: task 2t is Q row t and task 2t+1 is K row t while both
 // operands have rows, so a token's two rows run side by side and its table
-// rows are fetched once from memory and once from cache.  At most 128 registers per lane (4 waves per SIMD): the
-// whole step-size launch (2 x 3456 rows) is resident at once.
+// rows are fetched once from memory and once from cache.  At most 128
+// registers per lane: 4 waves per SIMD (the earlier layout needed 183, 2 per
+// SIMD).
 template <int PPL, int HALF_VECS, int THREADS>
 __global__ __launch_bounds__(THREADS, 4) void qknorm_rope_kernel(
     bf16* q, int64_t q_stride, int64_t rows_q, const float* __restrict__ wq, RopeTable tq, bf16* k,
@@ -668,8 +669,8 @@ static int qknorm_rope_launch(void* q, int64_t q_stride, int64_t rows_q, const f
   hipStream_t s = (hipStream_t)stream;
   const int64_t tasks = rows_q + rows_k;
   // 16-wave workgroups for 1024 < tasks <= 8192 (the step's 3456-row
-  // launches: all resident at once, one LDS copy of the norm weights per 16
-  // rows), 8-wave workgroups otherwise, in a grid of at most 2048 (measured
+  // launches; one LDS copy of the norm weights per 16 rows), 8-wave
+  // workgroups otherwise, in a grid of at most 2048 (measured
   // fastest for each: 3456-row Q + K 42.2 -> 39.9 us, 2 x 14640 rows 149.7 ->
   // 142.6 us against 4-wave workgroups; 68 + 68 rows 7.9 against 10.9 us in
   // 16-wave ones)
