@@ -117,9 +117,12 @@ def _check(got, ref, min_exact=0.9):
 
 
 @pytest.mark.parametrize("kind", ["bf16", "int8", "mxfp8"])
-@pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 16384), (16384, 4096)])
+@pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 16384), (16384, 4096), (4096, 2048), (2048, 4096)])
 def test_gemm_block_shapes(kind, K, N):
-    """The projection shapes of one video block at M = 3456 tokens."""
+    """The projection shapes of one video block at M = 3456 tokens (the last
+    two: the A2V query and output projections, whose 112 / 224 tiles of
+    256 x 256 take the 8-wave kernel for MXFP8 weights by the automatic
+    tile choice)."""
     from ltx_amd.kernels import gemm
 
     rng = np.random.default_rng(K + N)
