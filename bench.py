@@ -91,11 +91,14 @@ def parse_args(argv=None):
     ap.add_argument("--no-clip-768x512x121", action="store_true", help="skip the 768x512x121 leg")
     ap.add_argument("--no-gemm-shapes", action="store_true", help="skip the per-shape GEMM leg")
     ap.add_argument("--cpu-runs", type=int, default=5, help="timed oracle block runs after one warmup")
-    ap.add_argument("--counter-workload", choices=["ff-up", "ff-up-vs-library", "copy", "fused-ops"], default=None,
+    ap.add_argument("--counter-workload", choices=["ff-up", "ff-up-vs-library", "copy", "fused-ops", "attention"],
+                    default=None,
                     help="run only a short workload for rocprofv3 --pmc passes and exit: the video FF "
                          "up-projection GEMM (4 launches, --weights format), the three row kernels (adaln, "
-                         "gated add, QK-norm + RoPE; 4 cache-cold launches each) or a 1 GiB device copy (3 "
-                         "launches, the FETCH_SIZE / WRITE_SIZE calibration)")
+                         "gated add, QK-norm + RoPE; 4 cache-cold launches each), the video self-attention at "
+                         "3456 and 6144 tokens and the 3456 x 256 text cross-attention (4 launches each, 32 "
+                         "heads of 128, gated) or a 1 GiB device copy (3 launches, the FETCH_SIZE / WRITE_SIZE "
+                         "calibration)")
     return ap.parse_args(argv)
 
 
@@ -113,6 +116,18 @@ def counter_workload(kind: str, weights: str) -> None:
                 for i in range(4):
                     fn(i)
             del launchers
+    elif kind == "attention":
+        from ltx_amd.kernels.attention import flash_attention
+
+        g = torch.Generator(device="cuda").manual_seed(0)
+        for tq, tk in ((3456, 3456), (6144, 6144), (3456, 256)):
+            q = torch.randn((tq, 4096), generator=g, device="cuda").bfloat16()
+            k = torch.randn((tk, 4096), generator=g, device="cuda").bfloat16()
+            v = torch.randn((tk, 4096), generator=g, device="cuda").bfloat16()
+            gate = (torch.rand((tq, 32), generator=g, device="cuda") * 2).bfloat16()
+            out = torch.empty((tq, 4096), dtype=torch.bfloat16, device="cuda")
+            for _ in range(4):
+                flash_attention(q, k, v, 32, gate=gate, out=out)
     elif kind == "copy":
         src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
