@@ -171,6 +171,7 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
   const int work = SPLIT ? logical / nsplit : logical;
   const int head = work / qtiles;
   const int q0 = (work % qtiles) * kAttnQ + wave * 32;
+  const int live = __builtin_amdgcn_readfirstlane(q0 < Tq ? 1 : 0);
 
   const bf16* Kh = K + (int64_t)head * DH;
   const bf16* Vh = VROW ? V + (int64_t)head * DH : V + (int64_t)head * DH * v_ld;
@@ -343,9 +344,10 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
   // Half 1 of iteration b: S^T of block b from K slot Q into s[P] (its first
   // PF K fragments already in flight); remaining exps of block b-1 (s[1-P]);
   // first V reads of half 2 (block b-1, slot Q-1).
-  auto half1 = [&](auto qc, auto qkc, auto expc) {
+  auto half1 = [&](auto qc, auto qkc, auto expc, auto livec) __attribute__((always_inline)) {
     constexpr int Q = decltype(qc)::value, P = Q & 1;
-    constexpr bool QK = decltype(qkc)::value, EXP = decltype(expc)::value;
+    constexpr bool LV = decltype(livec)::value;
+    constexpr bool QK = decltype(qkc)::value && LV, EXP = decltype(expc)::value && LV;
     constexpr int VSLOT = (Q + RING - 1) % RING;
     if (QK) {
 #pragma unroll
@@ -402,9 +404,13 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
   // K_{b+3}, K_{b+4}, V_{b+2}, V_{b+3} into the slots of K_{b-1}, K_b,
   // V_{b-2}, V_{b-1}: each block is loaded before the sync that precedes its
   // first read.  The remaining slots read the first K fragments of block b+1.
-  auto half2 = [&](auto qc, auto pvc, auto newc, int b) {
+  auto half2 = [&](auto qc, auto pvc, auto newc, int b, auto livec) __attribute__((always_inline)) {
     constexpr int Q = decltype(qc)::value, P = Q & 1;
-    constexpr bool PV = decltype(pvc)::value, NEW = decltype(newc)::value;
+    constexpr bool LV = decltype(livec)::value;
+    // NEW_STAGE: the stage syncs and loads, which every wave runs; NEW: the
+    // block's own softmax work, which a wave without queries skips
+    constexpr bool NEW_STAGE = decltype(newc)::value;
+    constexpr bool PV = decltype(pvc)::value && LV, NEW = NEW_STAGE && LV;
     constexpr int VSLOT = (Q + RING - 1) % RING;
     const int kb = kb0 + b;
     if (PV && __any(alpha_pend != 1.0f)) {
@@ -425,7 +431,7 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
       __builtin_amdgcn_sched_barrier(0);
       const int nn = n + PF;
       if (PV && nn < NP) vf[nn / DTILES][nn % DTILES] = read_v(VSLOT, nn / DTILES, nn % DTILES);
-      if (NEW && nn == NP && !pre) {
+      if (NEW_STAGE && nn == NP && !pre) {
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (RING == 2) {
           sync_stage();
@@ -477,14 +483,14 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
   using BT = std::integral_constant<bool, true>;
   using BF = std::integral_constant<bool, false>;
   // iteration b in [1, nb), Q = b % RING
-  auto body = [&](auto qc, int b) {
-    half1(qc, BT(), BT());
-    half2(qc, BT(), BT(), b);
+  auto body = [&](auto qc, int b, auto livec) __attribute__((always_inline)) {
+    half1(qc, BT(), BT(), livec);
+    half2(qc, BT(), BT(), b, livec);
   };
   // drain (iteration nb): last exps and P.V of block nb-1
-  auto drain = [&](auto qc) {
-    half1(qc, BF(), BT());
-    half2(qc, BT(), BF(), 0);
+  auto drain = [&](auto qc, auto livec) __attribute__((always_inline)) {
+    half1(qc, BF(), BT(), livec);
+    half2(qc, BT(), BF(), 0, livec);
   };
 
   if (nb > 0) {
@@ -502,36 +508,45 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
       if (nb > 1) issue_k(kb0 + 1, 1);
       issue_v(kb0, 0);
     }
+    // a wave whose 32 queries all lie past Tq (the last query tile of a head)
+    // issues no MFMAs and no softmax work; it still moves its share of every
+    // K / V stage and meets every stage sync, at the same points of the loop
+    auto run_blocks = [&](auto lv) __attribute__((always_inline)) {
+      if (decltype(lv)::value) {
 #pragma unroll
-    for (int k = 0; k < PF; ++k) read_k(0, k);
-    half1(I0(), BT(), BF());
-    half2(I0(), BF(), BT(), 0);
-    int b = 1;
-    if constexpr (RING == 2) {
-      for (; b + 1 < nb; b += 2) {
-        body(I1(), b);
-        body(I0(), b + 1);
+        for (int k = 0; k < PF; ++k) read_k(0, k);
       }
-      if (b < nb) body(I1(), b);
-      if (nb & 1) drain(I1()); else drain(I0());
-    } else {
-      for (; b + 3 < nb; b += 4) {
-        body(I1(), b);
-        body(I2(), b + 1);
-        body(I3(), b + 2);
-        body(I0(), b + 3);
+      half1(I0(), BT(), BF(), lv);
+      half2(I0(), BF(), BT(), 0, lv);
+      int b = 1;
+      if constexpr (RING == 2) {
+        for (; b + 1 < nb; b += 2) {
+          body(I1(), b, lv);
+          body(I0(), b + 1, lv);
+        }
+        if (b < nb) body(I1(), b, lv);
+        if (nb & 1) drain(I1(), lv); else drain(I0(), lv);
+      } else {
+        for (; b + 3 < nb; b += 4) {
+          body(I1(), b, lv);
+          body(I2(), b + 1, lv);
+          body(I3(), b + 2, lv);
+          body(I0(), b + 3, lv);
+        }
+        // b % 4 == 1 here; up to three more iterations
+        if (b < nb) body(I1(), b++, lv);
+        if (b < nb) body(I2(), b++, lv);
+        if (b < nb) body(I3(), b++, lv);
+        switch (nb % 4) {
+          case 0: drain(I0(), lv); break;
+          case 1: drain(I1(), lv); break;
+          case 2: drain(I2(), lv); break;
+          default: drain(I3(), lv); break;
+        }
       }
-      // b % 4 == 1 here; up to three more iterations
-      if (b < nb) body(I1(), b++);
-      if (b < nb) body(I2(), b++);
-      if (b < nb) body(I3(), b++);
-      switch (nb % 4) {
-        case 0: drain(I0()); break;
-        case 1: drain(I1()); break;
-        case 2: drain(I2()); break;
-        default: drain(I3()); break;
-      }
-    }
+    };
+    if (live) run_blocks(BT());
+    else run_blocks(BF());
   }
 
   const int q = q0 + l32;
