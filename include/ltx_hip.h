@@ -463,7 +463,9 @@ int ltx_flash_attn_splitkv_bf16(const void* Q, int64_t q_rs, const void* K, int6
  * allocation: the partials go to a scratch array of
  * LTX_ATTN_NOALLOC_SCRATCH_BYTES that the library holds in device memory, one
  * per GPU, for the life of the process (its address is resolved once per
- * device, on the first call whose stream is on that device).  No counterpart
+ * device, on the first call whose stream is on that device; make that first
+ * call outside HIP graph capture -- later calls only enqueue kernels and can
+ * be captured).  No counterpart
  * in the reference: it exists for callers that cannot allocate device memory
  * (code under HIP graph capture, serving loops, harnesses that forbid
  * hipMalloc).  Same arguments and result contract as

@@ -149,6 +149,15 @@ int main(int argc, char** argv) {
                                              0.125f, 300, nullptr), LTX_ERR_INVALID_ARG);  // splits > 256
   EXPECT(ltx_flash_attn_splitkv_noalloc_bf16(d, 4096, d, 4096, d, 65536, d, 4096, nullptr, 0, 65536, 65536, 32,
                                              128, 0.1f, 256, nullptr), LTX_ERR_SCRATCH_LIMIT);
+  // oversize arguments: refused by the operand checks before the scratch need
+  // is computed, and the size helper reports -1 rather than a wrapped count
+  const int64_t hh = int64_t(1) << 40;
+  EXPECT(ltx_attn_splitkv_workspace_bytes(int64_t(1) << 40, hh, 128, 256), -1);
+  EXPECT(ltx_attn_splitkv_workspace_bytes(INT64_MAX, 1, 1, 1), -1);
+  EXPECT(ltx_flash_attn_splitkv_noalloc_bf16(d, hh * 128, d, hh * 128, d, 64, d, hh * 128, nullptr, 0, 1 << 30, 1,
+                                             hh, 128, 0.1f, 256, nullptr), LTX_ERR_UNSUPPORTED);
+  EXPECT(ltx_flash_attn_splitkv_noalloc_bf16(d, 4096, d, 4096, d, 32, d, 4096, nullptr, 0, 68, 3456, 32, 128,
+                                             0.1f, 16, nullptr), LTX_ERR_INVALID_ARG);  // tk_pad below Tk
 
   std::printf("%s: %d failure(s)\n", failures ? "FAIL" : "ok", failures);
   return failures ? 1 : 0;

@@ -53,15 +53,17 @@ constexpr float kLazyMax = 8.0f;         // log2 headroom before the max is rais
 
 typedef __attribute__((address_space(3))) void* lds_ptr_a;
 
-// 16 bytes per lane from base + voff + soff to LDS at lds_dst + 16 * lane: a
-// buffer load with the lds modifier; offsets at or past num_records load
-// zeros.  The descriptor (untyped, 32-bit data format) is built from
-// wave-uniform values, so it lives in scalar registers.
-__device__ __forceinline__ void attn_dma16(const void* base, int num_records, uint32_t voff, int soff,
-                                           char* lds_dst) {
+// 16 bytes per lane from base + voff to LDS at lds_dst + 16 * lane: a buffer
+// load with the lds modifier; a per-lane offset voff at or past num_records
+// loads zeros.  The range check covers the vector offset only (a scalar
+// offset is added after it, unchecked), so a key block's advance goes into
+// the descriptor's base and record count, never into the scalar offset.  The
+// descriptor (untyped, 32-bit data format) is built from wave-uniform values,
+// so it lives in scalar registers.
+__device__ __forceinline__ void attn_dma16(const char* base, int num_records, uint32_t voff, char* lds_dst) {
   const __amdgpu_buffer_rsrc_t r =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, num_records, 0x00020000);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_a)lds_dst, 16, voff, soff, 0, 0);
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, num_records, 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_a)lds_dst, 16, voff, 0, 0, 0);
 }
 
 // Position of key j (0..15 within its 16-key group) in the permuted Vt row:
@@ -187,12 +189,12 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
   }
 
   // ---- DMA sources.  Wave instruction i fills the 1 KiB LDS block
-  // WAVES*i + wave.  K: 1024/K_ROWB rows per block.  Buffer loads: a
-  // descriptor per operand (scalar registers) whose record count ends at the
-  // last key row of this head, one 32-bit per-lane offset, and the block's
-  // advance as the scalar offset.  Rows past Tk in the last block lie past
-  // the record count and load as zeros (their scores are masked, their P is
-  // 0).
+  // WAVES*i + wave.  K: 1024/K_ROWB rows per block.  Buffer loads: per key
+  // block a descriptor (scalar registers) whose base is the block's first
+  // key row and whose record count ends at the last key row of this head,
+  // and one fixed 32-bit per-lane offset within the block.  Rows past Tk in
+  // the last block then lie past the record count and load as zeros (their
+  // scores are masked, their P is 0); no load leaves the operand.
   constexpr int K_ROWS_PER = 1024 / K_ROWB;      // 4 (dh 128) or 8 (dh 64)
   constexpr int K_CH = K_ROWB / 16;               // 16-byte chunks per row
   const int k_records = (int)((int64_t)(Tk - 1) * k_rs * 2 + DH * 2);
@@ -229,17 +231,24 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
   const int nb = kb1 > kb0 ? kb1 - kb0 : 0;
   // a key range that fits the K / V rings is loaded whole before the first block
   const int pre = __builtin_amdgcn_readfirstlane(nb <= RING ? 1 : 0);
+  // byte advance per key block; every issued block kb < nblocks_all starts at
+  // or before key row Tk - 1 (Vt: column Tk_pad - 64), so the remaining
+  // record count kb_records - kb * step stays positive
   const int k_step = (int)(kAttnKB * k_rs * 2);
   const int v_step = VROW ? (int)(kAttnKB * v_ld * 2) : kAttnKB * 2;
   auto issue_k = [&](int kb, int buf) {
     char* Ks = Ks0 + buf * K_BYTES;
+    const char* base = reinterpret_cast<const char*>(Kh) + (int64_t)kb * k_step;
+    const int rec = k_records - kb * k_step;
 #pragma unroll
-    for (int i = 0; i < K_DMA; ++i) attn_dma16(Kh, k_records, k_voff[i], kb * k_step, Ks + (WAVES * i + wave) * 1024);
+    for (int i = 0; i < K_DMA; ++i) attn_dma16(base, rec, k_voff[i], Ks + (WAVES * i + wave) * 1024);
   };
   auto issue_v = [&](int kb, int buf) {
     char* Vs = Vs0 + buf * V_BYTES;
+    const char* base = reinterpret_cast<const char*>(Vh) + (int64_t)kb * v_step;
+    const int rec = v_records - kb * v_step;
 #pragma unroll
-    for (int i = 0; i < V_DMA; ++i) attn_dma16(Vh, v_records, v_voff[i], kb * v_step, Vs + (WAVES * i + wave) * 1024);
+    for (int i = 0; i < V_DMA; ++i) attn_dma16(base, rec, v_voff[i], Vs + (WAVES * i + wave) * 1024);
   };
 
   // Loop-invariant fragment-read offsets; ring buffer, 32-row sub-block and
@@ -779,8 +788,12 @@ extern "C" int ltx_flash_attn_v_bf16(const void* Q, int64_t q_rs, const void* K,
 
 extern "C" int64_t ltx_attn_splitkv_workspace_bytes(int64_t Tq, int64_t H, int64_t head_dim, int64_t splits) {
   if (Tq < 0 || H <= 0 || head_dim <= 0 || splits <= 0) return -1;
-  const int64_t rows = splits * Tq * H;
-  return rows * head_dim * 4 + 2 * ((rows * 4 + 255) / 256 * 256);
+  // -1 for sizes whose byte count does not fit an int64 (no wrapped result)
+  int64_t rows = 0, obytes = 0, total = 0;
+  if (__builtin_mul_overflow(splits, Tq, &rows) || __builtin_mul_overflow(rows, H, &rows)) return -1;
+  if (rows > (INT64_MAX / 16) || __builtin_mul_overflow(rows, head_dim * 4, &obytes)) return -1;
+  if (__builtin_add_overflow(obytes, 2 * ((rows * 4 + 255) / 256 * 256), &total)) return -1;
+  return total;
 }
 
 template <bool VROW>
@@ -850,7 +863,9 @@ extern "C" int ltx_flash_attn_splitkv_v_bf16(const void* Q, int64_t q_rs, const 
 // combine reads it, so nothing has to start at zero; calls that overlap on one
 // GPU share the array and race.  The host never passes `scratch` itself to a
 // kernel: its name is a host-side stand-in, and the device address comes from
-// hipGetSymbolAddress, resolved once per device with that device current.
+// hipGetSymbolAddress, resolved once per device with that device current, on
+// the first call on that device: that first call must be made outside HIP
+// graph capture; later calls enqueue only the two kernels and can be captured.
 static __device__ __align__(256) unsigned char scratch[LTX_ATTN_NOALLOC_SCRATCH_BYTES];
 
 namespace {
@@ -884,11 +899,15 @@ extern "C" int ltx_flash_attn_splitkv_noalloc_bf16(const void* Q, int64_t q_rs, 
                                                    int64_t H, int64_t head_dim, float scale, int64_t splits,
                                                    void* stream) {
   if (splits < 1 || splits > 256) return LTX_ERR_INVALID_ARG;
+  // the operands are validated before the scratch need is computed from them
+  int st = attn_check(Q, q_rs, K, k_rs, O, o_rs, gate, gate_rs, Tq, Tk, H, head_dim, scale);
+  if (st == LTX_OK) st = attn_check_vt(Vt, tk_pad, Tk);
+  if (st != LTX_OK) return st;
   const int64_t need = ltx_attn_splitkv_workspace_bytes(Tq, H, head_dim, splits);
   if (need < 0) return LTX_ERR_INVALID_ARG;
   if (need > LTX_ATTN_NOALLOC_SCRATCH_BYTES) return LTX_ERR_SCRATCH_LIMIT;
   void* ws = nullptr;
-  const int st = scratch_on_stream_device((hipStream_t)stream, &ws);
+  st = scratch_on_stream_device((hipStream_t)stream, &ws);
   if (st != LTX_OK) return st;
   return ltx_flash_attn_splitkv_bf16(Q, q_rs, K, k_rs, Vt, tk_pad, O, o_rs, gate, gate_rs, Tq, Tk, H,
                                      head_dim, scale, splits, ws, LTX_ATTN_NOALLOC_SCRATCH_BYTES, stream);

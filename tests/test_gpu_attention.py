@@ -162,3 +162,36 @@ def test_maybe_steel_attention_reference_api():
     assert max_rel_err(got.numpy(), ref.numpy()) <= 1e-2
     assert maybe_steel_attention(q, k, v, mask=torch.zeros(1, device=DEV)) is None
     assert maybe_steel_attention(q.float(), k.float(), v.float()) is None
+
+
+@pytest.mark.parametrize("tq,tk,H,dh,splits", [
+    (3456, 68, 32, 64, 1),    # audio -> video: the whole key range loaded before the first block
+    (3456, 121, 32, 64, 1),   # audio -> video at 768x512x121
+    (68, 68, 32, 64, 1),      # audio self-attention
+    (300, 1000, 4, 128, 1),   # key rings cycled, ragged last block
+    (68, 1000, 32, 64, 4),    # split-KV, ragged last range
+    (121, 121, 32, 64, 2),    # split-KV, each range loaded whole
+    (68, 3456 + 17, 32, 64, 16),
+])
+def test_rows_past_tk_never_read(tq, tk, H, dh, splits):
+    """K and V are row views of one allocation whose rows past Tk hold NaN
+    (at least one whole key block of them).  Rows of the last key block past
+    Tk must load as zeros, never from the rows behind them: the output is
+    finite and equals, bit for bit, both the Vt form and the same call on
+    NaN-free contiguous copies of K and V."""
+    from ltx_amd.kernels import attention as A
+
+    rng = np.random.default_rng(tq + 5 * tk + splits)
+    D = H * dh
+    q = _t(_bf(rng, (tq, D), 2.0))
+    buf = _t(_bf(rng, (tk + 64 + 11, 2 * D + 16)))
+    buf[tk:] = float("nan")
+    k, v = buf[:tk, D:2 * D], buf[:tk, :D]
+    g = _t(bf16r(rng.uniform(0, 2, (tq, H)).astype(np.float32)))
+    a = A.flash_attention(q, k, v, H, gate=g, splits=splits)
+    b = A.flash_attention(q, k, None, H, vt=A.transpose_v(v, H), gate=g, splits=splits)
+    c = A.flash_attention(q, k.contiguous(), v.contiguous(), H, gate=g, splits=splits)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(a.float()).all()), "rows past Tk were read"
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert torch.equal(a.view(torch.int16), c.view(torch.int16))

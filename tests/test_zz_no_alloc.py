@@ -69,7 +69,7 @@ def test_noalloc_split_kv_refuses_requests_above_the_scratch_limit():
     q, k, v, gate = _inputs(tq, 64, H, dh, 3)  # only pointers are passed; nothing runs
     out = torch.empty_like(q)
     status = _lib.lib().ltx_flash_attn_splitkv_noalloc_bf16(
-        q.data_ptr(), H * dh, k.data_ptr(), H * dh, v.data_ptr(), 64, out.data_ptr(), H * dh, gate.data_ptr(), H,
+        q.data_ptr(), H * dh, k.data_ptr(), H * dh, v.data_ptr(), tk, out.data_ptr(), H * dh, gate.data_ptr(), H,
         tq, tk, H, dh, 1.0 / math.sqrt(dh), splits, _lib.stream_of(q))
     assert status == _lib.ERR_SCRATCH_LIMIT
     assert "scratch" in _lib.lib().ltx_status_string(status).decode()
@@ -77,3 +77,33 @@ def test_noalloc_split_kv_refuses_requests_above_the_scratch_limit():
     assert _lib.lib().ltx_flash_attn_splitkv_noalloc_bf16(
         q.data_ptr(), H * dh, k.data_ptr(), H * dh, v.data_ptr(), 64, out.data_ptr(), H * dh, gate.data_ptr(), H,
         8, 64, H, dh, 1.0 / math.sqrt(dh), 0, _lib.stream_of(q)) == -1
+
+
+def test_noalloc_split_kv_replays_from_a_graph():
+    """Once the first call on the device has resolved the scratch address
+    (outside capture), the entry point enqueues only its two kernels: a HIP
+    graph holding it replays bit-identically to the workspace entry point,
+    with eager work between the replays reusing the same scratch."""
+    from ltx_amd import _lib
+    from ltx_amd.kernels import attention as A
+
+    tq, tk, H, dh, splits = 68, 3456, 32, 64, 16
+    ref, _ = _run_pair(tq, tk, H, dh, splits, 4)  # resolves the address outside capture
+    q, k, v, gate = _inputs(tq, tk, H, dh, 4)
+    vt = A.transpose_v(v, H)
+    tkp = vt.shape[-1]
+    out = torch.full((tq, H * dh), float("nan"), dtype=torch.bfloat16, device=DEV)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    print("no-alloc split-KV under graph capture", flush=True)
+    with torch.cuda.graph(graph):
+        _lib.call("ltx_flash_attn_splitkv_noalloc_bf16", q.data_ptr(), H * dh, k.data_ptr(), H * dh,
+                  vt.data_ptr(), tkp, out.data_ptr(), H * dh, gate.data_ptr(), H, tq, tk, H, dh,
+                  1.0 / math.sqrt(dh), splits, _lib.stream_of(q))
+    for i in range(3):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"replay {i}"
+        # eager work on the same scratch between replays (another problem size)
+        _run_pair(121, 6144, 32, 64, 16, 10 + i)
