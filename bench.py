@@ -20,17 +20,29 @@ Prints ONE JSON line.  Besides ms/step and tokens/s it carries:
                 ``traffic`` = HBM bytes per launch from the rocprofv3
                 FETCH_SIZE / WRITE_SIZE summary committed in profiles/ for
                 this kernel and weight format (null when none matches);
-  gemm_step     every GEMM launch of eager steps (queued behind graph
-                replays) timed with stream events around the launch, per
-                stream: flops / summed launch time (the audio stream's
-                launches overlap the video stream's, so their times include
-                sharing the chip; the host needs longer than the device to
-                enqueue an eager step, so these include host gaps);
-                ff_up_mfma_pct is the roofline kernel alone;
+  gemm_classes  the step's GEMMs by class (video QKV + gate, the two 4096 x
+                4096 output projections, FF down, text query, A2V query and
+                output, V2A key/value on the video tokens, the text contexts'
+                key/value, the audio stream's few-row GEMMs), each class timed
+                in one of the eight timed step graphs by the same device
+                clock stamps as the roofline kernel: launches, average us,
+                algorithmic flops / launch time and its fraction of the bf16
+                MFMA peak (the audio stream's and the contexts' launches run
+                beside the video stream's, sharing the chip);
+  attention     the flash-attention calls of the block alone (video self at
+                3456 and 6144 tokens, the 3456 x 256 text cross-attention,
+                A2V 3456 x 68 and split-KV V2A 68 x 3456), each replayed from
+                a HIP graph: us, TFLOP/s and fraction of the bf16 peak
+                (4 Tq Tk H dh flops);
+  video_only    the same 48-block step with the audio modality disabled (no
+                audio stream, no A2V / V2A), same box, graph replay, and
+                av_minus_video_ms = the headline minus it: what the audio
+                stream costs the step;
   gemm_shapes   the block's projection shapes at M=3456 (Q/K/V/out 4096x4096
-                x4, FF up 4096->16384, FF down 16384->4096) in int8 W8A16 and
-                MXFP8, each launch replayed from a HIP graph: ms, TFLOP/s and
-                fraction of the bf16 MFMA peak (the MFMAs are bf16);
+                x4, FF up 4096->16384, FF down 16384->4096) in int8 W8A16,
+                MXFP8 and bf16 weights (the library's automatic kernel
+                choice), each launch replayed from a HIP graph: ms, TFLOP/s
+                and fraction of the bf16 MFMA peak (the MFMAs are bf16);
   fused_ops     HBM GB/s of the row kernels (AdaLN, gated add, QK-norm +
                 RoPE) at the reference's test shape (T=14640, C=4096), at the
                 step's 3456 video rows (768x512x65) and at 1296 rows
@@ -90,6 +102,10 @@ def parse_args(argv=None):
     ap.add_argument("--no-fused-bench", action="store_true")
     ap.add_argument("--no-clip-768x512x121", action="store_true", help="skip the 768x512x121 leg")
     ap.add_argument("--no-gemm-shapes", action="store_true", help="skip the per-shape GEMM leg")
+    ap.add_argument("--no-attention-leg", action="store_true", help="skip the attention-call leg")
+    ap.add_argument("--no-video-only", action="store_true", help="skip the video-only step leg")
+    ap.add_argument("--no-class-stamps", action="store_true",
+                    help="stamp only the FF-up launches in the timed graphs (no per-class GEMM timing)")
     ap.add_argument("--cpu-runs", type=int, default=5, help="timed oracle block runs after one warmup")
     ap.add_argument("--counter-workload", choices=["ff-up", "ff-up-vs-library", "copy", "fused-ops", "attention"],
                     default=None,
@@ -315,11 +331,10 @@ def cpu_baseline(tv: int, ta: int, s: int, layers: int, grid, runs: int = 5):
 
 def gemm_step_profile(run_step, steps, tv, torch, prefill=None):
     """Time every GEMM launch of ``steps`` eager steps with events recorded on
-    its own stream around the launch.  ``prefill`` (graph replays of the step)
-    is queued first, so the device is still busy while the host enqueues the
-    eager steps: the events then bracket back-to-back kernels, as in the
-    replays, rather than gaps left by the host.  Returns (FF-up launch
-    durations in ms, per-stream summary, host enqueue ms per eager step)."""
+    its own stream around the launch (the ``--no-graph`` fallback: the events
+    include host gaps whenever the host enqueues slower than the device
+    runs).  ``prefill`` is queued first.  Returns (FF-up launch durations in
+    ms, per-stream summary, host enqueue ms per eager step)."""
     from ltx_amd.kernels import gemm
 
     recs = []
@@ -368,21 +383,59 @@ def gemm_step_profile(run_step, steps, tv, torch, prefill=None):
     return ff_up, summary, host_ms
 
 
+# GEMM classes of the step, by launch shape (kind, M, N, K, epilogue) at
+# 4096-wide video and 2048-wide audio streams
+def gemm_class(info, tv: int, ta: int, s: int):
+    from ltx_amd.kernels import gemm
+
+    _, m, n, k, epi = info
+    resid = epi in (gemm.EPI_RESIDUAL, gemm.EPI_RESIDUAL_ROUND)
+    if m == tv:
+        if k == 4096 and n == 16384:
+            return "ff_up"
+        if k == 16384:
+            return "ff_down"
+        if k == 4096 and n == 3 * 4096 + 32:
+            return "qkv"
+        if k == 4096 and n == 4096:
+            return "out" if resid else "v2a_kv"
+        if k == 4096 and n == 4096 + 32:
+            return "text_q"
+        if k == 4096 and n == 2048 + 32:
+            return "a2v_q"
+        if k == 2048 and n == 4096:
+            return "a2v_out"
+        return None
+    if m == ta:
+        return "audio"
+    if m == s:
+        return "context_kv"
+    return None
+
+
+# which classes besides FF up the step graph k carries stamps for: one group
+# per graph, so each timed graph holds few extra stamp kernels
+GEMM_CLASS_GRAPHS = (("qkv",), ("out",), ("ff_down",), ("text_q", "context_kv"), ("a2v_q", "a2v_out"),
+                     ("v2a_kv",), ("audio",), ())
+VIDEO_STREAM_CLASSES = ("ff_up", "ff_down", "qkv", "out", "text_q", "a2v_q", "a2v_out")
+
+
 class LaunchStamps:
     """Device clock stamps around chosen GEMM launches inside captured HIP
-    graphs.  While ``capturing(k)`` is active, every launch chosen by
-    ``select(info)`` gets a stamp kernel (ltx_device_clock_stamp) right before
-    and right after it on its stream, writing into slot range k; each replay
-    of that graph overwrites the range, so after the timed replays it holds
-    the last replay of every graph.  The counter's rate comes from two stamps
-    around a host sleep."""
+    graphs.  While ``capturing(k)`` is active, every launch for which
+    ``select(info, k)`` returns a label gets a stamp kernel
+    (ltx_device_clock_stamp) right before and right after it on its stream,
+    writing into slot range k; each replay of that graph overwrites the range,
+    so after the timed replays it holds the last replay of every graph.  The
+    counter's rate comes from two stamps around a host sleep."""
 
-    CAP = 128  # stamped launches per graph
+    CAP = 1024  # stamped launches per graph
 
     def __init__(self, torch, graphs: int, select, device: str = "cuda"):
         self.torch, self.select = torch, select
         self.slots = torch.zeros((graphs, 2 * self.CAP), dtype=torch.int64, device=device)
         self.count = [0] * graphs
+        self.labels = [[] for _ in range(graphs)]
         self.k, self.on = None, False
 
     def _stamp(self, addr):
@@ -393,10 +446,12 @@ class LaunchStamps:
     def hook(self, phase, info):
         k = self.k
         if phase == "pre":
-            self.on = bool(self.select(info))
+            label = self.select(info, k)
+            self.on = label is not None
             if self.on:
                 if self.count[k] >= self.CAP:
                     raise RuntimeError("too many stamped launches in one graph")
+                self.labels[k].append((label, info))
                 self._stamp(self.slots[k].data_ptr() + 16 * self.count[k])
         elif self.on:
             self._stamp(self.slots[k].data_ptr() + 16 * self.count[k] + 8)
@@ -436,19 +491,55 @@ class LaunchStamps:
         v = r.tolist()
         return (v[1] - v[0]) / ((t1 - t0) * 1e3)
 
-    def durations_ms(self, rate=None) -> list:
+    def durations_ms(self, rate=None, label=None) -> list:
+        """Stamped launch durations (ms), all or those of one label."""
+        return [d for lab, _, d in self.records(rate) if label is None or lab == label]
+
+    def records(self, rate=None) -> list:
+        """(label, launch info, duration ms) of every stamped launch."""
         rate = self.ticks_per_ms() if rate is None else rate
         v = self.slots.tolist()
         out = []
         for k, n in enumerate(self.count):
-            out += [(v[k][2 * i + 1] - v[k][2 * i]) / rate for i in range(n)]
+            out += [(self.labels[k][i][0], self.labels[k][i][1], (v[k][2 * i + 1] - v[k][2 * i]) / rate)
+                    for i in range(n)]
         return out
 
 
-def gemm_shapes(torch, fmt: str, m: int = 3456) -> dict:
+def gemm_class_summary(records) -> dict:
+    """Per GEMM class: launches, average us, algorithmic TFLOP/s and fraction
+    of the bf16 peak over the stamped launches; ``video_stream`` combines
+    the video-stream classes (flops over summed durations of one launch of
+    each kind per block, i.e. weighted by how often the step runs them)."""
+    acc = {}
+    for label, (_, m, n, k, _), ms in records:
+        a = acc.setdefault(label, [0, 0.0, 0.0])
+        a[0] += 1
+        a[1] += 2.0 * m * n * k
+        a[2] += ms
+    res = {}
+    for label, (cnt, fl, ms) in sorted(acc.items()):
+        res[label] = {"launches": cnt, "avg_us": round(ms / cnt * 1e3, 1),
+                      "gflop_per_launch": round(fl / cnt / 1e9, 2),
+                      "tflops": round(fl / (ms * 1e-3) / 1e12, 1),
+                      "frac_bf16_peak": round(fl / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+    per_block = {"ff_up": 1, "ff_down": 1, "qkv": 1, "out": 2, "text_q": 1, "a2v_q": 1, "a2v_out": 1}
+    if all(c in res for c in per_block):
+        fl = sum(res[c]["gflop_per_launch"] * per_block[c] for c in per_block)
+        us = sum(res[c]["avg_us"] * per_block[c] for c in per_block)
+        res["video_stream"] = {"us_per_block": round(us, 1), "gflop_per_block": round(fl, 1),
+                               "tflops": round(fl / us * 1e3, 1),
+                               "frac_bf16_peak": round(fl / us * 1e3 / PEAK_BF16_TFLOPS, 4)}
+    return res
+
+
+def gemm_shapes(torch, fmt: str, m: int = 3456, tile=None) -> dict:
     """The block's projection GEMMs at M rows in one weight format: each shape
-    launched 10 times from a HIP graph, best of three replays."""
+    launched 10 times from a HIP graph, best of three replays.  ``tile``
+    forces a kernel (gemm.TILE_*) instead of the automatic choice."""
     from ltx_amd.kernels import gemm
+
+    tile = gemm.TILE_AUTO if tile is None else tile
 
     g = torch.Generator(device="cuda").manual_seed(0)
     shapes = (("qkv_out_4096x4096", 4096, 4096, 4), ("ff_up_4096x16384", 4096, 16384, 1),
@@ -459,13 +550,13 @@ def gemm_shapes(torch, fmt: str, m: int = 3456) -> dict:
         w = (torch.randn((n, k), generator=g, device="cuda") * 0.02).bfloat16()
         wt = gemm.make_weight(w, torch.zeros(n, device="cuda"), kind=fmt)
         out = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
-        gemm.linear(x, wt, out=out)
+        gemm.linear(x, wt, out=out, tile=tile)
         torch.cuda.synchronize()
         iters = 10
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             for _ in range(iters):
-                gemm.linear(x, wt, out=out)
+                gemm.linear(x, wt, out=out, tile=tile)
         graph.replay()
         torch.cuda.synchronize()
         best = float("inf")
@@ -486,6 +577,89 @@ def gemm_shapes(torch, fmt: str, m: int = 3456) -> dict:
                           "tflops": round(tot_fl / (tot_ms * 1e-3) / 1e12, 1),
                           "frac_bf16_peak": round(tot_fl / (tot_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
     return res
+
+
+def attention_leg(torch, replays: int = 20) -> dict:
+    """The block's flash-attention calls alone, gated, 32 heads: video self at
+    3456 and 6144 tokens (dh 128), the 3456 x 256 text cross-attention, A2V
+    (3456 queries over 68 audio keys, dh 64) and V2A (68 over 3456, split-KV
+    as dispatched).  Each call replayed ``replays`` times from a HIP graph,
+    best of three replays."""
+    from ltx_amd.kernels.attention import flash_attention
+
+    g = torch.Generator(device="cuda").manual_seed(0)
+    res = {}
+    for name, tq, tk, dh in (("self_3456", 3456, 3456, 128), ("self_6144", 6144, 6144, 128),
+                             ("text_3456x256", 3456, 256, 128), ("a2v_3456x68", 3456, 68, 64),
+                             ("v2a_68x3456", 68, 3456, 64)):
+        d = 32 * dh
+        q = torch.randn((tq, d), generator=g, device="cuda").bfloat16()
+        k = torch.randn((tk, d), generator=g, device="cuda").bfloat16()
+        v = torch.randn((tk, d), generator=g, device="cuda").bfloat16()
+        gate = (torch.rand((tq, 32), generator=g, device="cuda") * 2).bfloat16()
+        out = torch.empty((tq, d), dtype=torch.bfloat16, device="cuda")
+        flash_attention(q, k, v, 32, gate=gate, out=out)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(replays):
+                flash_attention(q, k, v, 32, gate=gate, out=out)
+        graph.replay()
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(3):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            graph.replay()
+            b.record()
+            torch.cuda.synchronize()
+            best = min(best, a.elapsed_time(b) / replays)
+        fl = 4.0 * tq * tk * d
+        res[name] = {"us": round(best * 1e3, 1), "tflops": round(fl / (best * 1e-3) / 1e12, 1),
+                     "frac_bf16_peak": round(fl / (best * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                     "gflop": round(fl / 1e9, 2)}
+        del graph, q, k, v, gate, out
+    return res
+
+
+def video_only_leg(args, torch, s: int, steps_timed: int = 16) -> dict:
+    """The same 48-block step with the audio modality disabled: no audio
+    stream, no A2V / V2A sub-layers, video text cross-attention and FF
+    unchanged; the eight distilled steps as HIP graphs, one warm-up pass of
+    each, then ``steps_timed`` steps."""
+    from ltx_amd.model.transformer.model import LTXModel
+    from ltx_amd.pipeline import DenoiseState, denoise_step
+
+    model = LTXModel(num_layers=args.layers, weight_format=args.weights, seed=0, audio=False)
+    st = DenoiseState(model, args.height, args.width, args.frames, text_tokens=s, seed=0)
+    pes = model.rope(st.video_positions, None)
+    nsig = len(st.sigmas) - 1
+    denoise_step(model, st, 0, pes)
+    torch.cuda.synchronize()
+    pool = torch.cuda.graph_pool_handle()
+    graphs = []
+    for i in range(nsig):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, pool=pool):
+            denoise_step(model, st, i, pes)
+        graphs.append(g)
+    for _ in range(2):
+        for i in range(nsig):
+            graphs[i].replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps_timed):
+        graphs[i % nsig].replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / steps_timed * 1e3
+    tv = st.video_tokens
+    fl = step_flops(tv, 0, s, args.layers)
+    del graphs, model, st
+    torch.cuda.empty_cache()
+    return {"ms_per_step": round(ms, 3), "steps": steps_timed, "timing": "hip-graph replay",
+            "workload": f"{args.layers}-block video-only denoise step at {args.width}x{args.height}x{args.frames}",
+            "video_tokens": tv, "text_tokens": s, "step_tflop": round(fl / 1e12, 2),
+            "step_tflops_achieved": round(fl / (ms * 1e-3) / 1e12, 1)}
 
 
 def clip_768x512x121_leg(model, torch, steps_timed: int = 16) -> dict:
@@ -672,8 +846,15 @@ def main(argv=None):
 
     # the dominant kernel's launches (video FF up) get device clock stamps
     # inside the captured step graphs, so its duration is read from the timed
-    # replays themselves
-    stamps = LaunchStamps(torch, nsig, lambda info: info[4] == _gemm.EPI_GELU and info[1] == tv and info[3] == 4096)
+    # replays themselves; graph k also stamps the GEMM classes of
+    # GEMM_CLASS_GRAPHS[k]
+    def select(info, k):
+        c = gemm_class(info, tv, ta, s)
+        if c == "ff_up" or (not args.no_class_stamps and c in GEMM_CLASS_GRAPHS[k % len(GEMM_CLASS_GRAPHS)]):
+            return c
+        return None
+
+    stamps = LaunchStamps(torch, nsig, select)
     if not args.no_graph:
         graphs = []
         pool = torch.cuda.graph_pool_handle()
@@ -695,22 +876,16 @@ def main(argv=None):
     wall = time.perf_counter() - t_start
     ms = wall / args.steps * 1e3
 
-    # dominant kernel (FF up-projection GEMM): its stamps in the last timed
-    # replay of each step graph (eager: stream events, below)
-    durs = stamps.durations_ms() if graphs else []
-
-    # every GEMM, timed with stream events in eager steps queued behind graph
-    # replays
-    def prefill():
-        for i in range(2):
-            do(i)
-
-    durs_eager, gemm_step, host_ms = gemm_step_profile(run_step, args.kernel_steps, tv, torch, prefill=prefill)
-    gemm_step["host_enqueue_ms_per_eager_step"] = round(host_ms, 1)
-    gemm_step["ff_up_us_eager_events"] = round(sum(durs_eager) / len(durs_eager) * 1e3, 1)
+    # dominant kernel (FF up-projection GEMM) and the GEMM classes: their
+    # stamps in the last timed replay of each step graph (eager: stream
+    # events, below)
+    records = stamps.records() if graphs else []
+    durs = [d for lab, _, d in records if lab == "ff_up"]
     timing = "device clock stamps around each launch in the timed HIP-graph replays (last replay of each step graph)"
+    gemm_classes = gemm_class_summary(records) if records else None
     if not durs:
-        durs, timing = durs_eager, "stream events around each launch in eager steps"
+        durs, _, _ = gemm_step_profile(run_step, args.kernel_steps, tv, torch)
+        timing = "stream events around each launch in eager steps"
     k_ms = sum(durs) / len(durs)
     k_flop = 2.0 * tv * 4096 * 16384
     achieved = k_flop / (k_ms * 1e-3) / 1e12
@@ -736,10 +911,11 @@ def main(argv=None):
         "tokens_per_s": round((tv + ta) / (ms * 1e-3), 1),
         "step_tflop": round(flops / 1e12, 2), "step_tflops_achieved": round(flops / (ms * 1e-3) / 1e12, 1),
         "ff_up_mfma_pct": round(100 * achieved / PEAK_BF16_TFLOPS, 1),
-        "gemm_mfma_pct_step": round(100 * gemm_step["all"]["frac_bf16_peak"], 1),
         "roofline": roofline,
-        "gemm_step": gemm_step,
+        "gemm_classes": gemm_classes,
     }
+    if gemm_classes and "video_stream" in gemm_classes:
+        out["video_stream_gemm_mfma_pct"] = round(100 * gemm_classes["video_stream"]["frac_bf16_peak"], 1)
     del graphs
     if not args.no_clip_768x512x121 and args.layers == 48:
         print("# 768x512x121: 48-block MXFP8 step graphs", file=sys.stderr, flush=True)
@@ -748,12 +924,19 @@ def main(argv=None):
         out["guided_step"] = guided_step_ms(model, args, ta, s)
     del model, state
     torch.cuda.empty_cache()
+    if not args.no_video_only and ta:
+        print("# video-only step graphs", file=sys.stderr, flush=True)
+        out["video_only"] = video_only_leg(args, torch, s)
+        out["av_minus_video_ms"] = round(ms - out["video_only"]["ms_per_step"], 3)
+    if not args.no_attention_leg:
+        print("# attention calls", file=sys.stderr, flush=True)
+        out["attention"] = attention_leg(torch)
     if not args.no_gemm_shapes:
         print("# one block (bf16): video and AV", file=sys.stderr, flush=True)
         out["per_block"] = per_block_leg(torch, args, ta, s)
     if not args.no_gemm_shapes:
         print("# projection GEMM shapes at M=3456", file=sys.stderr, flush=True)
-        out["gemm_shapes"] = {fmt: gemm_shapes(torch, fmt) for fmt in ("int8", "mxfp8")}
+        out["gemm_shapes"] = {fmt: gemm_shapes(torch, fmt) for fmt in ("int8", "mxfp8", "bf16")}
     if not args.no_fused_bench:
         print("# fused ops", file=sys.stderr, flush=True)
         out["fused_ops"] = fused_op_bandwidth(torch)

@@ -60,7 +60,7 @@ def test_launch_stamps_pair_the_chosen_launches():
     per-graph slot ranges, and turns stamp pairs into durations."""
     import torch
 
-    st = bench.LaunchStamps(torch, 2, lambda info: info[0] == "ff_up", device="cpu")
+    st = bench.LaunchStamps(torch, 2, lambda info, k: "ff_up" if info[0] == "ff_up" else None, device="cpu")
     written = []
 
     def fake_stamp(addr):  # records the slot a stamp kernel would write
@@ -83,3 +83,32 @@ def test_launch_stamps_pair_the_chosen_launches():
     assert written == [base + k * row + o for k in range(2) for o in (0, 8, 16, 24)]
     d = st.durations_ms(rate=1000.0)  # 1000 ticks per ms
     assert d == [1.0, 1.0, 1.0, 1.0]
+    assert [lab for lab, _, _ in st.records(rate=1000.0)] == ["ff_up"] * 4
+
+
+def test_gemm_classes_of_the_step_shapes():
+    """Every GEMM shape of the 768x512x65 AV block maps to its class, and the
+    per-class summary is flops over stamped durations."""
+    from ltx_amd.kernels import gemm
+
+    tv, ta, s = 3456, 68, 256
+    B, R, G = gemm.EPI_BIAS, gemm.EPI_RESIDUAL, gemm.EPI_GELU
+    cases = {("mxfp8", tv, 16384, 4096, G): "ff_up", ("mxfp8", tv, 4096, 16384, R): "ff_down",
+             ("mxfp8", tv, 3 * 4096 + 32, 4096, B): "qkv", ("mxfp8", tv, 4096, 4096, R): "out",
+             ("mxfp8", tv, 4096, 4096, B): "v2a_kv", ("mxfp8", tv, 4096 + 32, 4096, B): "text_q",
+             ("mxfp8", tv, 2048 + 32, 4096, B): "a2v_q", ("mxfp8", tv, 4096, 2048, R): "a2v_out",
+             ("mxfp8", ta, 3 * 2048 + 32, 2048, B): "audio", ("mxfp8", s, 8192, 4096, B): "context_kv"}
+    for info, want in cases.items():
+        assert bench.gemm_class(info, tv, ta, s) == want, info
+    # each class is stamped in exactly one step graph (FF up in all of them)
+    stamped = [c for group in bench.GEMM_CLASS_GRAPHS for c in group]
+    assert len(stamped) == len(set(stamped)) and set(stamped) | {"ff_up"} == set(cases.values())
+    recs = [(c, info, 0.5) for info, c in cases.items() if c in bench.VIDEO_STREAM_CLASSES]
+    summ = bench.gemm_class_summary(recs + [("ff_up", ("mxfp8", tv, 16384, 4096, G), 0.25)])
+    fl = 2.0 * tv * 16384 * 4096
+    assert summ["ff_up"]["launches"] == 2 and summ["ff_up"]["avg_us"] == 375.0
+    assert summ["ff_up"]["tflops"] == pytest.approx(2 * fl / 0.75e-3 / 1e12, abs=0.1)
+    vs = summ["video_stream"]
+    # one launch of each class per block, two of the 4096 x 4096 output projections
+    assert vs["us_per_block"] == pytest.approx(375.0 + 500.0 * 5 + 2 * 500.0, abs=0.1)
+    assert vs["frac_bf16_peak"] == pytest.approx(vs["tflops"] / bench.PEAK_BF16_TFLOPS, abs=1e-3)
