@@ -818,9 +818,8 @@ __device__ __forceinline__ void buffer_dma16(const void* base, int num_records, 
       __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, num_records, kBufferRsrcWord3);
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds_dst, 16, voff, soff, 0, 0);
 }
-// the automatic tile choice uses the 8-wave kernel for MXFP8 weights (int8
-// stays on the 4-wave kernel, whose once-per-workgroup dequantisation costs
-// less VALU than int8's per-fragment conversion)
+// the automatic tile choice uses the 8-wave kernel for 8-bit weights (MXFP8
+// and int8) on problems of at least 100 256x256 tiles
 constexpr int kG8Stages = 3;
 
 template <int BKIND, int kG8Stages_ = 3>
@@ -1037,16 +1036,18 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
       o[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, sc, false));
       o[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, sc, true));
     } else {
-      const float nb = -128.0f * sc;
-      const uint32_t ws[2] = {w0 ^ 0x80808080u, w1 ^ 0x80808080u};
+      // bf16(fp32(q * s)): each signed byte converted by one sign-extending
+      // byte-select conversion, one fp32 product (a single rounding), then
+      // two values per bf16 conversion
+      const uint32_t ws[2] = {w0, w1};
 #pragma unroll
       for (int d = 0; d < 2; ++d) {
         const uint32_t u = ws[d];
         bf16x2 p0, p1;
-        p0[0] = (bf16)fmaf((float)(u & 0xffu), sc, nb);
-        p0[1] = (bf16)fmaf((float)((u >> 8) & 0xffu), sc, nb);
-        p1[0] = (bf16)fmaf((float)((u >> 16) & 0xffu), sc, nb);
-        p1[1] = (bf16)fmaf((float)(u >> 24), sc, nb);
+        p0[0] = (bf16)((float)(int8_t)u * sc);
+        p0[1] = (bf16)((float)(int8_t)(u >> 8) * sc);
+        p1[0] = (bf16)((float)(int8_t)(u >> 16) * sc);
+        p1[1] = (bf16)((float)((int32_t)u >> 24) * sc);
         o[2 * d] = __builtin_bit_cast(uint32_t, p0);
         o[2 * d + 1] = __builtin_bit_cast(uint32_t, p1);
       }
@@ -1303,13 +1304,15 @@ template <int BKIND, int EPI>
 static int launch_epi(const GemmArgs& p, int tile, hipStream_t s) {
   if (tile == 0) {
     // Large tiles when they still give most CUs a tile; 128x128 otherwise.
-    // MXFP8 takes the 8-wave kernel from 100 tiles of 256x256: the A2V query
-    // projection (3456 x 4096 -> 2048, 112 tiles) runs in 76 instead of 86 us
-    // alone, and the step gains 0.6-0.7 ms (the CUs its single round leaves
-    // free take the audio stream's work).  (256x128 tiles, 14 % faster on
-    // that projection alone, were 0.25 ms slower per step: explicit only.)
+    // 8-bit weights take the 8-wave kernel from 100 tiles of 256x256: the A2V
+    // query projection (3456 x 4096 -> 2048, 112 tiles) runs in 76 instead of
+    // 86 us alone, and the step gains 0.6-0.7 ms (the CUs its single round
+    // leaves free take the audio stream's work).  (256x128 tiles, 14 % faster
+    // on that projection alone, were 0.25 ms slower per step: explicit only.)
+    // int8 measured faster there than on the 4-wave kernel on every block
+    // shape (4096^2 109 vs 134 us, FF up 428 vs 472, FF down 405 vs 435).
     const int64_t big = (int64_t)((p.M + 255) / 256) * ((p.N + 255) / 256);
-    const bool g8 = BKIND == B_MXFP8 && g8_ok<BKIND>(p);
+    const bool g8 = (BKIND == B_MXFP8 || BKIND == B_INT8) && g8_ok<BKIND>(p);
     tile = big >= 160 ? (g8 ? 5 : 1) : (big >= 100 && g8 ? 5 : 2);
   }
   if (tile == 5) {
