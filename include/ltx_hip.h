@@ -272,6 +272,22 @@ int ltx_gemm_mxfp8_bf16(const void* A, int64_t lda, const uint8_t* Wq, int64_t l
                         const void* residual, int64_t ldr, const float* gate, int64_t sigmoid_from,
                         void* stream);
 
+/* MXFP8 activations x MXFP8 weights on the gfx950 scaled fp8 MFMA
+ * (v_mfma_scale_f32_32x32x64_f8f6f4), an opt-in path.  No counterpart in the
+ * reference: its MXFP8 weights (loader/transformer_cache.py:177-193) are
+ * dequantised and multiplied with bf16 activations, as ltx_gemm_mxfp8_bf16
+ * does; here the activations are quantised too (E4M3 codes (M, K), row stride
+ * lda bytes, E8M0 scales (M, K/32), row stride ld_ascale -- the layout
+ * ltx_quantize_mxfp8_bf16 writes for any rows), so results differ from the
+ * bf16-activation path by the activations' E4M3 rounding.  W / w_scale as in
+ * ltx_gemm_mxfp8_bf16; same epilogue codes and LTX_GEMM_ROUND_THEN_BIAS.
+ * Needs K % 512 == 0, N % 8 == 0, 16-byte aligned pointers and byte strides. */
+int ltx_gemm_mx_bf16(const uint8_t* A, int64_t lda, const uint8_t* a_scale, int64_t ld_ascale,
+                     const uint8_t* Wq, int64_t ldw, const uint8_t* w_scale, int64_t ld_scale,
+                     const float* bias, void* C, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                     int epilogue, const void* residual, int64_t ldr, const float* gate,
+                     int64_t sigmoid_from, void* stream);
+
 /* Split-K forms of the three GEMMs for few-row products (the 68-token audio
  * stream, 256-token contexts): `splits` blocks per 128x128 output tile each
  * accumulate K / splits of the product into an fp32 partial tile in

@@ -49,7 +49,10 @@
 
 namespace ltx {
 
-enum BKind { B_BF16 = 0, B_INT8 = 1, B_MXFP8 = 2 };
+// B_MX: MXFP8 weights and MXFP8 activations (E4M3 codes + E8M0 scale per 32
+// along K on both operands), multiplied by the scaled fp8 MFMA -- an opt-in
+// path with quantised activations, only on the 8-wave kernel.
+enum BKind { B_BF16 = 0, B_INT8 = 1, B_MXFP8 = 2, B_MX = 3 };
 // How stage tiles reach LDS: LDS DMA (global_load_lds), or global loads into
 // registers one stage ahead that are written to LDS during the next stage.
 enum Loader { LOAD_DMA = 0, LOAD_REG = 1 };
@@ -70,6 +73,8 @@ struct GemmArgs {
   int sig_from;        // columns n >= sig_from get the 2*sigmoid head-gate epilogue
   int round_then_bias; // bias added to the bf16-rounded product (quantised-linear form)
   float* partial;      // split-K: fp32 partial products [split][M][ldc], no epilogue
+  const uint8_t* ascale;  // B_MX: activation E8M0 scales (M, K/32)
+  int64_t ld_ascale;      // B_MX: their row stride (bytes)
   int M, N, K;         // split-K: K is the per-split depth
   int tiles_m, tiles_n;
 };
@@ -824,6 +829,7 @@ constexpr int kG8Stages = 3;
 
 template <int BKIND, int kG8Stages_ = 3>
 struct G8Cfg {
+  static constexpr bool MX = BKIND == B_MX;
   static constexpr int BM = 256, BN = 256, BK = 64;
   // 128x64 wave tiles: each weight fragment is dequantised by the two waves
   // that share its columns rather than four (64x128 tiles read fewer LDS
@@ -832,7 +838,8 @@ struct G8Cfg {
   static constexpr int WM = 128, WN = 64;
   static constexpr int TM = WM / 32, TN = WN / 32;
   static constexpr int WAVES_M = BM / WM;
-  static constexpr int A_ROWB = BK * 2, B_ROWB = BK;  // bf16 activations, 8-bit codes
+  // bf16 activations (MX: 8-bit codes like the weights), 8-bit weight codes
+  static constexpr int A_ROWB = MX ? BK : BK * 2, B_ROWB = BK;
   static constexpr int A_BYTES = BM * A_ROWB, B_BYTES = BN * B_ROWB;
   static constexpr int STAGE = A_BYTES + B_BYTES;
   // LDS: the three A stages, then the three B stages (every fragment read is
@@ -844,10 +851,18 @@ struct G8Cfg {
   static constexpr int EPI_BYTES = 8 * EPI_WAVE;
   static constexpr int LDS_BYTES = (kG8Stages * STAGE > EPI_BYTES) ? kG8Stages * STAGE : EPI_BYTES;
   static constexpr int COL_BYTES = 2 * BN * 4;
-  // MXFP8 scales of eight stages (256 rows x 16 E8M0 bytes), double buffered
+  // MXFP8 scales of eight stages (256 rows x 16 E8M0 bytes), double buffered;
+  // MX: the weights' then the activations' octets
   static constexpr int SC_OCT = BN * 16;
-  static constexpr int SC_BYTES = BKIND == B_MXFP8 ? 2 * SC_OCT : 0;
-  static_assert(LDS_BYTES + COL_BYTES + SC_BYTES <= 160 * 1024, "LDS");
+  static constexpr int SC_BYTES = BKIND == B_MXFP8 ? 2 * SC_OCT : (MX ? 4 * SC_OCT : 0);
+  // column values at LDS_BYTES; the scale octets after them, or (MX) right
+  // after the stages, inside the epilogue's staging area (dead by then: every
+  // scale load has landed before the epilogue's first barrier)
+  static constexpr int COL_OFF = LDS_BYTES;
+  static constexpr int SC_OFF = MX ? kG8Stages * STAGE : LDS_BYTES + COL_BYTES;
+  static constexpr int TOTAL = MX ? LDS_BYTES + COL_BYTES : LDS_BYTES + COL_BYTES + SC_BYTES;
+  static_assert(!MX || SC_OFF + SC_BYTES <= LDS_BYTES, "MX scales inside the staging area");
+  static_assert(TOTAL <= 160 * 1024, "LDS");
   static_assert(BKIND != B_BF16, "8-bit weights only");
 };
 
@@ -870,7 +885,8 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   constexpr int A_DMA = Cfg::A_DMA, B_DMA = Cfg::B_DMA;
   constexpr int EPI_ROWB = Cfg::EPI_ROWB, EPI_WAVE = Cfg::EPI_WAVE;
   constexpr bool RESID = EPI == LTX_GEMM_EPI_RESIDUAL || EPI == LTX_GEMM_EPI_RESIDUAL_ROUND;
-  __shared__ __attribute__((aligned(1024))) char lds[Cfg::LDS_BYTES + Cfg::COL_BYTES + Cfg::SC_BYTES];
+  constexpr bool MX = Cfg::MX;
+  __shared__ __attribute__((aligned(1024))) char lds[Cfg::TOTAL];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -892,7 +908,7 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   // mask whose tests cost vector instructions in every cluster)
   const int live = __builtin_amdgcn_readfirstlane((m0 + wm * WM < p.M && n0 + wn * WN < p.N) ? 1 : 0);
 
-  float* col_lds = reinterpret_cast<float*>(lds + Cfg::LDS_BYTES);
+  float* col_lds = reinterpret_cast<float*>(lds + Cfg::COL_OFF);
 
   // ---- direct-load sources.  A wave instruction fills one contiguous 1 KiB
   // block of LDS, lane j its 16-byte slot j; the lane's source address picks
@@ -906,15 +922,24 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   // -- no vector instructions per load (vector instructions of one wave take
   // matrix-pipe slots from the other).  The descriptors' record counts bound
   // every load to its operand (g8_ok checks the 32-bit extents).
-  const int a_records = (int)((int64_t)p.M * p.lda * 2), b_records = (int)((int64_t)p.N * p.ldb);
+  const int a_records = (int)((int64_t)p.M * p.lda * (MX ? 1 : 2)), b_records = (int)((int64_t)p.N * p.ldb);
   uint32_t a_src[A_DMA];
 #pragma unroll
   for (int d = 0; d < A_DMA; ++d) {
-    const int r = 8 * (8 * d + wave) + (lane >> 3);
-    int gm = m0 + r;
-    gm = gm < p.M ? gm : p.M - 1;
-    const int chunk = (lane & 7) ^ ((r >> 1) & 7);
-    a_src[d] = (uint32_t)((int64_t)gm * p.lda * 2) + chunk * 16;
+    if constexpr (MX) {
+      // activation codes: 64-byte rows laid out like the weight codes
+      const int r = 16 * (8 * d + wave) + (lane >> 2);
+      int gm = m0 + r;
+      gm = gm < p.M ? gm : p.M - 1;
+      const int chunk = (lane & 3) ^ ((r >> 2) & 3);
+      a_src[d] = (uint32_t)((int64_t)gm * p.lda) + chunk * 16;
+    } else {
+      const int r = 8 * (8 * d + wave) + (lane >> 3);
+      int gm = m0 + r;
+      gm = gm < p.M ? gm : p.M - 1;
+      const int chunk = (lane & 7) ^ ((r >> 1) & 7);
+      a_src[d] = (uint32_t)((int64_t)gm * p.lda * 2) + chunk * 16;
+    }
   }
   uint32_t b_src[B_DMA];
 #pragma unroll
@@ -930,7 +955,7 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
     char* Bs = lds + B_REGION + buf * B_BYTES;
 #pragma unroll
     for (int d = 0; d < A_DMA; ++d)
-      buffer_dma16(p.A, a_records, a_src[d], kt * (Cfg::BK * 2), As + (8 * d + wave) * 1024);
+      buffer_dma16(p.A, a_records, a_src[d], kt * Cfg::A_ROWB, As + (8 * d + wave) * 1024);
 #pragma unroll
     for (int d = 0; d < B_DMA; ++d)
       buffer_dma16(p.B, b_records, b_src[d], kt * Cfg::BK, Bs + (8 * d + wave) * 1024);
@@ -953,6 +978,10 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
 #pragma unroll
   for (int pp = 0; pp < 2; ++pp)
     b_base[pp] = B_REGION + (wn * WN + fr) * B_ROWB + (((2 * pp + h) ^ b_swz) * 16);
+  // MX: activation code fragments, read like the weight codes
+  int a_mx[2];
+#pragma unroll
+  for (int pp = 0; pp < 2; ++pp) a_mx[pp] = (wm * WM + fr) * A_ROWB + (((2 * pp + h) ^ b_swz) * 16);
   // MXFP8 scales reach LDS by direct loads too, eight stages at a time: the
   // loop then holds no register-destined global load, whose first use would
   // make the compiler wait for every load in flight (its wait counting does
@@ -960,22 +989,33 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   // bytes (the E8M0 of k-blocks 16o..16o+15, i.e. stages 8o..8o+7), laid out
   // [row][16]; waves 0-3 each move 64 rows per octet.  int8: the row scale
   // in a register.
-  char* const sc_lds = lds + Cfg::LDS_BYTES + Cfg::COL_BYTES;
-  const int sc_records = BKIND == B_MXFP8 ? (int)((int64_t)p.N * p.ld_scale) : 0;
-  const int sc_read = Cfg::LDS_BYTES + Cfg::COL_BYTES + (wn * WN + fr) * 16;
+  // MX: group 0 moves the weights' octets, group 1 the activations' (256
+  // activation rows x 16 bytes, after the weights' two octet buffers).
+  char* const sc_lds = lds + Cfg::SC_OFF;
+  constexpr bool SCALED = BKIND == B_MXFP8 || MX;
+  const int sc_records = SCALED ? (int)((int64_t)p.N * p.ld_scale) : 0;
+  const int asc_records = MX ? (int)((int64_t)p.M * p.ld_ascale) : 0;
+  const int sc_read = Cfg::SC_OFF + (wn * WN + fr) * 16;
+  const int asc_read = Cfg::SC_OFF + 2 * Cfg::SC_OCT + (wm * WM + fr) * 16;
   uint32_t sc_src = 0;
-  {
+  if (grp == 0 || !MX) {
     int gn = n0 + (wave & 3) * 64 + lane;
     gn = gn < p.N ? gn : p.N - 1;
     sc_src = (uint32_t)((int64_t)gn * p.ld_scale);
+  } else {
+    int gm = m0 + (wave & 3) * 64 + lane;
+    gm = gm < p.M ? gm : p.M - 1;
+    sc_src = (uint32_t)((int64_t)gm * p.ld_ascale);
   }
   const int noct = KT >> 3;
   auto dma_scales = [&](int oct) {
-    if constexpr (BKIND == B_MXFP8) {
-      if (grp == 0) {
-        oct = oct < noct ? oct : noct - 1;  // past the end: re-read the last octet
+    if constexpr (SCALED) {
+      oct = oct < noct ? oct : noct - 1;  // past the end: re-read the last octet
+      if (grp == 0)
         buffer_dma16(p.bscale, sc_records, sc_src, oct * 16, sc_lds + (oct & 1) * Cfg::SC_OCT + wave * 1024);
-      }
+      else if (MX)
+        buffer_dma16(p.ascale, asc_records, sc_src, oct * 16,
+                     sc_lds + (2 + (oct & 1)) * Cfg::SC_OCT + (wave & 3) * 1024);
     }
   };
   float s_i8[TN];
@@ -990,32 +1030,49 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   // loads of stage kt+2, plus (group 0, MXFP8) the scales in the first stage
   // of an octet
   constexpr int VM_DMA = A_DMA + B_DMA;
-  constexpr int VM_SCALES = BKIND == B_MXFP8 ? 1 : 0;
+  constexpr int VM_SCALES = SCALED ? 1 : 0;
 
-  bf16x8 fa[4][TM];  // A fragments of the stage's four k-steps
+  bf16x8 fa[MX ? 1 : 4][TM];  // A fragments of the stage's four k-steps
   u32x4 fb[2][TN];   // weight codes of the stage's two k-step pairs (16 per lane)
+  u32x4 fa8[2][MX ? TM : 1];  // MX: activation codes, as the weight codes
+  uint32_t sca[MX ? TM : 1];  // MX: this stage pair's E8M0 bytes of the lane's activation rows
   // fragment reads of stage kt, which sits in buffer BUF (compile-time)
   auto read_stage = [&](int kt, auto bufc) __attribute__((always_inline)) {
     constexpr int BUF = decltype(bufc)::value;
-    if constexpr (BKIND == B_MXFP8) {
+    if constexpr (SCALED) {
       const int sa = sc_read + ((kt >> 3) & 1) * Cfg::SC_OCT + ((kt & 7) >> 1) * 4;
 #pragma unroll
       for (int j = 0; j < TN; ++j) scw[j] = *reinterpret_cast<const uint32_t*>(lds + sa + j * 32 * 16);
     }
+    if constexpr (MX) {
+      const int sa = asc_read + ((kt >> 3) & 1) * Cfg::SC_OCT + ((kt & 7) >> 1) * 4;
 #pragma unroll
-    for (int pp = 0; pp < 2; ++pp) {
+      for (int i = 0; i < TM; ++i) sca[i] = *reinterpret_cast<const uint32_t*>(lds + sa + i * 32 * 16);
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
-        fb[pp][j] = *reinterpret_cast<const u32x4*>(lds + b_base[pp] + BUF * B_BYTES + j * 32 * B_ROWB);
+      for (int pp = 0; pp < 2; ++pp) {
 #pragma unroll
-      for (int s = 0; s < 2; ++s)
+        for (int j = 0; j < TN; ++j)
+          fb[pp][j] = *reinterpret_cast<const u32x4*>(lds + b_base[pp] + BUF * B_BYTES + j * 32 * B_ROWB);
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-          const int* base = BUF == 0 ? a_lo : a_hi;
-          constexpr int rel = (BUF == 0 ? 0 : BUF - 1) * A_BYTES;
-          fa[2 * pp + s][i] =
-              *reinterpret_cast<const bf16x8*>(lds + base[2 * pp + s] + rel + i * 32 * A_ROWB);
-        }
+        for (int i = 0; i < TM; ++i)
+          fa8[pp][i] = *reinterpret_cast<const u32x4*>(lds + a_mx[pp] + BUF * A_BYTES + i * 32 * A_ROWB);
+      }
+    } else {
+#pragma unroll
+      for (int pp = 0; pp < 2; ++pp) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          fb[pp][j] = *reinterpret_cast<const u32x4*>(lds + b_base[pp] + BUF * B_BYTES + j * 32 * B_ROWB);
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+          for (int i = 0; i < TM; ++i) {
+            const int* base = BUF == 0 ? a_lo : a_hi;
+            constexpr int rel = (BUF == 0 ? 0 : BUF - 1) * A_BYTES;
+            fa[2 * pp + s][i] =
+                *reinterpret_cast<const bf16x8*>(lds + base[2 * pp + s] + rel + i * 32 * A_ROWB);
+          }
+      }
     }
   };
 
@@ -1072,8 +1129,9 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
     return dequant(fb[pp][j][2 * s], fb[pp][j][2 * s + 1], scf[pp][j]);
   };
   // end of the memory cluster of stage kt (its fragment reads have landed):
-  // the stage's scales and fragments 0 and 1
+  // the stage's scales and fragments 0 and 1 (MX: nothing to decode)
   auto prep_stage = [&](int kt) __attribute__((always_inline)) {
+    if constexpr (MX) return;
 #pragma unroll
     for (int j = 0; j < TN; ++j) decode(kt, 0, j);
     bq[0] = frag_dequant(0);
@@ -1083,14 +1141,39 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   };
   // compute cluster of stage kt: 4 k-steps x TN weight fragments x TM MFMAs.
   // Fragment f+1 (f >= 1) is dequantised while the MFMAs of fragment f run.
-  auto compute_stage = [&]() __attribute__((always_inline)) {
+  // MX: TN x TM scaled fp8 MFMAs of 64 k.  Their operand contract (probed on
+  // the device): lane (row r, half h) holds k = 16h + [0, 16) in bytes 0-15
+  // and k = 32 + 16h + [0, 16) in bytes 16-31 -- the two 16-byte code chunks
+  // h and 2 + h of the row, as read above -- and lane r + 32b carries the
+  // E8M0 scale of row r's k-block b (opsel 0: bits 0-7).  The stage's two
+  // blocks are bytes 2 (kt & 1) + b of the octet word.
+  auto compute_stage = [&](int kt) __attribute__((always_inline)) {
+    if constexpr (MX) {
+      const int sh = 16 * (kt & 1) + 8 * h;
+      int ws[TN], as[TM];
 #pragma unroll
-    for (int f = 0; f < NF; ++f) {
-      const int kk = f / TN, j = f % TN;
-      if (f >= 1 && f + 1 < NF) bq[(f + 1) & 1] = frag_dequant(f + 1);
+      for (int j = 0; j < TN; ++j) ws[j] = (int)(scw[j] >> sh);
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bq[f & 1], fa[kk][i], acc[i][j], 0, 0, 0);
+      for (int i = 0; i < TM; ++i) as[i] = (int)(sca[i] >> sh);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const i32x8 w = __builtin_bit_cast(i32x8, __builtin_shufflevector(fb[0][j], fb[1][j], 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const i32x8 a =
+              __builtin_bit_cast(i32x8, __builtin_shufflevector(fa8[0][i], fa8[1][i], 0, 1, 2, 3, 4, 5, 6, 7));
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w, a, acc[i][j], 0, 0, 0, ws[j], 0, as[i]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        const int kk = f / TN, j = f % TN;
+        if (f >= 1 && f + 1 < NF) bq[(f + 1) & 1] = frag_dequant(f + 1);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bq[f & 1], fa[kk][i], acc[i][j], 0, 0, 0);
+      }
     }
   };
 
@@ -1119,18 +1202,21 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   auto stage_iter = [&](int kt, auto bufc, auto grpc) __attribute__((always_inline)) {
     constexpr int BUF = decltype(bufc)::value;
     constexpr int GRP = decltype(grpc)::value;
-    const bool oct_start = BKIND == B_MXFP8 && (kt & 7) == 0;
-    // memory cluster
-    if (GRP == 0 && oct_start) dma_scales((kt >> 3) + 1);
+    const bool oct_start = SCALED && (kt & 7) == 0;
+    // memory cluster (MX: group 1 moves the activations' scale octets)
+    if ((GRP == 0 || MX) && oct_start) dma_scales((kt >> 3) + 1);
     dma_stage(kt + 2 < KT ? kt + 2 : KT - 1, (BUF + 2) % kG8Stages);
     if (live) read_stage(kt, bufc);
     wait_lgkmcnt0();
     if (live) prep_stage(kt);
-    if (GRP == 1) wait_vmcnt<VM_DMA>();
+    if (GRP == 1) {
+      if (MX && oct_start) wait_vmcnt<VM_DMA + VM_SCALES>();
+      else wait_vmcnt<VM_DMA>();
+    }
     barrier_nofence();
     // compute cluster
     __builtin_amdgcn_s_setprio(1);
-    if (live) compute_stage();
+    if (live) compute_stage(kt);
     __builtin_amdgcn_s_setprio(0);
     if (GRP == 0) {
       if (oct_start) wait_vmcnt<VM_DMA + VM_SCALES>();
@@ -1288,9 +1374,13 @@ template <int BKIND>
 static bool g8_ok(const GemmArgs& p) {
   if (BKIND == B_BF16) return false;
   // operand extents are 31-bit buffer record counts in the kernel
-  if ((int64_t)p.M * p.lda * 2 >= ((int64_t)1 << 31) || (int64_t)p.N * p.ldb >= ((int64_t)1 << 31) ||
-      (int64_t)p.N * p.ld_scale >= ((int64_t)1 << 31))
+  if ((int64_t)p.M * p.lda * (BKIND == B_MX ? 1 : 2) >= ((int64_t)1 << 31) ||
+      (int64_t)p.N * p.ldb >= ((int64_t)1 << 31) || (int64_t)p.N * p.ld_scale >= ((int64_t)1 << 31))
     return false;
+  if (BKIND == B_MX)
+    return p.K % 512 == 0 && p.ld_scale % 16 == 0 && ((uintptr_t)p.bscale & 15u) == 0 &&
+           p.ld_ascale % 16 == 0 && ((uintptr_t)p.ascale & 15u) == 0 &&
+           (int64_t)p.M * p.ld_ascale < ((int64_t)1 << 31);
   if (BKIND == B_MXFP8)
     return p.K % 512 == 0 && p.ld_scale % 16 == 0 && ((uintptr_t)p.bscale & 15u) == 0;
   return true;
@@ -1301,7 +1391,7 @@ static bool g8_ok(const GemmArgs& p) {
 // LDS-DMA loader (3), 256x128 register-staged (4), and the 8-wave 256x256
 // kernel for 8-bit weights (5).
 template <int BKIND, int EPI>
-static int launch_epi(const GemmArgs& p, int tile, hipStream_t s) {
+static int launch_epi_w(const GemmArgs& p, int tile, hipStream_t s) {
   if (tile == 0) {
     // Large tiles when they still give most CUs a tile; 128x128 otherwise.
     // 8-bit weights take the 8-wave kernel from 100 tiles of 256x256: the A2V
@@ -1333,6 +1423,19 @@ static int launch_epi(const GemmArgs& p, int tile, hipStream_t s) {
   else
     launch_tile<256, 256, 64, 2, BKIND, EPI, 0, LOAD_DMA>(p, s);
   return LTX_OK;
+}
+
+template <int BKIND, int EPI>
+static int launch_epi(const GemmArgs& p, int tile, hipStream_t s) {
+  if constexpr (BKIND == B_MX) {
+    // quantised activations: the 8-wave kernel only
+    if (tile != 0 && tile != 5) return LTX_ERR_UNSUPPORTED;
+    if (!g8_ok<BKIND>(p)) return LTX_ERR_UNSUPPORTED;
+    launch_g8<BKIND, EPI>(p, s);
+    return LTX_OK;
+  } else {
+    return launch_epi_w<BKIND, EPI>(p, tile, s);
+  }
 }
 
 template <int BKIND>
@@ -1497,6 +1600,8 @@ static GemmArgs make_args(const void* A, int64_t lda, const void* B, int64_t ldb
   p.sig_from = (int)(sigmoid_from < N ? (sigmoid_from < 0 ? 0 : sigmoid_from) : N);
   p.round_then_bias = 0;
   p.partial = nullptr;
+  p.ascale = nullptr;
+  p.ld_ascale = 0;
   p.M = (int)M;
   p.N = (int)N;
   p.K = (int)K;
@@ -1549,6 +1654,37 @@ extern "C" int ltx_gemm_mxfp8_bf16(const void* A, int64_t lda, const uint8_t* Wq
 }
 
 // ---- split-K entry points ------------------------------------------------------
+// MXFP8 activations x MXFP8 weights on the scaled fp8 MFMA (opt-in; no
+// counterpart in the reference, whose MXFP8 path dequantises the weights and
+// multiplies bf16 activations).  A: E4M3 codes (M, K) with row stride lda
+// bytes and E8M0 scales (M, K/32) with row stride ld_ascale, as written by
+// ltx_quantize_mxfp8_bf16 on the activation rows; W, w_scale as
+// ltx_gemm_mxfp8_bf16.  Same epilogues and quantised-linear rounding flag.
+extern "C" int ltx_gemm_mx_bf16(const uint8_t* A, int64_t lda, const uint8_t* a_scale, int64_t ld_ascale,
+                                const uint8_t* Wq, int64_t ldw, const uint8_t* w_scale, int64_t ld_scale,
+                                const float* bias, void* C, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                                int epilogue, const void* residual, int64_t ldr, const float* gate,
+                                int64_t sigmoid_from, void* stream) {
+  if (!A || !a_scale || !Wq || !w_scale || !C || M < 0 || N < 0 || K < 0) return LTX_ERR_INVALID_ARG;
+  if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 2) return LTX_ERR_UNSUPPORTED;
+  const int epi = epilogue & 0xff;
+  if (epilogue & ~(0xfff | LTX_GEMM_ROUND_THEN_BIAS)) return LTX_ERR_INVALID_ARG;
+  if (epi > LTX_GEMM_EPI_SIGMOID2) return LTX_ERR_INVALID_ARG;
+  if ((epi == LTX_GEMM_EPI_RESIDUAL || epi == LTX_GEMM_EPI_RESIDUAL_ROUND) && (!residual || !gate || ldr < N))
+    return LTX_ERR_INVALID_ARG;
+  if (lda < K || ldw < K || ldc < N || ld_ascale < K / 32 || ld_scale < K / 32) return LTX_ERR_INVALID_ARG;
+  if (K % 512 != 0 || N % 8 != 0) return LTX_ERR_UNSUPPORTED;
+  if (!al16(A) || !al16(Wq) || !al16(C) || !al16(a_scale) || !al16(w_scale) || lda % 16 || ldw % 16 ||
+      ldc % 8 || ld_ascale % 16 || ld_scale % 16 || (residual && (!al16(residual) || ldr % 8)))
+    return LTX_ERR_ALIGNMENT;
+  if (M == 0 || N == 0) return LTX_OK;
+  GemmArgs p = make_args(A, lda, Wq, ldw, w_scale, ld_scale, bias, C, ldc, M, N, K, residual, ldr, gate,
+                         sigmoid_from);
+  p.ascale = a_scale;
+  p.ld_ascale = ld_ascale;
+  return launch_kind<B_MX>(p, epilogue, (hipStream_t)stream);
+}
+
 extern "C" int64_t ltx_gemm_splitk_workspace_bytes(int64_t M, int64_t N, int64_t splits) {
   if (M < 0 || N < 0 || splits < 1) return -1;
   return splits * M * N * 4;

@@ -47,6 +47,8 @@ SIGNATURES: dict[str, list] = {
                                    _vp, _i64, _int, _vp, _i64, _vp],
     "ltx_gemm_splitk_mxfp8_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp,
                                    _i64, _vp, _i64, _int, _vp, _i64, _vp],
+    "ltx_gemm_mx_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp,
+                         _i64, _vp, _i64, _vp],
     "ltx_quantize_mxfp8_bf16": [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp],
     "ltx_dequantize_mxfp8_bf16": [_vp, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _vp],
     "ltx_quantize_w8_bf16": [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp],

@@ -14,10 +14,17 @@ evaluates right after the projection:
 * ``EPI_RESIDUAL_ROUND``  ``bf16(res + bf16(gate * bf16(x W^T + b)))`` (transformer.py:387, :484)
 * ``EPI_SIGMOID2``        ``bf16(2 * bf16(sigmoid(bf16(x W^T + b))))``, the per-head gate
                           (attention.py:563-569)
+
+Opt-in (``MX_ACTIVATIONS``, environment ``LTX_MX_ACTIVATIONS=1``): MXFP8
+weights multiply MXFP8-quantised activations on the scaled fp8 MFMA
+(:func:`linear_mx`) instead of bf16 activations.  That is not the reference's
+arithmetic -- its MXFP8 path keeps the activations in bf16 -- and the
+activations' E4M3 rounding moves outputs by a few percent of their range.
 """
 
 from __future__ import annotations
 
+import os
 from dataclasses import dataclass
 
 import torch
@@ -32,6 +39,12 @@ EPI_SIGMOID2 = _lib.GEMM_EPI_SIGMOID2
 TILE_AUTO, TILE_256, TILE_128, TILE_256_DMA, TILE_256x128, TILE_G8 = 0, 1, 2, 3, 4, 5
 
 FORMATS = ("bf16", "int8", "mxfp8")
+
+# Opt-in quantised-activation path for MXFP8 weights (see the module text):
+# products with at least this many 256x256 tiles quantise their activations
+# and run ltx_gemm_mx_bf16.
+MX_ACTIVATIONS = os.environ.get("LTX_MX_ACTIVATIONS", "0") == "1"
+MX_MIN_TILES = 100
 
 # Optional launch observer: called as hook(phase, info) with phase "pre" /
 # "post" around every GEMM launch on the launching stream (used by bench.py
@@ -152,6 +165,69 @@ def auto_splits(m: int, n: int, k: int, kind: str, max_blocks: int | None = None
     return s
 
 
+def quantize_rows_mxfp8(x: torch.Tensor, codes: torch.Tensor | None = None,
+                        scales: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """MXFP8 of the rows of x (..., K) bf16 with the library's encoder (the
+    weights' OCP rule, blocks of 32 along K): E4M3 codes (M, K) uint8 and E8M0
+    scales (M, K / 32) uint8."""
+    k = x.shape[-1]
+    if k % 32:
+        raise ValueError(f"K={k} is not a multiple of 32")
+    xv, lda = _lib.row_view(x, k)
+    m = x.numel() // k
+    if codes is None:
+        codes = torch.empty((m, k), dtype=torch.uint8, device=x.device)
+    if scales is None:
+        scales = torch.empty((m, k // 32), dtype=torch.uint8, device=x.device)
+    _lib.call("ltx_quantize_mxfp8_bf16", xv.data_ptr(), lda, m, k, codes.data_ptr(), codes.stride(0),
+              scales.data_ptr(), scales.stride(0), _lib.stream_of(x), detail=f"activations M={m} K={k}")
+    return codes, scales
+
+
+def linear_mx(codes: torch.Tensor, scales: torch.Tensor, weight: LinearWeight, *, epilogue: int = EPI_BIAS,
+              out: torch.Tensor | None = None, residual: torch.Tensor | None = None,
+              gate: torch.Tensor | None = None, sigmoid_from: int | None = None) -> torch.Tensor:
+    """``epilogue(x @ W.T + b)`` with x given as MXFP8 rows (codes (M, K),
+    scales (M, K/32), from :func:`quantize_rows_mxfp8`) and MXFP8 weights, on
+    the scaled fp8 MFMA; the weights' quantised-linear rounding is kept.
+    Returns (M, N) bf16."""
+    if weight.kind != "mxfp8":
+        raise ValueError(f"linear_mx needs MXFP8 weights, got {weight.kind!r}")
+    m, k = codes.shape
+    n = weight.out_features
+    if k != weight.in_features or scales.shape != (m, k // 32):
+        raise ValueError(f"activation codes {tuple(codes.shape)} / scales {tuple(scales.shape)} do not match "
+                         f"K={weight.in_features}")
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=codes.device)
+    ov, ldc = _lib.row_view(out, n)
+    rptr, ldr, gptr = None, 0, None
+    if epilogue in (EPI_RESIDUAL, EPI_RESIDUAL_ROUND):
+        if residual is None or gate is None:
+            raise ValueError("residual epilogues need residual and gate")
+        rv, ldr = _lib.row_view(residual, n)
+        rptr = rv.data_ptr()
+        gate = gate.reshape(-1).contiguous()
+        if gate.dtype != torch.float32 or gate.numel() != n:
+            raise ValueError("gate must be fp32 with N elements")
+        gptr = gate.data_ptr()
+    flags = epilogue
+    if weight.qlinear and weight.bias is not None:
+        flags |= _lib.GEMM_ROUND_THEN_BIAS
+    sig = n if sigmoid_from is None else int(sigmoid_from)
+    bptr = None if weight.bias is None else weight.bias.data_ptr()
+    _lib.call("ltx_gemm_mx_bf16", codes.data_ptr(), codes.stride(0), scales.data_ptr(), scales.stride(0),
+              weight.w.data_ptr(), weight.w.stride(0), weight.scale.data_ptr(), weight.scale.stride(0), bptr,
+              ov.data_ptr(), ldc, m, n, k, flags, rptr, ldr, gptr, sig, _lib.stream_of(codes),
+              detail=f"mx M={m} N={n} K={k} epi={epilogue}")
+    return out
+
+
+def _mx_eligible(m: int, n: int, k: int, weight: LinearWeight, tile: int) -> bool:
+    return (MX_ACTIVATIONS and weight.kind == "mxfp8" and tile in (TILE_AUTO, TILE_G8) and k % 512 == 0
+            and ((m + 255) // 256) * ((n + 255) // 256) >= MX_MIN_TILES)
+
+
 def linear(x: torch.Tensor, weight: LinearWeight, *, epilogue: int = EPI_BIAS,
            out: torch.Tensor | None = None, residual: torch.Tensor | None = None,
            gate: torch.Tensor | None = None, tile: int = TILE_AUTO,
@@ -204,6 +280,13 @@ def linear(x: torch.Tensor, weight: LinearWeight, *, epilogue: int = EPI_BIAS,
         splits = auto_splits(m, n, k, weight.kind) if tile in (TILE_AUTO, TILE_128) else 1
     if hook is not None:
         hook("pre", info)
+    if splits == 1 and _mx_eligible(m, n, k, weight, tile):
+        codes, scales = quantize_rows_mxfp8(x)
+        linear_mx(codes, scales, weight, epilogue=epilogue, out=ov, residual=residual, gate=gate,
+                  sigmoid_from=sigmoid_from)
+        if hook is not None:
+            hook("post", info)
+        return out
     if splits > 1:
         ws_bytes = splits * m * n * 4
         ws = torch.empty(splits * m * n, dtype=torch.float32, device=x.device)
