@@ -288,6 +288,18 @@ int ltx_gemm_mx_bf16(const uint8_t* A, int64_t lda, const uint8_t* a_scale, int6
                      int epilogue, const void* residual, int64_t ldr, const float* gate,
                      int64_t sigmoid_from, void* stream);
 
+/* The opt-in MX path's feed-forward up-projection (no counterpart in the
+ * reference): ltx_gemm_mx_bf16 with the GELU epilogue
+ * (feed_forward.py:101-102) whose bf16 result is written as MXFP8 rows --
+ * E4M3 codes (M, N) with row stride ldcq bytes and E8M0 scales (M, N/32) --
+ * exactly what ltx_quantize_mxfp8_bf16 makes of the bf16 GELU output, i.e.
+ * the down-projection's quantised input.  flags: 0 or LTX_GEMM_ROUND_THEN_BIAS.
+ * Needs N % 32 == 0 besides ltx_gemm_mx_bf16's conditions. */
+int ltx_gemm_mx_gelu_mxfp8(const uint8_t* A, int64_t lda, const uint8_t* a_scale, int64_t ld_ascale,
+                           const uint8_t* Wq, int64_t ldw, const uint8_t* w_scale, int64_t ld_scale,
+                           const float* bias, uint8_t* Cq, int64_t ldcq, uint8_t* c_scale, int64_t ld_cscale,
+                           int64_t M, int64_t N, int64_t K, int flags, void* stream);
+
 /* Split-K forms of the three GEMMs for few-row products (the 68-token audio
  * stream, 256-token contexts): `splits` blocks per 128x128 output tile each
  * accumulate K / splits of the product into an fp32 partial tile in

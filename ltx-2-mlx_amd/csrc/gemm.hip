@@ -75,6 +75,8 @@ struct GemmArgs {
   float* partial;      // split-K: fp32 partial products [split][M][ldc], no epilogue
   const uint8_t* ascale;  // B_MX: activation E8M0 scales (M, K/32)
   int64_t ld_ascale;      // B_MX: their row stride (bytes)
+  uint8_t* cscale;        // kEpiGeluMx: output E8M0 scales (M, N/32); C holds the codes
+  int64_t ld_cscale;
   int M, N, K;         // split-K: K is the per-split depth
   int tiles_m, tiles_n;
 };
@@ -83,6 +85,10 @@ constexpr int kGemmThreads = 256;
 // EPI value of the split-K pass: the accumulators go to the fp32 partial
 // buffer as they are, the epilogue runs in splitk_epilogue_kernel.
 constexpr int kEpiPartial = 16;
+// EPI value of the MX kernel's FF up-projection: the GELU epilogue whose
+// bf16 result leaves as MXFP8 rows (codes in C, E8M0 scales in cscale) --
+// the next product's quantised activations, written by this one.
+constexpr int kEpiGeluMx = 5;
 constexpr int kGroupM = 4;
 constexpr int kNumXcd = 8;
 
@@ -1283,13 +1289,13 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
           }
 #pragma unroll
           for (int e = 0; e < 4; ++e) y[e] += bias4[e];
-          if (EPI == LTX_GEMM_EPI_GELU || EPI == LTX_GEMM_EPI_SIGMOID2 || SIG) {
+          if (EPI == LTX_GEMM_EPI_GELU || EPI == kEpiGeluMx || EPI == LTX_GEMM_EPI_SIGMOID2 || SIG) {
             float r[4] = {y[0], y[1], y[2], y[3]};
             round_bf2(r[0], r[1]);
             round_bf2(r[2], r[3]);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              if (EPI == LTX_GEMM_EPI_GELU) y[e] = gelu_tanh(r[e]);
+              if (EPI == LTX_GEMM_EPI_GELU || EPI == kEpiGeluMx) y[e] = gelu_tanh(r[e]);
               if (EPI == LTX_GEMM_EPI_SIGMOID2) y[e] = sigmoid2_bf(r[e]);
               if (SIG && gn + e >= p.sig_from) y[e] = sigmoid2_bf(r[e]);
             }
@@ -1350,7 +1356,30 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
         v[e] = (bf16)o;
       }
     }
-    if (gm < p.M && col_ok) *reinterpret_cast<bf16x8*>(p.C + (int64_t)gm * p.ldc + gn2) = v;
+    if constexpr (EPI == kEpiGeluMx) {
+      // the row's 32-column block spans lanes ch & ~3 .. ch | 3 (N % 32 == 0:
+      // a block lies wholly inside or outside the output); its maximum takes
+      // two lane exchanges, then 8 codes per lane and one scale byte per block
+      float f[8], amax = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        f[e] = (float)v[e];
+        amax = fmaxf(amax, fabsf(f[e]));
+      }
+      amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+      amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+      const int X = mxfp8_block_exponent(amax);
+      const float sx = ldexpf(1.0f, X), lim = 448.0f * sx;
+      const uint32_t w0 = e4m3x4_ocp(f[0], f[1], f[2], f[3], sx, lim);
+      const uint32_t w1 = e4m3x4_ocp(f[4], f[5], f[6], f[7], sx, lim);
+      if (gm < p.M && col_ok) {
+        uint8_t* cq = reinterpret_cast<uint8_t*>(p.C);
+        *reinterpret_cast<u32x2*>(cq + (int64_t)gm * p.ldc + gn2) = u32x2{w0, w1};
+        if ((ch & 3) == 0) p.cscale[(int64_t)gm * p.ld_cscale + gn2 / 32] = (uint8_t)(X + 127);
+      }
+    } else {
+      if (gm < p.M && col_ok) *reinterpret_cast<bf16x8*>(p.C + (int64_t)gm * p.ldc + gn2) = v;
+    }
   }
 }
 
@@ -1452,6 +1481,13 @@ static int launch_kind(const GemmArgs& p, int epilogue, hipStream_t s) {
     case LTX_GEMM_EPI_RESIDUAL: st = launch_epi<BKIND, LTX_GEMM_EPI_RESIDUAL>(q, tile, s); break;
     case LTX_GEMM_EPI_RESIDUAL_ROUND: st = launch_epi<BKIND, LTX_GEMM_EPI_RESIDUAL_ROUND>(q, tile, s); break;
     case LTX_GEMM_EPI_SIGMOID2: st = launch_epi<BKIND, LTX_GEMM_EPI_SIGMOID2>(q, tile, s); break;
+    case kEpiGeluMx:
+      if constexpr (BKIND == B_MX) {
+        st = launch_epi<BKIND, kEpiGeluMx>(q, tile, s);
+        break;
+      } else {
+        return LTX_ERR_INVALID_ARG;
+      }
     default: return LTX_ERR_INVALID_ARG;
   }
   if (st != LTX_OK) return st;
@@ -1602,6 +1638,8 @@ static GemmArgs make_args(const void* A, int64_t lda, const void* B, int64_t ldb
   p.partial = nullptr;
   p.ascale = nullptr;
   p.ld_ascale = 0;
+  p.cscale = nullptr;
+  p.ld_cscale = 0;
   p.M = (int)M;
   p.N = (int)N;
   p.K = (int)K;
@@ -1683,6 +1721,34 @@ extern "C" int ltx_gemm_mx_bf16(const uint8_t* A, int64_t lda, const uint8_t* a_
   p.ascale = a_scale;
   p.ld_ascale = ld_ascale;
   return launch_kind<B_MX>(p, epilogue, (hipStream_t)stream);
+}
+
+// The MX path's feed-forward up-projection: GELU epilogue whose bf16 result
+// is written as MXFP8 rows -- codes (M, N) with row stride ldcq bytes, E8M0
+// scales (M, N/32) -- the quantised input of the down-projection, bit for bit
+// what ltx_quantize_mxfp8_bf16 makes of the bf16 GELU output.
+extern "C" int ltx_gemm_mx_gelu_mxfp8(const uint8_t* A, int64_t lda, const uint8_t* a_scale, int64_t ld_ascale,
+                                      const uint8_t* Wq, int64_t ldw, const uint8_t* w_scale, int64_t ld_scale,
+                                      const float* bias, uint8_t* Cq, int64_t ldcq, uint8_t* c_scale,
+                                      int64_t ld_cscale, int64_t M, int64_t N, int64_t K, int flags,
+                                      void* stream) {
+  if (!A || !a_scale || !Wq || !w_scale || !Cq || !c_scale || M < 0 || N < 0 || K < 0)
+    return LTX_ERR_INVALID_ARG;
+  if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 2) return LTX_ERR_UNSUPPORTED;
+  if (flags & ~LTX_GEMM_ROUND_THEN_BIAS) return LTX_ERR_INVALID_ARG;
+  if (lda < K || ldw < K || ldcq < N || ld_ascale < K / 32 || ld_scale < K / 32 || ld_cscale < N / 32)
+    return LTX_ERR_INVALID_ARG;
+  if (K % 512 != 0 || N % 32 != 0) return LTX_ERR_UNSUPPORTED;
+  if (!al16(A) || !al16(Wq) || !al16(Cq) || !al16(a_scale) || !al16(w_scale) || lda % 16 || ldw % 16 ||
+      ldcq % 8 || ld_ascale % 16 || ld_scale % 16)
+    return LTX_ERR_ALIGNMENT;
+  if (M == 0 || N == 0) return LTX_OK;
+  GemmArgs p = make_args(A, lda, Wq, ldw, w_scale, ld_scale, bias, Cq, ldcq, M, N, K, nullptr, 0, nullptr, N);
+  p.ascale = a_scale;
+  p.ld_ascale = ld_ascale;
+  p.cscale = c_scale;
+  p.ld_cscale = ld_cscale;
+  return launch_kind<B_MX>(p, kEpiGeluMx | flags, (hipStream_t)stream);
 }
 
 extern "C" int64_t ltx_gemm_splitk_workspace_bytes(int64_t M, int64_t N, int64_t splits) {

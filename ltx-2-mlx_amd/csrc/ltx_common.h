@@ -72,6 +72,33 @@ __device__ __forceinline__ float sub_rn(float a, float b) {
 // RMSNorm normalizer.
 __device__ __forceinline__ float rsqrt_rn(float v) { return __frsqrt_rn(v); }
 
+// MXFP8 (OCP MX v1.0, E4M3 elements, E8M0 block scale) encoding of four
+// values of one block whose exponent is X = floor(log2(block max)) - 8:
+// code = E4M3(v / 2^X), rounded to nearest even and saturated to +-448.
+// The hardware conversion divides by its scale operand (2^X) and rounds the
+// same way but turns values past 448 into NaN, so they are clamped to
+// +-448 * 2^X first (NaN passes the clamp and stays NaN).  Measured on the
+// device: for every finite bf16 value and every X in [-127, 127] the codes
+// equal the rule's, bit for bit.  s = 2^X, lim = 448 * s.
+__device__ __forceinline__ uint32_t e4m3x4_ocp(float v0, float v1, float v2, float v3, float s, float lim) {
+  auto cl = [lim](float v) { return fabsf(v) >= lim ? __builtin_copysignf(lim, v) : v; };
+  typedef short s16x2 __attribute__((ext_vector_type(2)));
+  s16x2 w = {0, 0};
+  w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w, cl(v0), cl(v1), s, false);
+  w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w, cl(v2), cl(v3), s, true);
+  return __builtin_bit_cast(uint32_t, w);
+}
+
+// The block exponent of the MXFP8 rule for a block maximum amax >= 0:
+// floor(log2(amax)) - 8 clamped to [-127, 127]; -127 for an all-zero block.
+__device__ __forceinline__ int mxfp8_block_exponent(float amax) {
+  if (!(amax > 0.0f)) return -127;
+  int e;
+  frexpf(amax, &e);
+  const int X = (e - 1) - 8;
+  return X < -127 ? -127 : (X > 127 ? 127 : X);
+}
+
 }  // namespace ltx
 
 // Launch-status helper shared by the C entry points.

@@ -20,66 +20,41 @@
 
 namespace ltx {
 
-__device__ __forceinline__ uint32_t e4m3_encode_sat(float v) {
-  const uint32_t sign = (__float_as_uint(v) >> 24) & 0x80u;
-  const float a = fabsf(v);
-  if (a != a) return 0x7Fu | sign;  // NaN
-  if (a >= 448.0f) return 0x7Eu | sign;
-  if (a < 0.015625f) {  // below 2^-6: subnormal steps of 2^-9 (8 -> min normal)
-    return sign | (uint32_t)rintf(a * 512.0f);
-  }
-  int e;
-  frexpf(a, &e);
-  int E = e - 1;  // a in [2^E, 2^(E+1))
-  float m = rintf(ldexpf(a, 3 - E));  // [8, 16]
-  if (m == 16.0f) {
-    E += 1;
-    m = 8.0f;
-  }
-  uint32_t code = ((uint32_t)(E + 7) << 3) | ((uint32_t)m - 8u);
-  if (code > 0x7Eu) code = 0x7Eu;
-  return sign | code;
-}
-
-// One thread per 32-element block.
-__global__ void mxfp8_quantize_kernel(const bf16* __restrict__ W, int64_t ldw, int64_t N,
-                                      int64_t K, uint8_t* __restrict__ q, int64_t ldq,
-                                      uint8_t* __restrict__ sc, int64_t lds) {
-  const int64_t nb = K / 32;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= N * nb) return;
-  const int64_t n = idx / nb, b = idx % nb;
-  const bf16* src = W + n * ldw + b * 32;
-  float v[32];
+// Rows of 32-element blocks: one wave per 512-element chunk of a row, lane l
+// holding elements 8l..8l+7 (one 16-byte load), lanes 4b..4b+3 forming block
+// b; the block maximum takes two lane exchanges, the codes leave as one
+// 8-byte store per lane (512 contiguous bytes per wave) and lane 4b writes the
+// block's scale byte.  Chunks past K (K % 512 != 0) leave their lanes idle.
+// Used for weights (at load) and for activation rows (the opt-in MX path).
+__global__ __launch_bounds__(256) void mxfp8_quantize_kernel(const bf16* __restrict__ W, int64_t ldw, int64_t N,
+                                                             int64_t K, uint8_t* __restrict__ q, int64_t ldq,
+                                                             uint8_t* __restrict__ sc, int64_t lds) {
+  const int lane = threadIdx.x & 63;
+  const int64_t chunks = (K + 511) / 512;
+  const int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (task >= N * chunks) return;  // whole waves: the exchanges below see all 64 lanes
+  const int64_t n = task / chunks;
+  const int64_t col = (task % chunks) * 512 + lane * 8;
+  const bool in = col < K;  // K % 32 == 0: a block's four lanes agree
+  float v[8];
   float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 32; i += 8) {
-    bf16x8 x = *reinterpret_cast<const bf16x8*>(src + i);
+  if (in) {
+    const bf16x8 x = *reinterpret_cast<const bf16x8*>(W + n * ldw + col);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      v[i + e] = (float)x[e];
-      amax = fmaxf(amax, fabsf(v[i + e]));
+      v[e] = (float)x[e];
+      amax = fmaxf(amax, fabsf(v[e]));
     }
   }
-  int X = -127;
-  if (amax > 0.0f) {
-    int e;
-    frexpf(amax, &e);
-    X = (e - 1) - 8;
-    X = X < -127 ? -127 : (X > 127 ? 127 : X);
-  }
-  sc[n * lds + b] = (uint8_t)(X + 127);
-  uint32_t words[8];
-#pragma unroll
-  for (int w = 0; w < 8; ++w) {
-    uint32_t word = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) word |= e4m3_encode_sat(ldexpf(v[4 * w + e], -X)) << (8 * e);
-    words[w] = word;
-  }
-  uint8_t* dst = q + n * ldq + b * 32;
-  *reinterpret_cast<u32x4*>(dst) = u32x4{words[0], words[1], words[2], words[3]};
-  *reinterpret_cast<u32x4*>(dst + 16) = u32x4{words[4], words[5], words[6], words[7]};
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+  if (!in) return;
+  const int X = mxfp8_block_exponent(amax);
+  if ((lane & 3) == 0) sc[n * lds + col / 32] = (uint8_t)(X + 127);
+  const float s = ldexpf(1.0f, X), lim = 448.0f * s;
+  const uint32_t w0 = e4m3x4_ocp(v[0], v[1], v[2], v[3], s, lim);
+  const uint32_t w1 = e4m3x4_ocp(v[4], v[5], v[6], v[7], s, lim);
+  *reinterpret_cast<u32x2*>(q + n * ldq + col) = u32x2{w0, w1};
 }
 
 __global__ void mxfp8_dequantize_kernel(const uint8_t* __restrict__ q, int64_t ldq,
@@ -213,10 +188,11 @@ extern "C" int ltx_quantize_mxfp8_bf16(const void* W, int64_t ldw, int64_t N, in
   if (!W || !q || !scales || N < 0 || K < 0) return LTX_ERR_INVALID_ARG;
   if (K % 32) return LTX_ERR_UNSUPPORTED;
   if (ldw < K || ldq < K || ld_scale < K / 32) return LTX_ERR_INVALID_ARG;
-  if (!a16(W) || !a16(q) || ldw % 8 || ldq % 16) return LTX_ERR_ALIGNMENT;
-  const int64_t total = N * (K / 32);
-  if (total == 0) return LTX_OK;
-  mxfp8_quantize_kernel<<<(int)((total + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+  if (!a16(W) || !a16(q) || ldw % 8 || ldq % 8) return LTX_ERR_ALIGNMENT;
+  const int64_t tasks = N * ((K + 511) / 512);  // one wave each, four per workgroup
+  if (tasks == 0) return LTX_OK;
+  if ((tasks + 3) / 4 > INT32_MAX) return LTX_ERR_UNSUPPORTED;
+  mxfp8_quantize_kernel<<<(int)((tasks + 3) / 4), 256, 0, (hipStream_t)stream>>>(
       (const bf16*)W, ldw, N, K, q, ldq, scales, ld_scale);
   return ltx_launch_status();
 }

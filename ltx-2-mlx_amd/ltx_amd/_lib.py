@@ -49,6 +49,8 @@ SIGNATURES: dict[str, list] = {
                                    _i64, _vp, _i64, _int, _vp, _i64, _vp],
     "ltx_gemm_mx_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp,
                          _i64, _vp, _i64, _vp],
+    "ltx_gemm_mx_gelu_mxfp8": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _i64, _i64,
+                               _i64, _int, _vp],
     "ltx_quantize_mxfp8_bf16": [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp],
     "ltx_dequantize_mxfp8_bf16": [_vp, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _vp],
     "ltx_quantize_w8_bf16": [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp],

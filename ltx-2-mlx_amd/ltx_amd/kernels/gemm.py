@@ -165,6 +165,19 @@ def auto_splits(m: int, n: int, k: int, kind: str, max_blocks: int | None = None
     return s
 
 
+@dataclass
+class MxRows:
+    """Activation rows in MXFP8: E4M3 codes (M, K) uint8 and E8M0 scales
+    (M, K/32) uint8 -- the opt-in MX path's quantised GEMM input."""
+
+    codes: torch.Tensor
+    scales: torch.Tensor
+
+    @property
+    def shape(self):
+        return self.codes.shape
+
+
 def quantize_rows_mxfp8(x: torch.Tensor, codes: torch.Tensor | None = None,
                         scales: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """MXFP8 of the rows of x (..., K) bf16 with the library's encoder (the
@@ -223,6 +236,32 @@ def linear_mx(codes: torch.Tensor, scales: torch.Tensor, weight: LinearWeight, *
     return out
 
 
+def linear_mx_gelu(x: MxRows, weight: LinearWeight) -> MxRows:
+    """The MX path's FF up-projection: ``mxfp8(bf16(gelu_tanh(bf16(x W^T + b))))``
+    with the quantisation in the GEMM's epilogue (ltx_gemm_mx_gelu_mxfp8)."""
+    if weight.kind != "mxfp8":
+        raise ValueError(f"linear_mx_gelu needs MXFP8 weights, got {weight.kind!r}")
+    m, k = x.codes.shape
+    n = weight.out_features
+    if k != weight.in_features or n % 32:
+        raise ValueError(f"K={k} / N={n} do not fit the weight {weight.out_features}x{weight.in_features}")
+    codes = torch.empty((m, n), dtype=torch.uint8, device=x.codes.device)
+    scales = torch.empty((m, n // 32), dtype=torch.uint8, device=x.codes.device)
+    flags = _lib.GEMM_ROUND_THEN_BIAS if (weight.qlinear and weight.bias is not None) else 0
+    bptr = None if weight.bias is None else weight.bias.data_ptr()
+    hook = LAUNCH_HOOK
+    info = (weight.kind, m, n, k, EPI_GELU)
+    if hook is not None:
+        hook("pre", info)
+    _lib.call("ltx_gemm_mx_gelu_mxfp8", x.codes.data_ptr(), x.codes.stride(0), x.scales.data_ptr(),
+              x.scales.stride(0), weight.w.data_ptr(), weight.w.stride(0), weight.scale.data_ptr(),
+              weight.scale.stride(0), bptr, codes.data_ptr(), n, scales.data_ptr(), n // 32, m, n, k, flags,
+              _lib.stream_of(x.codes), detail=f"mx gelu M={m} N={n} K={k}")
+    if hook is not None:
+        hook("post", info)
+    return MxRows(codes, scales)
+
+
 def _mx_eligible(m: int, n: int, k: int, weight: LinearWeight, tile: int) -> bool:
     return (MX_ACTIVATIONS and weight.kind == "mxfp8" and tile in (TILE_AUTO, TILE_G8) and k % 512 == 0
             and ((m + 255) // 256) * ((n + 255) // 256) >= MX_MIN_TILES)
@@ -243,6 +282,16 @@ def linear(x: torch.Tensor, weight: LinearWeight, *, epilogue: int = EPI_BIAS,
     """
     k = weight.in_features
     n = weight.out_features
+    if isinstance(x, MxRows):  # quantised rows of the opt-in MX path
+        hook = LAUNCH_HOOK
+        info = (weight.kind, x.codes.shape[0], n, k, epilogue)
+        if hook is not None:
+            hook("pre", info)
+        out = linear_mx(x.codes, x.scales, weight, epilogue=epilogue, out=out, residual=residual, gate=gate,
+                        sigmoid_from=sigmoid_from)
+        if hook is not None:
+            hook("post", info)
+        return out
     if x.dtype != torch.bfloat16:
         raise TypeError(f"linear expects bf16 activations, got {x.dtype}")
     xv, lda = _lib.row_view(x, k)

@@ -128,3 +128,108 @@ def test_opt_in_switch_routes_mxfp8_products(monkeypatch):
     assert torch.equal(routed.view(torch.int16), mx.view(torch.int16))
     assert not torch.equal(plain.view(torch.int16), mx.view(torch.int16))
     assert torch.equal(i8.view(torch.int16), i8_plain.view(torch.int16))
+
+
+@pytest.mark.parametrize("m,k,n", [(3456, 4096, 16384), (700, 1024, 544)])
+def test_gelu_epilogue_writes_the_quantised_rows_of_its_bf16_output(m, k, n):
+    """ltx_gemm_mx_gelu_mxfp8 (the FF up-projection writing the
+    down-projection's MXFP8 input) equals, bit for bit, the bf16 GELU
+    epilogue followed by the row quantiser."""
+    from ltx_amd.kernels import gemm
+
+    print(f"mx gelu->mxfp8 epilogue M={m} K={k} N={n}", flush=True)
+    rng = np.random.default_rng(m + n)
+    x = _t(rng.standard_normal((m, k)).astype(np.float32))
+    wt = gemm.make_weight(_t((rng.standard_normal((n, k)) * 0.02).astype(np.float32)),
+                          torch.from_numpy((rng.standard_normal(n) * 0.1).astype(np.float32)).to(DEV), kind="mxfp8")
+    xq = gemm.MxRows(*gemm.quantize_rows_mxfp8(x))
+    hb = gemm.linear_mx(xq.codes, xq.scales, wt, epilogue=gemm.EPI_GELU)
+    want = gemm.quantize_rows_mxfp8(hb)
+    got = gemm.linear_mx_gelu(xq, wt)
+    torch.cuda.synchronize()
+    assert torch.equal(got.codes, want[0]) and torch.equal(got.scales, want[1])
+
+
+def test_row_quantiser_edge_values_match_the_oracle():
+    """The row quantiser (the hardware E4M3 conversion after a clamp to
+    +-448 * 2^X) against the oracle's OCP encoder on blocks built to hit the
+    rule's corners: all-zero blocks, E4M3 subnormal outputs (elements 2^-10
+    .. 2^-17 of the block maximum), saturation (maxima just below 2^(X+9)),
+    ties between codes, negative zeros, tiny and huge block maxima."""
+    from ltx_amd.kernels import gemm
+
+    rng = np.random.default_rng(3)
+    rows, k = 64, 1024
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    b = x.reshape(rows, k // 32, 32)
+    b[0] = 0.0
+    b[1] = -0.0
+    b[2, :, 1:] = b[2, :, 1:] * np.exp2(-rng.integers(10, 18, size=(k // 32, 31)))   # subnormal codes
+    b[3, :, 0] = 511.0 * np.exp2(rng.integers(-20, 20, size=k // 32))               # saturation
+    b[4] = (np.arange(32) % 16 + 8.5)[None, :] * np.exp2(rng.integers(-3, 3, size=(k // 32, 1)))  # ties
+    b[5] *= 1e-30
+    b[6] *= 1e30
+    b[7] = np.where(rng.random((k // 32, 32)) < 0.5, -0.0, b[7])
+    x = bf16r(x)
+    codes, scales = gemm.quantize_rows_mxfp8(_t(x))
+    qc, qs = oq.mxfp8_quantize(x)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(scales.cpu().numpy(), qs)
+    np.testing.assert_array_equal(codes.cpu().numpy(), qc)
+
+
+def test_mx_path_eight_steps_four_blocks_vs_oracle(monkeypatch):
+    """The opt-in path through a whole denoise: a 4-block full-width MXFP8
+    model on a 384-token video grid with every eligible product on the
+    quantised-activation GEMM (the FF hidden rows quantised in the
+    up-projection's epilogue), against the oracle's bf16-activation
+    arithmetic, per step over the eight distilled sigmas.  The E4M3 rounding
+    of the activations is the whole difference; the per-step latent cosine is
+    gated at 0.999, as for the default path."""
+    from test_gpu_model import _model_weights
+
+    from ltx_amd.kernels import gemm
+    from ltx_amd.model.transformer.model import LTXModel
+    from ltx_amd.pipeline import DenoiseState, denoise
+    from oracle import block as ob
+    from oracle import rope as orope
+
+    monkeypatch.setattr(gemm, "MX_ACTIVATIONS", True)
+    monkeypatch.setattr(gemm, "MX_MIN_TILES", 1)
+    routed = []
+    mx_fn, gelu_fn = gemm.linear_mx, gemm.linear_mx_gelu
+
+    def count_mx(codes, *a, **kw):
+        routed.append(codes.shape[0])
+        return mx_fn(codes, *a, **kw)
+
+    def count_gelu(x, *a, **kw):
+        routed.append(x.codes.shape[0])
+        return gelu_fn(x, *a, **kw)
+
+    monkeypatch.setattr(gemm, "linear_mx", count_mx)
+    monkeypatch.setattr(gemm, "linear_mx_gelu", count_gelu)
+    print("MX path: 4-block MXFP8 model, 384 video tokens, 8 steps vs oracle", flush=True)
+    model = LTXModel(num_layers=4, weight_format="mxfp8", seed=21)
+    st = DenoiseState(model, height=256, width=384, frames=25, text_tokens=256, audio_frames=26, seed=7)
+    MW = _model_weights(model)
+    vlat, alat = st.video_latent.float().cpu(), st.audio_latent.float().cpu()
+    vctx, actx = st.video_context.float().cpu(), st.audio_context.float().cpu()
+    vpos, apos = st.video_positions, st.audio_positions
+    pes = tuple(tuple(torch.from_numpy(a) for a in p) for p in (
+        orope.rope_tables(vpos, 4096, 32, orope.VIDEO_MAX_POS),
+        orope.rope_tables(vpos[:, 0:1], 2048, 32, orope.AUDIO_MAX_POS),
+        orope.rope_tables(apos, 2048, 32, orope.AUDIO_MAX_POS),
+        orope.rope_tables(apos[:, 0:1], 2048, 32, orope.AUDIO_MAX_POS)))
+    got = []
+    denoise(model, st, callback=lambda step, s: got.append(
+        (s.video_latent.float().cpu().clone(), s.audio_latent.float().cpu().clone())))
+    # the video stream's projections took the MX path (M = 384 rows): at least
+    # QKV, out, text Q / out, A2V Q / out, V2A K|V and FF up / down per block
+    assert routed.count(384) >= 8 * 4 * 9
+    sig = st.sigmas
+    for step in range(8):
+        vlat, alat = ob.model_step(MW, vlat, alat, vctx, actx, sig[step], sig[step + 1], pes)
+        cv, ca = cos_sim(got[step][0].numpy(), vlat.numpy()), cos_sim(got[step][1].numpy(), alat.numpy())
+        print(f"MX step {step}: video cos {cv:.6f} audio cos {ca:.6f}", flush=True)
+        assert cv >= 0.999 and ca >= 0.999
