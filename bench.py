@@ -34,6 +34,10 @@ Prints ONE JSON line.  Besides ms/step and tokens/s it carries:
                 A2V 3456 x 68 and split-KV V2A 68 x 3456), each replayed from
                 a HIP graph: us, TFLOP/s and fraction of the bf16 peak
                 (4 Tq Tk H dh flops);
+  mx_opt_in     the opt-in MX path (MXFP8 activations on the scaled fp8
+                MFMA; not the reference's arithmetic): ms per step with the
+                same model, the FF-up launch in those step graphs against the
+                5 PFLOP/s fp8 peak, and the big products alone;
   video_only    the same 48-block step with the audio modality disabled (no
                 audio stream, no A2V / V2A), same box, graph replay, and
                 av_minus_video_ms = the headline minus it: what the audio
@@ -104,6 +108,7 @@ def parse_args(argv=None):
     ap.add_argument("--no-gemm-shapes", action="store_true", help="skip the per-shape GEMM leg")
     ap.add_argument("--no-attention-leg", action="store_true", help="skip the attention-call leg")
     ap.add_argument("--no-video-only", action="store_true", help="skip the video-only step leg")
+    ap.add_argument("--no-mx", action="store_true", help="skip the opt-in MXFP8-activation leg")
     ap.add_argument("--no-class-stamps", action="store_true",
                     help="stamp only the FF-up launches in the timed graphs (no per-class GEMM timing)")
     ap.add_argument("--cpu-runs", type=int, default=5, help="timed oracle block runs after one warmup")
@@ -662,6 +667,94 @@ def video_only_leg(args, torch, s: int, steps_timed: int = 16) -> dict:
             "step_tflops_achieved": round(fl / (ms * 1e-3) / 1e12, 1)}
 
 
+PEAK_FP8_TFLOPS = 5000.0
+
+
+def mx_opt_in_leg(model, state, pes, torch, tv: int, ta: int, s: int, steps_timed: int = 16) -> dict:
+    """The opt-in MX path (gemm.MX_ACTIVATIONS): the same model and step with
+    every large MXFP8 product on the scaled fp8 MFMA, activations quantised to
+    MXFP8 (the FF hidden rows by the up-projection's epilogue, the other
+    inputs by the row quantiser); eight step graphs captured anew, 16 warm-up
+    and ``steps_timed`` timed replays, FF-up launches stamped as in the
+    headline.  Plus the block's three big products alone (graph replay of 10
+    launches, best of three): quantised-input GEMM time against the 5 PFLOP/s
+    dense fp8 peak."""
+    from ltx_amd.kernels import gemm
+    from ltx_amd.pipeline import denoise_step
+
+    nsig = len(state.sigmas) - 1
+    stamps = LaunchStamps(torch, nsig, lambda info, k: "ff_up" if gemm_class(info, tv, ta, s) == "ff_up" else None)
+    gemm.MX_ACTIVATIONS = True
+    try:
+        denoise_step(model, state, 0, pes)
+        torch.cuda.synchronize()
+        pool = torch.cuda.graph_pool_handle()
+        graphs = []
+        for i in range(nsig):
+            g = torch.cuda.CUDAGraph()
+            with stamps.capturing(i), torch.cuda.graph(g, pool=pool):
+                denoise_step(model, state, i, pes)
+            graphs.append(g)
+    finally:
+        gemm.MX_ACTIVATIONS = False
+    for i in range(16):
+        graphs[i % nsig].replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps_timed):
+        graphs[i % nsig].replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / steps_timed * 1e3
+    durs = stamps.durations_ms()
+    del graphs
+    fl = 2.0 * tv * 4096 * 16384
+    k_ms = sum(durs) / len(durs)
+    res = {"ms_per_step": round(ms, 3), "steps": steps_timed, "timing": "hip-graph replay",
+           "tokens_per_s": round((tv + ta) / (ms * 1e-3), 1),
+           "ff_up_in_step": {"launch_us": round(k_ms * 1e3, 1), "launches_timed": len(durs),
+                             "tflops": round(fl / (k_ms * 1e-3) / 1e12, 1),
+                             "frac_fp8_peak": round(fl / (k_ms * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4)},
+           "arithmetic": "MXFP8 activations x MXFP8 weights (scaled fp8 MFMA); the reference keeps bf16 "
+                         "activations -- opt-in, not the parity path"}
+    g = torch.Generator(device="cuda").manual_seed(0)
+    shapes = {}
+    for name, m, k, n in (("ff_up_4096x16384", tv, 4096, 16384), ("ff_down_16384x4096", tv, 16384, 4096),
+                          ("qkv_4096x12320", tv, 4096, 3 * 4096 + 32)):
+        x = torch.randn((m, k), generator=g, device="cuda").bfloat16()
+        wt = gemm.make_weight((torch.randn((n, k), generator=g, device="cuda") * 0.02).bfloat16(),
+                              torch.zeros(n, device="cuda"), kind="mxfp8")
+        codes, scales = gemm.quantize_rows_mxfp8(x)
+        out = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+        for label, fn in (("gemm", lambda: gemm.linear_mx(codes, scales, wt, out=out)),
+                          ("row_quantiser", lambda: gemm.quantize_rows_mxfp8(x, codes, scales))):
+            fn()
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for _ in range(10):
+                    fn()
+            graph.replay()
+            torch.cuda.synchronize()
+            best = float("inf")
+            for _ in range(3):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                graph.replay()
+                b.record()
+                torch.cuda.synchronize()
+                best = min(best, a.elapsed_time(b) / 10)
+            del graph
+            if label == "gemm":
+                fl = 2.0 * m * n * k
+                shapes[name] = {"us": round(best * 1e3, 1), "tflops": round(fl / (best * 1e-3) / 1e12, 1),
+                                "frac_fp8_peak": round(fl / (best * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4)}
+            else:
+                shapes[name]["row_quantiser_us"] = round(best * 1e3, 1)
+        del x, wt, codes, scales, out
+    res["gemm_alone"] = shapes
+    return res
+
+
 def clip_768x512x121_leg(model, torch, steps_timed: int = 16) -> dict:
     """ms per step at 768x512x121: 6144 video + 121 audio + 256 text tokens,
     the eight distilled steps captured as HIP graphs, one full warmup pass,
@@ -917,6 +1010,9 @@ def main(argv=None):
     if gemm_classes and "video_stream" in gemm_classes:
         out["video_stream_gemm_mfma_pct"] = round(100 * gemm_classes["video_stream"]["frac_bf16_peak"], 1)
     del graphs
+    if args.weights == "mxfp8" and not args.no_mx:
+        print("# opt-in MX path: step graphs with MXFP8 activations", file=sys.stderr, flush=True)
+        out["mx_opt_in"] = mx_opt_in_leg(model, state, pes, torch, tv, ta, s)
     if not args.no_clip_768x512x121 and args.layers == 48:
         print("# 768x512x121: 48-block MXFP8 step graphs", file=sys.stderr, flush=True)
         out["clip_768x512x121"] = clip_768x512x121_leg(model, torch)
