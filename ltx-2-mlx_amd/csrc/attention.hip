@@ -47,6 +47,7 @@ namespace ltx {
 
 constexpr int kAttnWaves = 8;            // full-size tiles: 8 waves = 256 queries
 constexpr int kAttnSplitWaves = 4;       // split-KV tiles: 4 waves = 128 queries
+constexpr int kAttnSmallTk = 256;        // single-pass key ranges up to this take 4-wave tiles
 constexpr int kAttnKB = 64;              // keys per stage
 constexpr int kNumXcdAttn = 8;
 constexpr float kLazyMax = 8.0f;         // log2 headroom before the max is raised
@@ -154,7 +155,7 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
   // K ring (RING x K_BYTES) followed by the V ring (RING x V_BYTES): a ring of
   // 4 lets the workgroup synchronise every other key block (the split-KV
   // tiles, two workgroups per CU, keep 2)
-  constexpr int RING = SPLIT ? 2 : 4;
+  constexpr int RING = (SPLIT || WAVES == kAttnSplitWaves) ? 2 : 4;
   __shared__ __attribute__((aligned(1024))) char lds[RING * (K_BYTES + V_BYTES)];
   char* const Ks0 = lds;
   char* const Vs0 = lds + RING * K_BYTES;
@@ -746,19 +747,32 @@ static int launch_attn(const void* Q, int64_t q_rs, const void* K, int64_t k_rs,
                        void* O, int64_t o_rs, const void* gate, int64_t gate_rs, int64_t Tq, int64_t Tk,
                        int64_t H, int64_t head_dim, float scale, hipStream_t s) {
   if (Tq == 0) return LTX_OK;
-  constexpr int QT = AttnCfg<64, kAttnWaves>::QT;
+  // Short key ranges (text contexts, audio keys) leave a workgroup mostly
+  // waiting on its loads and its epilogue: 128-query workgroups with rings of
+  // two key blocks (64 KB of LDS at dh 128) put two of them on a CU, so one
+  // computes while the other waits.
+  const bool small = Tk <= kAttnSmallTk;
+  const int QT = small ? AttnCfg<64, kAttnSplitWaves>::QT : AttnCfg<64, kAttnWaves>::QT;
   const int64_t nwg = (Tq + QT - 1) / QT * H;
   if (nwg > INT32_MAX) return LTX_ERR_UNSUPPORTED;
   const float scale_log2 = scale * 1.4426950408889634f;
   const SplitOut none{nullptr, nullptr, nullptr, 1};
-#define LTX_FA(DH, G)                                                                              \
-  flash_attn_kernel<DH, G, kAttnWaves, false, VROW><<<(int)nwg, 64 * kAttnWaves, 0, s>>>(          \
+#define LTX_FA(DH, G, W)                                                                           \
+  flash_attn_kernel<DH, G, W, false, VROW><<<(int)nwg, 64 * W, 0, s>>>(                            \
       (const bf16*)Q, q_rs, (const bf16*)K, k_rs, (const bf16*)V, v_ld, (bf16*)O, o_rs,             \
       (const bf16*)gate, gate_rs, (int)Tq, (int)Tk, (int)H, scale_log2, none)
-  if (head_dim == 128) {
-    if (gate) LTX_FA(128, true); else LTX_FA(128, false);
+  if (small) {
+    if (head_dim == 128) {
+      if (gate) LTX_FA(128, true, kAttnSplitWaves); else LTX_FA(128, false, kAttnSplitWaves);
+    } else {
+      if (gate) LTX_FA(64, true, kAttnSplitWaves); else LTX_FA(64, false, kAttnSplitWaves);
+    }
   } else {
-    if (gate) LTX_FA(64, true); else LTX_FA(64, false);
+    if (head_dim == 128) {
+      if (gate) LTX_FA(128, true, kAttnWaves); else LTX_FA(128, false, kAttnWaves);
+    } else {
+      if (gate) LTX_FA(64, true, kAttnWaves); else LTX_FA(64, false, kAttnWaves);
+    }
   }
 #undef LTX_FA
   return ltx_launch_status();
