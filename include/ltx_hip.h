@@ -327,6 +327,45 @@ int ltx_gemm_splitk_mxfp8_bf16(const void* A, int64_t lda, const uint8_t* Wq, in
                                int64_t sigmoid_from, int splits, float* workspace,
                                int64_t workspace_bytes, void* stream);
 
+/* Few-row forms of the three GEMMs, in one launch: the same products as
+ * ltx_gemm_bf16 / ltx_gemm_w8a16_bf16 / ltx_gemm_mxfp8_bf16 (the reference's
+ * nn.Linear / nn.QuantizedLinear calls, attention.py:425-437,
+ * feed_forward.py:91-112, loader/transformer_cache.py:177-193) for products
+ * with few rows -- the 68- or 121-token audio stream -- which these kernels
+ * bind by their weight bytes rather than their flops.  Workgroups of 128
+ * columns x up to 128 rows each accumulate K / splits of the product into an
+ * fp32 partial tile in `workspace` (ltx_gemm_rows_workspace_bytes(M, N,
+ * splits) bytes, 16-byte aligned); the last split of each tile to finish sums
+ * the partials in split order and applies the epilogue, with the flags and
+ * rounding points of ltx_gemm_* (the fp32 sum order differs).  `counters`
+ * (ltx_gemm_rows_counter_words(M, N) uint32 words, 4-byte aligned; needed
+ * when splits > 1) must be zero on the first call and every call leaves them
+ * zero, so one zeroed array serves every later call on a stream; calls that
+ * may run at the same time need their own workspace and counters.
+ * K % (128 * splits) == 0 for 8-bit weights, K % (64 * splits) == 0 for bf16;
+ * 1 <= splits <= 64; MXFP8 scale rows 4-byte aligned with ld_scale % 4 == 0.
+ * Operand rules as for ltx_gemm_*. */
+int64_t ltx_gemm_rows_workspace_bytes(int64_t M, int64_t N, int64_t splits);
+int64_t ltx_gemm_rows_counter_words(int64_t M, int64_t N);
+int ltx_gemm_rows_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, const float* bias,
+                       void* C, int64_t ldc, int64_t M, int64_t N, int64_t K, int epilogue,
+                       const void* residual, int64_t ldr, const float* gate, int64_t sigmoid_from,
+                       int splits, float* workspace, int64_t workspace_bytes, uint32_t* counters,
+                       int64_t counter_words, void* stream);
+int ltx_gemm_rows_w8a16_bf16(const void* A, int64_t lda, const int8_t* Wq, int64_t ldw,
+                             const float* w_scale, const float* bias, void* C, int64_t ldc,
+                             int64_t M, int64_t N, int64_t K, int epilogue, const void* residual,
+                             int64_t ldr, const float* gate, int64_t sigmoid_from, int splits,
+                             float* workspace, int64_t workspace_bytes, uint32_t* counters,
+                             int64_t counter_words, void* stream);
+int ltx_gemm_rows_mxfp8_bf16(const void* A, int64_t lda, const uint8_t* Wq, int64_t ldw,
+                             const uint8_t* w_scale, int64_t ld_scale, const float* bias, void* C,
+                             int64_t ldc, int64_t M, int64_t N, int64_t K, int epilogue,
+                             const void* residual, int64_t ldr, const float* gate,
+                             int64_t sigmoid_from, int splits, float* workspace,
+                             int64_t workspace_bytes, uint32_t* counters, int64_t counter_words,
+                             void* stream);
+
 /* ---- weight formats (load-time) --------------------------------------------
  * MXFP8, OCP Microscaling v1.0 with E4M3 elements, blocks of 32 along K and an
  * E8M0 scale (the storage of loader/transformer_cache.py:1255-1267; codes (N,K)

@@ -47,6 +47,12 @@ SIGNATURES: dict[str, list] = {
                                    _vp, _i64, _int, _vp, _i64, _vp],
     "ltx_gemm_splitk_mxfp8_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp,
                                    _i64, _vp, _i64, _int, _vp, _i64, _vp],
+    "ltx_gemm_rows_bf16": [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64, _vp, _i64,
+                           _int, _vp, _i64, _vp, _i64, _vp],
+    "ltx_gemm_rows_w8a16_bf16": [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64,
+                                 _vp, _i64, _int, _vp, _i64, _vp, _i64, _vp],
+    "ltx_gemm_rows_mxfp8_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp,
+                                 _i64, _vp, _i64, _int, _vp, _i64, _vp, _i64, _vp],
     "ltx_gemm_mx_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp,
                          _i64, _vp, _i64, _vp],
     "ltx_gemm_mx_gelu_mxfp8": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _i64, _i64,
@@ -124,6 +130,10 @@ def lib() -> ctypes.CDLL:
         handle.ltx_attn_splitkv_workspace_bytes.restype = _i64
         handle.ltx_gemm_splitk_workspace_bytes.argtypes = [_i64, _i64, _i64]
         handle.ltx_gemm_splitk_workspace_bytes.restype = _i64
+        handle.ltx_gemm_rows_workspace_bytes.argtypes = [_i64, _i64, _i64]
+        handle.ltx_gemm_rows_workspace_bytes.restype = _i64
+        handle.ltx_gemm_rows_counter_words.argtypes = [_i64, _i64]
+        handle.ltx_gemm_rows_counter_words.restype = _i64
         handle.ltx_status_string.argtypes = [ctypes.c_int]
         handle.ltx_status_string.restype = ctypes.c_char_p
         _LIB = handle

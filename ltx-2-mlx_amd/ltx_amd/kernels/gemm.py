@@ -165,6 +165,126 @@ def auto_splits(m: int, n: int, k: int, kind: str, max_blocks: int | None = None
     return s
 
 
+# Few-row products (at most ROWS_MAX_M rows: the 68 / 121-token audio stream)
+# can run on the one-launch split-K kernel of ltx_gemm_rows_* with about
+# ROWS_TARGET_WGS workgroups (LTX_GEMM_ROWS=1).  Off by default: inside the
+# 48-block step, where these products run on the audio stream beside the
+# video stream's GEMMs, its workgroups (one per CU, held for the whole K
+# stream) cost the step 0.9-2.0 ms against the split-K tile kernel (two
+# workgroups per CU) in A/B runs on one box, although alone it is up to 15 %
+# faster on the larger audio products.
+ROWS_KERNEL = os.environ.get("LTX_GEMM_ROWS", "0") == "1"
+ROWS_MAX_M = int(os.environ.get("LTX_GEMM_ROWS_MAX_M", "128"))
+ROWS_TARGET_WGS = int(os.environ.get("LTX_GEMM_ROWS_WGS", "256"))
+_ROWS_COUNTER_WORDS = 1 << 14
+_rows_counters: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def rows_tiles(m: int, n: int) -> int:
+    """Output tiles of ltx_gemm_rows_* (its counter words): row tiles of 64, 96
+    or 128 rows x column tiles of 128."""
+    bm = 64 if m <= 64 else (96 if m <= 96 else 128)
+    return -(-m // bm) * -(-n // 128)
+
+
+def rows_splits(m: int, n: int, k: int, kind: str, target: int | None = None) -> int:
+    """Split count of a few-row product: the largest power of two keeping at
+    most ``target`` (default ``ROWS_TARGET_WGS``) workgroups, K divisible by
+    the split granularity and at least two K stages per split."""
+    target = ROWS_TARGET_WGS if target is None else target
+    ks = 64 if kind == "bf16" else 128
+    tiles = rows_tiles(m, n)
+    s = 1
+    while s < 64 and tiles * s * 2 <= target and k % (ks * s * 2) == 0 and k // (s * 2) >= 2 * ks:
+        s *= 2
+    return s
+
+
+def rows_eligible(m: int, n: int, k: int, kind: str) -> bool:
+    ks = 64 if kind == "bf16" else 128
+    return ROWS_KERNEL and 0 < m <= ROWS_MAX_M and k % ks == 0 and n % 8 == 0
+
+
+def _rows_counters_for(device: torch.device, stream: int, words: int) -> torch.Tensor:
+    """A zeroed counter array for the calls of one stream (every call leaves
+    it zero).  Cached per stream outside graph capture; under capture without
+    a cached array, a fresh one whose zero fill is part of the graph."""
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    buf = _rows_counters.get(key)
+    if buf is not None and buf.numel() >= words:
+        return buf
+    buf = torch.zeros(max(words, _ROWS_COUNTER_WORDS), dtype=torch.int32, device=device)
+    if not torch.cuda.is_current_stream_capturing():
+        _rows_counters[key] = buf
+    return buf
+
+
+def linear_rows(x: torch.Tensor, weight: LinearWeight, *, epilogue: int = EPI_BIAS,
+                out: torch.Tensor | None = None, residual: torch.Tensor | None = None,
+                gate: torch.Tensor | None = None, sigmoid_from: int | None = None,
+                splits: int | None = None) -> torch.Tensor:
+    """:func:`linear` for few-row x on the one-launch split-K kernel
+    (ltx_gemm_rows_*): same epilogues, same rounding points."""
+    k = weight.in_features
+    n = weight.out_features
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"linear_rows expects bf16 activations, got {x.dtype}")
+    xv, lda = _lib.row_view(x, k)
+    m = x.numel() // k
+    lead = x.shape[:-1]
+    if out is None:
+        out = torch.empty((*lead, n), dtype=torch.bfloat16, device=x.device)
+    ov, ldc = _lib.row_view(out, n)
+    if ov.data_ptr() != out.data_ptr():
+        raise ValueError("out must be a row-strided view")
+    rptr, ldr, gptr = None, 0, None
+    if epilogue in (EPI_RESIDUAL, EPI_RESIDUAL_ROUND):
+        if residual is None or gate is None:
+            raise ValueError("residual epilogues need residual and gate")
+        rv, ldr = _lib.row_view(residual, n)
+        if rv.data_ptr() != residual.data_ptr():
+            raise ValueError("residual must be a row-strided view")
+        rptr = rv.data_ptr()
+        gate = gate.reshape(-1).contiguous()
+        if gate.dtype != torch.float32 or gate.numel() != n:
+            raise ValueError("gate must be fp32 with N elements")
+        gptr = gate.data_ptr()
+    flags = epilogue
+    if weight.qlinear and weight.bias is not None:
+        flags |= _lib.GEMM_ROUND_THEN_BIAS
+    sig = n if sigmoid_from is None else int(sigmoid_from)
+    bptr = None if weight.bias is None else weight.bias.data_ptr()
+    if m == 0:
+        return out
+    s = rows_splits(m, n, k, weight.kind) if splits is None else int(splits)
+    stream = _lib.stream_of(x)
+    ws = torch.empty(s * m * n, dtype=torch.float32, device=x.device)
+    words = rows_tiles(m, n)
+    cnt = _rows_counters_for(x.device, stream, words)
+    args = (ws.data_ptr(), ws.numel() * 4, cnt.data_ptr(), cnt.numel(), stream)
+    detail = f"rows {weight.kind} M={m} N={n} K={k} epi={epilogue} splits={s}"
+    hook = LAUNCH_HOOK
+    info = (weight.kind, m, n, k, epilogue)
+    if hook is not None:
+        hook("pre", info)
+    if weight.kind == "bf16":
+        _lib.call("ltx_gemm_rows_bf16", xv.data_ptr(), lda, weight.w.data_ptr(), weight.w.stride(0), bptr,
+                  ov.data_ptr(), ldc, m, n, k, flags, rptr, ldr, gptr, sig, s, *args, detail=detail)
+    elif weight.kind == "int8":
+        _lib.call("ltx_gemm_rows_w8a16_bf16", xv.data_ptr(), lda, weight.w.data_ptr(), weight.w.stride(0),
+                  weight.scale.data_ptr(), bptr, ov.data_ptr(), ldc, m, n, k, flags, rptr, ldr, gptr, sig, s,
+                  *args, detail=detail)
+    elif weight.kind == "mxfp8":
+        _lib.call("ltx_gemm_rows_mxfp8_bf16", xv.data_ptr(), lda, weight.w.data_ptr(), weight.w.stride(0),
+                  weight.scale.data_ptr(), weight.scale.stride(0), bptr, ov.data_ptr(), ldc, m, n, k, flags, rptr,
+                  ldr, gptr, sig, s, *args, detail=detail)
+    else:
+        raise ValueError(f"unknown weight format {weight.kind!r}")
+    if hook is not None:
+        hook("post", info)
+    return out
+
+
 @dataclass
 class MxRows:
     """Activation rows in MXFP8: E4M3 codes (M, K) uint8 and E8M0 scales
@@ -279,9 +399,15 @@ def linear(x: torch.Tensor, weight: LinearWeight, *, epilogue: int = EPI_BIAS,
     gate instead (fused gate-logit columns of a Q/QKV projection).
     ``splits``: split-K factor (None: ``auto_splits`` for the 128x128 tiles,
     1: single pass); the split form sums fp32 partials from a workspace.
+    With ``ROWS_KERNEL`` set, few-row products with ``splits=None`` and the
+    automatic tile choice run on :func:`linear_rows`.
     """
     k = weight.in_features
     n = weight.out_features
+    if (splits is None and tile == TILE_AUTO and not isinstance(x, MxRows)
+            and rows_eligible(x.numel() // max(k, 1), n, k, weight.kind)):
+        return linear_rows(x, weight, epilogue=epilogue, out=out, residual=residual, gate=gate,
+                           sigmoid_from=sigmoid_from)
     if isinstance(x, MxRows):  # quantised rows of the opt-in MX path
         hook = LAUNCH_HOOK
         info = (weight.kind, x.codes.shape[0], n, k, epilogue)

@@ -34,7 +34,8 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
     # every declared symbol is bound with a signature in the ctypes layer
     bound = set(_lib.SIGNATURES) | {"ltx_status_string", "ltx_attn_vt_padded_len",
-                                     "ltx_attn_splitkv_workspace_bytes", "ltx_gemm_splitk_workspace_bytes"}
+                                     "ltx_attn_splitkv_workspace_bytes", "ltx_gemm_splitk_workspace_bytes",
+                                     "ltx_gemm_rows_workspace_bytes", "ltx_gemm_rows_counter_words"}
     assert set(declared_symbols()) <= bound, set(declared_symbols()) - bound
 
 
@@ -93,3 +94,18 @@ def test_argument_validation_without_gpu():
                                     16, 16, None) == -1
     assert lib.ltx_gemm_splitk_bf16(16, 2048, 16, 2048, None, 16, 64, 4, 64, 2048, 0, None, 0, None, 64, 3,
                                     16, 1 << 30, None) == -2
+    # few-row GEMM: workspace and counter sizes; missing counters with splits > 1,
+    # a K not divisible by 128 * splits (8-bit weights), a misaligned scale row
+    # and a bad split count rejected before any launch
+    assert lib.ltx_gemm_rows_workspace_bytes(68, 2048, 4) == 4 * 68 * 2048 * 4
+    assert lib.ltx_gemm_rows_counter_words(68, 2048) == 16
+    assert lib.ltx_gemm_rows_counter_words(121, 6176) == 49
+    assert lib.ltx_gemm_rows_counter_words(256, 4096) == 64
+    assert lib.ltx_gemm_rows_bf16(16, 2048, 16, 2048, None, 16, 2048, 68, 2048, 2048, 0, None, 0, None, 2048, 4,
+                                  16, 1 << 30, None, 0, None) == -1
+    assert lib.ltx_gemm_rows_mxfp8_bf16(16, 2048, 16, 2048, 16, 64, None, 16, 2048, 68, 2048, 2048, 0, None, 0,
+                                        None, 2048, 32, 16, 1 << 30, 16, 1 << 10, None) == -2
+    assert lib.ltx_gemm_rows_mxfp8_bf16(16, 2048, 16, 2048, 16, 66, None, 16, 2048, 68, 2048, 2048, 0, None, 0,
+                                        None, 2048, 4, 16, 1 << 30, 16, 1 << 10, None) == -4
+    assert lib.ltx_gemm_rows_w8a16_bf16(16, 2048, 16, 2048, 16, None, 16, 2048, 68, 2048, 2048, 0, None, 0,
+                                        None, 2048, 65, 16, 1 << 30, 16, 1 << 10, None) == -1
