@@ -248,6 +248,10 @@ int ltx_broadcast_add_f32(const float* table, const float* vec, float* out, int6
  * K % 512 == 0 and 16-byte aligned scale rows), else LTX_ERR_UNSUPPORTED.
  * The default for MXFP8 weights when 256x256 tiles are chosen. */
 #define LTX_GEMM_TILE_G8 (5 << 8)
+/* The eight-wave kernel with 128 x 256 tiles (8-bit weights, same conditions
+ * as LTX_GEMM_TILE_G8), for products whose 256 x 256 tiles fill only part of
+ * one round; never the automatic choice. */
+#define LTX_GEMM_TILE_G8_128 (6 << 8)
 /* OR-ed into `epilogue`: the bias is added to the bf16-rounded product,
  * acc' = bf16(acc) + bias, before the epilogue's own steps -- the
  * quantised-linear form `quantized_matmul(x, w) + bias` of nn.QuantizedLinear

@@ -746,15 +746,17 @@ constexpr int kG8Threads = 512;
 // and int8) on problems of at least 100 256x256 tiles
 constexpr int kG8Stages = 3;
 
-template <int BKIND, int kG8Stages_ = 3>
+template <int BKIND, int BM_ = 256, int kG8Stages_ = 3>
 struct G8Cfg {
   static constexpr bool MX = BKIND == B_MX;
-  static constexpr int BM = 256, BN = 256, BK = 64;
+  static constexpr int BM = BM_, BN = 256, BK = 64;
   // 128x64 wave tiles: each weight fragment is dequantised by the two waves
   // that share its columns rather than four (64x128 tiles read fewer LDS
   // bytes per MFMA, but MXFP8 measured 2.5 % slower with them: the
-  // conversions cost more power than the extra fragment reads)
-  static constexpr int WM = 128, WN = 64;
+  // conversions cost more power than the extra fragment reads).  Tiles of
+  // 128 rows (BM_ = 128: 64x64 wave tiles) for products whose 256-row tiles
+  // fill only part of one round.
+  static constexpr int WM = BM / 2, WN = 64;
   static constexpr int TM = WM / 32, TN = WN / 32;
   static constexpr int WAVES_M = BM / WM;
   // bf16 activations (MX: 8-bit codes like the weights), 8-bit weight codes
@@ -783,11 +785,12 @@ struct G8Cfg {
   static_assert(!MX || SC_OFF + SC_BYTES <= LDS_BYTES, "MX scales inside the staging area");
   static_assert(TOTAL <= 160 * 1024, "LDS");
   static_assert(BKIND != B_BF16, "8-bit weights only");
+  static_assert(BM == 256 || (BM == 128 && !MX), "256-row tiles, or 128 for 8-bit weights");
 };
 
-template <int BKIND, int EPI>
+template <int BKIND, int EPI, int BM_ = 256>
 __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
-  using Cfg = G8Cfg<BKIND>;
+  using Cfg = G8Cfg<BKIND, BM_>;
   constexpr int BN = Cfg::BN, WM = Cfg::WM, WN = Cfg::WN, TM = Cfg::TM, TN = Cfg::TN;
   constexpr int A_ROWB = Cfg::A_ROWB, B_ROWB = Cfg::B_ROWB, A_BYTES = Cfg::A_BYTES, B_BYTES = Cfg::B_BYTES;
   constexpr int B_REGION = Cfg::B_REGION;
@@ -1286,11 +1289,11 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   }
 }
 
-template <int BKIND, int EPI>
+template <int BKIND, int EPI, int BM = 256>
 static void launch_g8(GemmArgs p, hipStream_t s) {
-  p.tiles_m = (p.M + 255) / 256;
+  p.tiles_m = (p.M + BM - 1) / BM;
   p.tiles_n = (p.N + 255) / 256;
-  gemm8_kernel<BKIND, EPI><<<p.tiles_m * p.tiles_n, kG8Threads, 0, s>>>(p);
+  gemm8_kernel<BKIND, EPI, BM><<<p.tiles_m * p.tiles_n, kG8Threads, 0, s>>>(p);
 }
 
 template <int BM, int BN, int BK, int STAGES, int BKIND, int EPI, int SWZ = 0, int LOADER = LOAD_DMA>
@@ -1320,8 +1323,8 @@ static bool g8_ok(const GemmArgs& p) {
 
 // Tile shapes (all K step 64): 256x256 and 128x128 with the register-staged
 // loader (1 and 2; 128x128 runs two workgroups per CU), 256x256 with the
-// LDS-DMA loader (3), 256x128 register-staged (4), and the 8-wave 256x256
-// kernel for 8-bit weights (5).
+// LDS-DMA loader (3), 256x128 register-staged (4), and the 8-wave kernel for
+// 8-bit weights with 256x256 (5) or 128x256 tiles (6).
 template <int BKIND, int EPI>
 static int launch_epi_w(const GemmArgs& p, int tile, hipStream_t s) {
   if (tile == 0) {
@@ -1333,14 +1336,19 @@ static int launch_epi_w(const GemmArgs& p, int tile, hipStream_t s) {
     // on that projection alone, were 0.25 ms slower per step: explicit only.)
     // int8 measured faster there than on the 4-wave kernel on every block
     // shape (4096^2 109 vs 134 us, FF up 428 vs 472, FF down 405 vs 435).
+    // (128-row tiles for the A2V query projection, 126 -> 243 tiles: 79 ->
+    // 61 us alone, but the step 1.0-1.6 ms slower in two A/B pairs -- 48 %
+    // more CU time per launch, which the audio stream's work beside it then
+    // lacks: explicit only, LTX_GEMM_TILE_G8_128.)
     const int64_t big = (int64_t)((p.M + 255) / 256) * ((p.N + 255) / 256);
     const bool g8 = (BKIND == B_MXFP8 || BKIND == B_INT8) && g8_ok<BKIND>(p);
     tile = big >= 160 ? (g8 ? 5 : 1) : (big >= 100 && g8 ? 5 : 2);
   }
-  if (tile == 5) {
+  if (tile == 5 || tile == 6) {
     if constexpr (BKIND != B_BF16) {
       if (!g8_ok<BKIND>(p)) return LTX_ERR_UNSUPPORTED;
-      launch_g8<BKIND, EPI>(p, s);
+      if (tile == 5) launch_g8<BKIND, EPI>(p, s);
+      else launch_g8<BKIND, EPI, 128>(p, s);
       return LTX_OK;
     } else {
       return LTX_ERR_UNSUPPORTED;
@@ -1374,7 +1382,7 @@ template <int BKIND>
 static int launch_kind(const GemmArgs& p, int epilogue, hipStream_t s) {
   const int epi = epilogue & 0xff;
   const int tile = (epilogue >> 8) & 0xf;
-  if (tile > 5) return LTX_ERR_INVALID_ARG;
+  if (tile > 6) return LTX_ERR_INVALID_ARG;
   GemmArgs q = p;
   q.round_then_bias = (epilogue & LTX_GEMM_ROUND_THEN_BIAS) != 0;
   int st;

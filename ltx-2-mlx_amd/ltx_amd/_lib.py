@@ -102,6 +102,7 @@ GEMM_TILE_128 = 2 << 8
 GEMM_TILE_256_DMA = 3 << 8
 GEMM_TILE_256x128 = 4 << 8
 GEMM_TILE_G8 = 5 << 8
+GEMM_TILE_G8_128 = 6 << 8
 GEMM_ROUND_THEN_BIAS = 1 << 12
 # Status of a request above the fixed scratch of a no-allocation entry point
 ERR_SCRATCH_LIMIT = -5

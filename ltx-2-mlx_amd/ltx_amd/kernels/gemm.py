@@ -36,7 +36,8 @@ EPI_GELU = _lib.GEMM_EPI_GELU
 EPI_RESIDUAL = _lib.GEMM_EPI_RESIDUAL
 EPI_RESIDUAL_ROUND = _lib.GEMM_EPI_RESIDUAL_ROUND
 EPI_SIGMOID2 = _lib.GEMM_EPI_SIGMOID2
-TILE_AUTO, TILE_256, TILE_128, TILE_256_DMA, TILE_256x128, TILE_G8 = 0, 1, 2, 3, 4, 5
+TILE_AUTO, TILE_256, TILE_128, TILE_256_DMA, TILE_256x128, TILE_G8, TILE_G8_128 = 0, 1, 2, 3, 4, 5, 6
+
 
 FORMATS = ("bf16", "int8", "mxfp8")
 

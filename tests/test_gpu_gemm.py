@@ -262,38 +262,46 @@ def test_gemm_splitk_rejects_bad_splits():
 
 
 # ---- the 8-wave kernel for 8-bit weights (tile 5) ---------------------------
+@pytest.mark.parametrize("rows", [256, 128])
 @pytest.mark.parametrize("kind", ["int8", "mxfp8"])
 @pytest.mark.parametrize("K,N", [(512, 384), (1024, 520), (4096, 256)])
-def test_gemm8_identity_returns_decoded_weight(kind, K, N):
-    """C = I @ W'^T through the 8-wave kernel: the per-fragment dequantisation
-    (scales from LDS, eight stages per octet for MXFP8) is bit-exact; K = 512
-    is one octet, 4096 eight; N = 520 leaves a ragged last tile."""
+def test_gemm8_identity_returns_decoded_weight(kind, K, N, rows):
+    """C = I @ W'^T through the 8-wave kernel (256- and 128-row tiles): the
+    per-fragment dequantisation (scales from LDS, eight stages per octet for
+    MXFP8) is bit-exact; K = 512 is one octet, 4096 eight; N = 520 leaves a
+    ragged last tile."""
     from ltx_amd.kernels import gemm
+
+    tile = gemm.TILE_G8 if rows == 256 else gemm.TILE_G8_128
 
     rng = np.random.default_rng(K + N)
     W = _weight_matrix(rng, N, K)
     W[5] = bf16r(np.logspace(-6, 2, K, dtype=np.float32) * np.sign(rng.standard_normal(K)).astype(np.float32))
     wt = gemm.make_weight(_t(W), kind=kind)
     eye = torch.eye(K, dtype=torch.bfloat16, device=DEV)
-    print(f"gemm8 identity {kind} K={K} N={N}", flush=True)
-    out = gemm.linear(eye, wt, tile=gemm.TILE_G8)
+    print(f"gemm8 identity {kind} K={K} N={N} rows={rows}", flush=True)
+    out = gemm.linear(eye, wt, tile=tile)
     deq = gemm.dequantize(wt)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(bf16_from_torch(out), bf16_from_torch(deq).T)
 
 
+@pytest.mark.parametrize("rows", [256, 128])
 @pytest.mark.parametrize("epi", ["bias", "gelu", "sigmoid2", "residual", "residual_round"])
 @pytest.mark.parametrize("kind", ["int8", "mxfp8"])
 @pytest.mark.parametrize("M,K,N", [(700, 1024, 1288), (3456, 4096, 768)])
-def test_gemm8_epilogues(epi, kind, M, K, N):
-    """Every epilogue through the 8-wave kernel, ragged M and N, against the
-    oracle, with the 2*sigmoid head-gate columns of a fused projection for
-    the bias epilogue; in place on the residual stream for the gated forms."""
+def test_gemm8_epilogues(epi, kind, M, K, N, rows):
+    """Every epilogue through the 8-wave kernel (256- and 128-row tiles),
+    ragged M and N, against the oracle, with the 2*sigmoid head-gate columns
+    of a fused projection for the bias epilogue; in place on the residual
+    stream for the gated forms."""
     from ltx_amd.kernels import gemm
+
+    tile = gemm.TILE_G8 if rows == 256 else gemm.TILE_G8_128
 
     codes = {"bias": gemm.EPI_BIAS, "gelu": gemm.EPI_GELU, "sigmoid2": gemm.EPI_SIGMOID2,
              "residual": gemm.EPI_RESIDUAL, "residual_round": gemm.EPI_RESIDUAL_ROUND}
-    print(f"gemm8 {kind} {epi} M={M} K={K} N={N}", flush=True)
+    print(f"gemm8 {kind} {epi} M={M} K={K} N={N} rows={rows}", flush=True)
     rng = np.random.default_rng(M + N + len(epi))
     x = _bf(rng, (M, K))
     W = _bf(rng, (N, K), 0.05)
@@ -305,10 +313,10 @@ def test_gemm8_epilogues(epi, kind, M, K, N):
     rt = _t(res)
     if epi.startswith("residual"):
         out = gemm.linear(_t(x), wt, epilogue=codes[epi], out=rt, residual=rt, gate=_t(g, torch.float32),
-                          tile=gemm.TILE_G8)
+                          tile=tile)
         assert out.data_ptr() == rt.data_ptr()
     else:
-        out = gemm.linear(_t(x), wt, epilogue=codes[epi], tile=gemm.TILE_G8, sigmoid_from=sig)
+        out = gemm.linear(_t(x), wt, epilogue=codes[epi], tile=tile, sigmoid_from=sig)
     torch.cuda.synchronize()
     qlin = kind == "mxfp8"
     ref = oq.linear(x, _decoded(kind, W), b, epilogue=epi, residual=res, gate=g, round_then_bias=qlin)
@@ -328,5 +336,6 @@ def test_gemm8_rejects_what_it_does_not_cover():
 
     for kind, k in (("bf16", 512), ("mxfp8", 1152)):  # bf16 weights; MXFP8 K not a multiple of 512
         wt = gemm.make_weight(torch.zeros((256, k), dtype=torch.bfloat16, device=DEV), kind=kind)
-        with pytest.raises(_lib.LtxKernelError, match="unsupported"):
-            gemm.linear(torch.zeros((300, k), dtype=torch.bfloat16, device=DEV), wt, tile=gemm.TILE_G8)
+        for tile in (gemm.TILE_G8, gemm.TILE_G8_128):
+            with pytest.raises(_lib.LtxKernelError, match="unsupported"):
+                gemm.linear(torch.zeros((300, k), dtype=torch.bfloat16, device=DEV), wt, tile=tile)
