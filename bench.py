@@ -120,13 +120,19 @@ def parse_args(argv=None):
                          "3456 and 6144 tokens and the 3456 x 256 text cross-attention (4 launches each, 32 "
                          "heads of 128, gated) or a 1 GiB device copy (3 launches, the FETCH_SIZE / WRITE_SIZE "
                          "calibration)")
+    ap.add_argument("--counter-tile", choices=["auto", "256", "g8"], default="auto",
+                    help="tile choice of the ff-up counter workload: the library's automatic choice (the "
+                         "8-wave kernel for MXFP8 and int8, the 4-wave 256x256 kernel for bf16), the 4-wave "
+                         "256x256 kernel, or the 8-wave kernel")
     return ap.parse_args(argv)
 
 
-def counter_workload(kind: str, weights: str) -> None:
+def counter_workload(kind: str, weights: str, tile_name: str = "auto") -> None:
     import torch
 
     from ltx_amd.kernels import gemm
+
+    tile = {"auto": gemm.TILE_AUTO, "256": gemm.TILE_256, "g8": gemm.TILE_G8}[tile_name]
 
     if kind == "fused-ops":
         # each row kernel 4 times on cache-cold rotating buffers (counter
@@ -157,6 +163,7 @@ def counter_workload(kind: str, weights: str) -> None:
     elif kind == "ff-up-vs-library":
         # the FF up-projection shape through the vendor library (hipBLASLt,
         # plain bf16 linear) and through this library's bf16 and MXFP8 GEMMs
+        # (bias epilogue; the --counter-tile choice)
         g = torch.Generator(device="cuda").manual_seed(0)
         x = torch.randn((3456, 4096), generator=g, device="cuda").bfloat16()
         w = (torch.randn((16384, 4096), generator=g, device="cuda") * 0.02).bfloat16()
@@ -164,8 +171,8 @@ def counter_workload(kind: str, weights: str) -> None:
         wb, wm = gemm.make_weight(w, b, kind="bf16"), gemm.make_weight(w, b, kind="mxfp8")
         for _ in range(3):
             torch.nn.functional.linear(x, w)
-            gemm.linear(x, wb, tile=gemm.TILE_256)
-            gemm.linear(x, wm, tile=gemm.TILE_256)
+            gemm.linear(x, wb, tile=gemm.TILE_256 if tile == gemm.TILE_G8 else tile)
+            gemm.linear(x, wm, tile=tile)
     else:
         g = torch.Generator(device="cuda").manual_seed(0)
         x = torch.randn((3456, 4096), generator=g, device="cuda").bfloat16()
@@ -173,9 +180,9 @@ def counter_workload(kind: str, weights: str) -> None:
         wt = gemm.make_weight(w, torch.zeros(16384, device="cuda"), kind=weights)
         out = torch.empty((3456, 16384), dtype=torch.bfloat16, device="cuda")
         for _ in range(4):
-            gemm.linear(x, wt, epilogue=gemm.EPI_GELU, out=out)
+            gemm.linear(x, wt, epilogue=gemm.EPI_GELU, out=out, tile=tile)
     torch.cuda.synchronize()
-    print(f"counter workload {kind} ({weights}) done", flush=True)
+    print(f"counter workload {kind} ({weights}, tile {tile_name}) done", flush=True)
 
 
 def step_flops(tv: int, ta: int, s: int, layers: int) -> float:
@@ -904,7 +911,7 @@ def main(argv=None):
                                    "here (see DESIGN.md for the sharding design)", "n_gpus": args.gpus}))
         return 2
     if args.counter_workload:
-        counter_workload(args.counter_workload, args.weights)
+        counter_workload(args.counter_workload, args.weights, args.counter_tile)
         return 0
     import torch
 
