@@ -1,16 +1,24 @@
 // Host-side checks of the C ABI, built against the library compiled with
-// AddressSanitizer on its host code (build.sh).  Every call takes an
-// argument-validation path that returns before any device work -- null
-// pointers, unsupported shapes, misaligned pointers or strides, empty
-// problems, workspace and padding helpers -- so the program runs without a
-// GPU and AddressSanitizer sees all the host code those paths execute.
+// AddressSanitizer on its host code (build.py).  The first part drives every
+// entry point through its argument-validation paths, which return before any
+// device work -- null pointers, unsupported shapes, misaligned pointers or
+// strides, empty problems, workspace and padding helpers.  The second part,
+// run only where no GPU is present, makes valid calls at the workloads'
+// shapes: each entry point then runs all of its host code -- tile and kernel
+// choice, split counts, workspace and scratch arithmetic, launch geometry --
+// up to the kernel launch, which the HIP runtime refuses for want of a
+// device (LTX_ERR_HIP), so AddressSanitizer sees the launch planning too.
 // Device pointers are fake, 16-byte aligned addresses that the library must
 // never dereference on the host.
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <initializer_list>
 
 #include "../../include/ltx_hip.h"
+
+// the HIP runtime's device count (C ABI of libamdhip64, which the library links)
+extern "C" int hipGetDeviceCount(int* count);
 
 static int failures = 0;
 
@@ -158,6 +166,132 @@ int main(int argc, char** argv) {
                                              hh, 128, 0.1f, 256, nullptr), LTX_ERR_UNSUPPORTED);
   EXPECT(ltx_flash_attn_splitkv_noalloc_bf16(d, 4096, d, 4096, d, 32, d, 4096, nullptr, 0, 68, 3456, 32, 128,
                                              0.1f, 16, nullptr), LTX_ERR_INVALID_ARG);  // tk_pad below Tk
+
+  // ---- launch planning: valid calls, refused at the launch (no device).
+  // Never with a device present: the fake addresses would reach a kernel.
+  int ndev = 0;
+  const int dev_status = hipGetDeviceCount(&ndev);  // 100: hipErrorNoDevice
+  if (ndev != 0 || (dev_status != 0 && dev_status != 100)) {
+    std::printf("launch-planning checks skipped: a device is present\n");
+  } else {
+    const uint8_t* q8 = static_cast<const uint8_t*>(d);
+    const int8_t* i8 = static_cast<const int8_t*>(d);
+    float* ws = fo;
+    uint32_t* cnt = static_cast<uint32_t*>(d);
+    const int64_t big = int64_t(1) << 30;
+    // row kernels at the step's shapes (video 3456 x 4096, audio 68 x 2048, the
+    // reference's T = 14640 test shape)
+    for (int64_t rows : {int64_t(68), int64_t(3456), int64_t(14640)}) {
+      for (int64_t c : {int64_t(2048), int64_t(4096)}) {
+        EXPECT(ltx_adaln_norm_fused_bf16(d, c, fd, fd, d, c, rows, c, 1e-6f, 0, nullptr), LTX_ERR_HIP);
+        EXPECT(ltx_adaln_norm_fused2_bf16(d, c, fd, fd, d, c, fd, fd, d, c, rows, c, 1e-6f, 0, nullptr),
+               LTX_ERR_HIP);
+        EXPECT(ltx_gated_add_fused_bf16(d, c, d, c, fd, d, c, rows, c, 0, nullptr), LTX_ERR_HIP);
+        EXPECT(ltx_qknorm_rope_bf16(d, 3 * c, rows, fd, fd, fd, d, 3 * c, rows, fd, fd, fd, c, c == 4096 ? 128 : 64,
+                                    1e-6f, nullptr), LTX_ERR_HIP);
+        EXPECT(ltx_qknorm_rope_axes_bf16(d, 3 * c, rows, fd, fd, fd, id, 3, 49, d, 3 * c, rows / 2, fd, fd, fd, id, 3,
+                                         49, c, c == 4096 ? 128 : 64, 1e-6f, nullptr), LTX_ERR_HIP);
+        EXPECT(ltx_output_norm_modulate_bf16(d, c, fd, fd, d, c, rows, c, 1e-6f, nullptr), LTX_ERR_HIP);
+      }
+    }
+    // GEMMs: every tile choice on the block's shapes, the 68-row audio shapes
+    // and the text-context shapes, every epilogue code
+    struct Shape { int64_t m, n, k; };
+    const Shape shapes[] = {{3456, 16384, 4096}, {3456, 4096, 16384}, {3456, 12320, 4096}, {3456, 2080, 4096},
+                            {3456, 4096, 2048}, {68, 6176, 2048}, {68, 2048, 8192}, {256, 8192, 4096},
+                            {10368, 4096, 4096}, {1, 1024, 4096}};
+    for (const Shape& sh : shapes) {
+      for (int tile = 0; tile <= 6; ++tile) {
+        for (int epi = 0; epi <= 4; ++epi) {
+          const int flags = epi | (tile << 8);
+          const void* r = epi == 2 || epi == 3 ? d : nullptr;
+          const float* g = epi == 2 || epi == 3 ? fd : nullptr;
+          const int want_bf16 = tile >= 5 ? LTX_ERR_UNSUPPORTED : LTX_ERR_HIP;
+          EXPECT(ltx_gemm_bf16(d, sh.k, d, sh.k, fd, d, sh.n, sh.m, sh.n, sh.k, flags, r, sh.n, g, sh.n - 32,
+                               nullptr), want_bf16);
+          EXPECT(ltx_gemm_w8a16_bf16(d, sh.k, i8, sh.k, fd, fd, d, sh.n, sh.m, sh.n, sh.k, flags, r, sh.n, g,
+                                     sh.n - 32, nullptr), LTX_ERR_HIP);
+          EXPECT(ltx_gemm_mxfp8_bf16(d, sh.k, q8, sh.k, q8, sh.k / 32, fd, d, sh.n, sh.m, sh.n, sh.k,
+                                     flags | LTX_GEMM_ROUND_THEN_BIAS, r, sh.n, g, sh.n - 32, nullptr),
+                 LTX_ERR_HIP);
+        }
+      }
+      for (int splits : {1, 2, 4, 8, 16}) {
+        if (sh.k % (128 * splits) != 0) continue;
+        const int64_t need = ltx_gemm_splitk_workspace_bytes(sh.m, sh.n, splits);
+        const int64_t rneed = ltx_gemm_rows_workspace_bytes(sh.m, sh.n, splits);
+        const int64_t words = ltx_gemm_rows_counter_words(sh.m, sh.n);
+        EXPECT(need > 0 && rneed == need && words > 0, 1);
+        EXPECT(ltx_gemm_splitk_bf16(d, sh.k, d, sh.k, fd, d, sh.n, sh.m, sh.n, sh.k, 0, nullptr, 0, nullptr, sh.n,
+                                    splits, ws, need, nullptr), sh.m * sh.n * 4 * splits >= big ? LTX_ERR_HIP : LTX_ERR_HIP);
+        EXPECT(ltx_gemm_splitk_mxfp8_bf16(d, sh.k, q8, sh.k, q8, sh.k / 32, fd, d, sh.n, sh.m, sh.n, sh.k, 3, d,
+                                          sh.n, fd, sh.n, splits, ws, need, nullptr), LTX_ERR_HIP);
+        EXPECT(ltx_gemm_splitk_w8a16_bf16(d, sh.k, i8, sh.k, fd, fd, d, sh.n, sh.m, sh.n, sh.k, 1, nullptr, 0,
+                                          nullptr, sh.n, splits, ws, need, nullptr), LTX_ERR_HIP);
+        if (sh.m <= 256) {
+          EXPECT(ltx_gemm_rows_bf16(d, sh.k, d, sh.k, fd, d, sh.n, sh.m, sh.n, sh.k, 2, d, sh.n, fd, sh.n, splits,
+                                    ws, rneed, cnt, words, nullptr), LTX_ERR_HIP);
+          EXPECT(ltx_gemm_rows_w8a16_bf16(d, sh.k, i8, sh.k, fd, fd, d, sh.n, sh.m, sh.n, sh.k, 1, nullptr, 0,
+                                          nullptr, sh.n, splits, ws, rneed, cnt, words, nullptr), LTX_ERR_HIP);
+          EXPECT(ltx_gemm_rows_mxfp8_bf16(d, sh.k, q8, sh.k, q8, sh.k / 32, fd, d, sh.n, sh.m, sh.n, sh.k,
+                                          4 | LTX_GEMM_ROUND_THEN_BIAS, nullptr, 0, nullptr, sh.n - 32, splits, ws,
+                                          rneed, cnt, words, nullptr), LTX_ERR_HIP);
+        }
+      }
+      if (sh.k % 512 == 0 && sh.m >= 256) {
+        EXPECT(ltx_gemm_mx_bf16(q8, sh.k, q8, sh.k / 32, q8, sh.k, q8, sh.k / 32, fd, d, sh.n, sh.m, sh.n, sh.k, 2, d,
+                                sh.n, fd, sh.n, nullptr), LTX_ERR_HIP);
+        EXPECT(ltx_gemm_mx_gelu_mxfp8(q8, sh.k, q8, sh.k / 32, q8, sh.k, q8, sh.k / 32, fd,
+                                      static_cast<uint8_t*>(d), sh.n, static_cast<uint8_t*>(d), sh.n / 32, sh.m,
+                                      sh.n, sh.k, LTX_GEMM_ROUND_THEN_BIAS, nullptr), LTX_ERR_HIP);
+      }
+    }
+    // weight formats at the block's shapes
+    EXPECT(ltx_quantize_mxfp8_bf16(d, 4096, 16384, 4096, static_cast<uint8_t*>(d), 4096, static_cast<uint8_t*>(d),
+                                   128, nullptr), LTX_ERR_HIP);
+    EXPECT(ltx_dequantize_mxfp8_bf16(q8, 4096, q8, 128, 16384, 4096, d, 4096, nullptr), LTX_ERR_HIP);
+    EXPECT(ltx_quantize_w8_bf16(d, 4096, 16384, 4096, static_cast<int8_t*>(d), 4096, fo, nullptr), LTX_ERR_HIP);
+    EXPECT(ltx_dequantize_w8_bf16(i8, 4096, fd, 16384, 4096, d, 4096, nullptr), LTX_ERR_HIP);
+    EXPECT(ltx_dequantize_fp8_e4m3(q8, int64_t(16384) * 4096, fd, d, 0, nullptr), LTX_ERR_HIP);
+    // attention: every call shape of the block, both V layouts, split-KV with
+    // its workspace, the no-allocation form (which resolves its scratch first)
+    struct Attn { int64_t tq, tk, h, dh; };
+    const Attn calls[] = {{3456, 3456, 32, 128}, {6144, 6144, 32, 128}, {3456, 256, 32, 128}, {3456, 68, 32, 64},
+                          {68, 3456, 32, 64}, {68, 68, 32, 64}, {68, 256, 32, 64}, {1, 1, 1, 64}};
+    for (const Attn& a : calls) {
+      const int64_t rs = a.h * a.dh, tkp = ltx_attn_vt_padded_len(a.tk);
+      EXPECT(ltx_flash_attn_v_bf16(d, rs, d, rs, d, rs, d, rs, d, a.h, a.tq, a.tk, a.h, a.dh, 0.1f, nullptr),
+             LTX_ERR_HIP);
+      EXPECT(ltx_flash_attn_bf16(d, rs, d, rs, d, tkp, d, rs, nullptr, 0, a.tq, a.tk, a.h, a.dh, 0.1f, nullptr),
+             LTX_ERR_HIP);
+      EXPECT(ltx_attn_transpose_v_bf16(d, rs, a.tk, a.h, a.dh, d, tkp, nullptr), LTX_ERR_HIP);
+      for (int64_t splits : {int64_t(2), int64_t(16), int64_t(54)}) {
+        const int64_t need = ltx_attn_splitkv_workspace_bytes(a.tq, a.h, a.dh, splits);
+        EXPECT(need > 0, 1);
+        EXPECT(ltx_flash_attn_splitkv_v_bf16(d, rs, d, rs, d, rs, d, rs, d, a.h, a.tq, a.tk, a.h, a.dh, 0.1f, splits,
+                                             d, need, nullptr), LTX_ERR_HIP);
+        EXPECT(ltx_flash_attn_splitkv_bf16(d, rs, d, rs, d, tkp, d, rs, nullptr, 0, a.tq, a.tk, a.h, a.dh, 0.1f,
+                                           splits, d, need, nullptr), LTX_ERR_HIP);
+        if (need <= (int64_t(32) << 20))
+          EXPECT(ltx_flash_attn_splitkv_noalloc_bf16(d, rs, d, rs, d, tkp, d, rs, nullptr, 0, a.tq, a.tk, a.h, a.dh,
+                                                     0.1f, splits, nullptr), LTX_ERR_HIP);
+      }
+    }
+    // step glue, guidance, latents, text features at the workloads' sizes
+    EXPECT(ltx_euler_x0_step_bf16(d, d, 1.0f, 0.5f, d, 3456 * 128, nullptr), LTX_ERR_HIP);
+    EXPECT(ltx_timestep_embedding_f32(fd, 4, 1000.0f, fo, 256, nullptr), LTX_ERR_HIP);
+    EXPECT(ltx_gemv_f32_bf16w(fd, 2, 4096, d, fd, fo, 9 * 4096, 1, nullptr), LTX_ERR_HIP);
+    EXPECT(ltx_broadcast_add_f32(fd, fd, fo, 48 * 16, 4096, nullptr), LTX_ERR_HIP);
+    EXPECT(ltx_x0_from_velocity_f32(d, d, 0.5f, fo, 3456 * 128, nullptr), LTX_ERR_HIP);
+    EXPECT(ltx_guidance_f32(fd, fd, fd, fd, 3.0f, 1.0f, 0.0f, fd, fd, fo, 3456 * 128, 0, nullptr), LTX_ERR_HIP);
+    EXPECT(ltx_guidance_stats_f32(fd, fd, 3456 * 128, LTX_GUIDE_STATS_STD_RATIO, 0.7f, 0.3f, fo, nullptr),
+           LTX_ERR_HIP);
+    EXPECT(ltx_ge_correct_f32(fd, fo, fo, 0, 0.5f, 0.5f, 3456 * 128, nullptr), LTX_ERR_HIP);
+    EXPECT(ltx_euler_step_bf16(d, fd, 0.5f, d, 3456 * 128, nullptr), LTX_ERR_HIP);
+    EXPECT(ltx_swap_axes(d, 9, 128, 384, 2, static_cast<char*>(d) + (1 << 24), nullptr), LTX_ERR_HIP);
+    EXPECT(ltx_gemma_features_bf16(d, 49, 1024, 3840, 1024 * 3840, 3840, id, 1e-6f, 1.0f, 1.0f, d, d, 49 * 3840,
+                                   nullptr), LTX_ERR_HIP);
+  }
 
   std::printf("%s: %d failure(s)\n", failures ? "FAIL" : "ok", failures);
   return failures ? 1 : 0;

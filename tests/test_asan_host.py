@@ -4,8 +4,13 @@
 ``-fsanitize=address`` on the host side and links ``host_checks.cpp``, which
 drives every entry point through its argument-validation paths (null
 pointers, unsupported shapes, misalignment, empty problems, workspace and
-padding helpers) without a GPU.  The first build takes about a minute and a
-half; later runs reuse the objects.
+padding helpers) and then, where no GPU is present, makes valid calls at the
+workloads' shapes (every GEMM tile choice and epilogue, split counts, the
+few-row and MX forms, every attention call shape with its split-KV
+workspace and the no-allocation scratch, the row kernels, guidance and
+latent kernels): their host code runs up to the kernel launch, which the
+HIP runtime refuses for want of a device.  The first build takes about a
+minute and a half; later runs reuse the objects.
 """
 
 from __future__ import annotations
