@@ -22,6 +22,7 @@ import torch
 from ...kernels import attention as attn_k
 from ...kernels import gemm
 from ...kernels.rope_ops import qknorm_rope_
+from ...utils import signpost as _sp
 
 
 class Attention:
@@ -82,6 +83,7 @@ class Attention:
         """
         inner, heads = self.inner_dim, self.heads
         gate_cols = heads if self.gated else 0
+        _sp.begin("attn_qkv")
         if self.self_attention:
             buf = gemm.linear(x, self.proj_q, sigmoid_from=3 * inner)
             q, k, v = buf[:, :inner], buf[:, inner:2 * inner], buf[:, 2 * inner:3 * inner]
@@ -99,9 +101,12 @@ class Attention:
         k_done = kv is not None  # keys already normalised by context_kv
         if passes == 1:
             qknorm_rope_(q, self.q_norm, pe, k[:0] if k_done else k, self.k_norm, k_tab, heads, self.norm_eps)
+            _sp.end("attn_qkv")
             if kv_ready is not None:
                 torch.cuda.current_stream().wait_event(kv_ready)
-            return attn_k.flash_attention(q, k, v, heads, gate=g)
+            with _sp.signpost("attn_sdpa"):
+                return attn_k.flash_attention(q, k, v, heads, gate=g)
+        _sp.end("attn_qkv")
         tq, tk = q.shape[0] // passes, k.shape[0] // passes
         if tq * passes != q.shape[0] or tk * passes != k.shape[0]:
             raise ValueError(f"{q.shape[0]} query / {k.shape[0]} key rows do not split into {passes} passes")

@@ -49,6 +49,7 @@ import torch
 
 from ... import _lib
 from ...kernels import fused_ops, gemm
+from ...utils import signpost as _sp
 from .attention import Attention
 from .feed_forward import FeedForward
 from ...components.perturbations import BatchedPerturbationConfig  # noqa: F401  (the block's perturbation type)
@@ -291,9 +292,11 @@ class BasicAVTransformerBlock:
         ta = a2.shape[0] // npass if a2 is not None else 0
         v_owned = a_owned = False
 
-        def residual_gemm(o, weight, stream_x, owned, gate, epi):
+        def residual_gemm(o, weight, stream_x, owned, gate, epi, phase="attn_out"):
             out = stream_x if owned else torch.empty_like(stream_x)
+            _sp.begin(phase)
             gemm.linear(o, weight, epilogue=epi, out=out, residual=stream_x, gate=gate)
+            _sp.end(phase)
             return out
 
         def partial_residual(x2, owned, t, rng, sublayer):
@@ -387,6 +390,7 @@ class BasicAVTransformerBlock:
                     nb._prefetched_kv[0].record_stream(main)
 
         if run_vx:
+            _sp.begin("video_self_attn")
             pe = _tables(video.positional_embeddings)
             rng = runs(keep("skip_video_self_attn"))
             if rng == [(0, npass)]:
@@ -404,7 +408,9 @@ class BasicAVTransformerBlock:
                                 gate=ada_v[ROW_GATE_MSA])
                 v2 = partial_residual(v2, v_owned, tv, rng, video_self)
                 v_owned = True
+            _sp.end("video_self_attn")
             mark("video self-attn")
+            _sp.begin("video_text_ca")
             if side is not None and kv_v is None:
                 context_kv_on_side()
             a = adaln(v2, ada_v[ROW_SCALE_Q], ada_v[ROW_SHIFT_Q], eps, rn)
@@ -426,11 +432,13 @@ class BasicAVTransformerBlock:
                         if npass > 1 else self.attn2.core(a, c)
             v2 = residual_gemm(o, self.attn2.to_out, v2, v_owned, ada_v[ROW_GATE_Q], gemm.EPI_RESIDUAL_ROUND)
             v_owned = True
+            _sp.end("video_text_ca")
             mark("video text-attn")
 
         if run_ax:
             with on_audio():
                 fork_side()
+                _sp.begin("audio_self_attn")
                 pe = _tables(audio.positional_embeddings)
                 rng = runs(keep("skip_audio_self_attn"))
                 if rng == [(0, npass)]:
@@ -447,7 +455,9 @@ class BasicAVTransformerBlock:
                                     gate=ada_a[ROW_GATE_MSA])
                     a2 = partial_residual(a2, a_owned, ta, rng, audio_self)
                     a_owned = True
+                _sp.end("audio_self_attn")
                 mark("audio self-attn")
+                _sp.begin("audio_text_ca")
                 a = adaln(a2, ada_a[ROW_SCALE_Q], ada_a[ROW_SHIFT_Q], eps, rn)
                 c, cp = ctx_rows(audio, 0, npass)
                 c = adaln(c, ada_a[ROW_SCALE_KV], ada_a[ROW_SHIFT_KV], eps, _lib.ADALN_NO_NORM)
@@ -459,9 +469,11 @@ class BasicAVTransformerBlock:
                 a2 = residual_gemm(o, self.audio_attn2.to_out, a2, a_owned, ada_a[ROW_GATE_Q],
                                    gemm.EPI_RESIDUAL_ROUND)
                 a_owned = True
+                _sp.end("audio_text_ca")
                 mark("audio text-attn")
 
         if run_a2v or run_v2a:
+            _sp.begin("a2v_cross")
             vpe = _tables(video.cross_positional_embeddings)
             ape = _tables(audio.cross_positional_embeddings)
             # modulated inputs of both directions from the pre-A2V streams
@@ -501,8 +513,10 @@ class BasicAVTransformerBlock:
                                 residual=src, gate=ada_v[ROW_GATE_AV])
                 v2 = partial_residual(v2, v_owned, tv, rng, a2v)
                 v_owned = True
+            _sp.end("a2v_cross")
             if run_a2v:
                 mark("audio->video attn")
+            _sp.begin("v2a_cross")
             rng = runs(keep("skip_v2a_cross_attn")) if run_v2a else []
             if rng:
                 with on_audio():
@@ -521,18 +535,30 @@ class BasicAVTransformerBlock:
                         a2 = partial_residual(a2, a_owned, ta, rng, v2a)
                     a_owned = True
                     mark("video->audio attn")
+            _sp.end("v2a_cross")
 
         if run_vx:
+            _sp.begin("video_ff")
+            _sp.begin("v_ff_adaln")
             h = adaln(v2, ada_v[ROW_SCALE_MLP], ada_v[ROW_SHIFT_MLP], eps, flags)
+            _sp.end("v_ff_adaln")
+            _sp.begin("v_ff_inner")
             f = self.ff.hidden(h)
-            v2 = residual_gemm(f, self.ff.project_out, v2, v_owned, ada_v[ROW_GATE_MLP], gemm.EPI_RESIDUAL)
+            v2 = residual_gemm(f, self.ff.project_out, v2, v_owned, ada_v[ROW_GATE_MLP], gemm.EPI_RESIDUAL,
+                               phase=None)
+            _sp.end("v_ff_inner")
+            _sp.signpost_barrier(v2)
+            _sp.end("video_ff")
             mark("video ff")
         if run_ax:
             with on_audio():
+                _sp.begin("audio_ff")
                 h = adaln(a2, ada_a[ROW_SCALE_MLP], ada_a[ROW_SHIFT_MLP], eps, flags)
                 f = self.audio_ff.hidden(h)
                 a2 = residual_gemm(f, self.audio_ff.project_out, a2, a_owned, ada_a[ROW_GATE_MLP],
-                                   gemm.EPI_RESIDUAL)
+                                   gemm.EPI_RESIDUAL, phase=None)
+                _sp.signpost_barrier(a2)
+                _sp.end("audio_ff")
                 mark("audio ff")
 
         def pack(args, x2, x_in, owned):
