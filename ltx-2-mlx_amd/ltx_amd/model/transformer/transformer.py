@@ -408,6 +408,7 @@ class BasicAVTransformerBlock:
                                 gate=ada_v[ROW_GATE_MSA])
                 v2 = partial_residual(v2, v_owned, tv, rng, video_self)
                 v_owned = True
+            _sp.signpost_barrier(v2)
             _sp.end("video_self_attn")
             mark("video self-attn")
             _sp.begin("video_text_ca")
@@ -432,6 +433,7 @@ class BasicAVTransformerBlock:
                         if npass > 1 else self.attn2.core(a, c)
             v2 = residual_gemm(o, self.attn2.to_out, v2, v_owned, ada_v[ROW_GATE_Q], gemm.EPI_RESIDUAL_ROUND)
             v_owned = True
+            _sp.signpost_barrier(v2)
             _sp.end("video_text_ca")
             mark("video text-attn")
 
@@ -455,6 +457,7 @@ class BasicAVTransformerBlock:
                                     gate=ada_a[ROW_GATE_MSA])
                     a2 = partial_residual(a2, a_owned, ta, rng, audio_self)
                     a_owned = True
+                _sp.signpost_barrier(a2)
                 _sp.end("audio_self_attn")
                 mark("audio self-attn")
                 _sp.begin("audio_text_ca")
@@ -469,6 +472,7 @@ class BasicAVTransformerBlock:
                 a2 = residual_gemm(o, self.audio_attn2.to_out, a2, a_owned, ada_a[ROW_GATE_Q],
                                    gemm.EPI_RESIDUAL_ROUND)
                 a_owned = True
+                _sp.signpost_barrier(a2)
                 _sp.end("audio_text_ca")
                 mark("audio text-attn")
 
@@ -513,6 +517,7 @@ class BasicAVTransformerBlock:
                                 residual=src, gate=ada_v[ROW_GATE_AV])
                 v2 = partial_residual(v2, v_owned, tv, rng, a2v)
                 v_owned = True
+            _sp.signpost_barrier(v2)
             _sp.end("a2v_cross")
             if run_a2v:
                 mark("audio->video attn")
@@ -535,6 +540,7 @@ class BasicAVTransformerBlock:
                         a2 = partial_residual(a2, a_owned, ta, rng, v2a)
                     a_owned = True
                     mark("video->audio attn")
+            _sp.signpost_barrier(a2)
             _sp.end("v2a_cross")
 
         if run_vx:

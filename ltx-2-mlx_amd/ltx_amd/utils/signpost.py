@@ -9,8 +9,8 @@ switches, the same API -- ``with signpost("video_self_attn"): ...`` and
 * ``LTX_PROFILE_SIGNPOSTS=1`` turns it on; unset, ``signpost`` is a no-op
   that loads nothing and formats nothing.
 * Ranges are rocTX ranges (``roctxRangePushA`` / ``roctxRangePop`` of
-  ``libroctx64.so``), shown by ``rocprofv3 --marker-trace`` beside the
-  kernels of the same process.
+  rocprofiler-sdk's ``librocprofiler-sdk-roctx.so``), recorded by
+  ``rocprofv3 --marker-trace`` beside the kernels of the same process.
 * ``LTX_PROFILE_SIGNPOST_LOG=<path>``: a sidecar log, one line per event,
   ``<ns> <begin|end> <phase>`` on ``time.monotonic_ns()``.
 * ``LTX_PROFILE_SIGNPOSTS_SYNC=1``: ``signpost_barrier`` synchronises the
@@ -67,8 +67,11 @@ def _init() -> None:
         if path:
             _log_fh = open(path, "w", buffering=1)
             _log_fh.write(f"# LTX signpost log  pid={os.getpid()}  phases={','.join(PHASES)}\n")
-        for name in ("libroctx64.so", "libroctx64.so.4",
-                     os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib", "libroctx64.so")):
+        # rocprofiler-sdk's rocTX (what rocprofv3 --marker-trace records) first,
+        # the roctracer-era library after it
+        lib_dir = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib")
+        for name in ("librocprofiler-sdk-roctx.so", os.path.join(lib_dir, "librocprofiler-sdk-roctx.so"),
+                     "libroctx64.so", os.path.join(lib_dir, "libroctx64.so")):
             try:
                 lib = ctypes.CDLL(name)
             except OSError:
