@@ -10,6 +10,8 @@ counts.
   6144 + 121 tokens (normwise max relative error <= 1e-2, cosine >= 0.999
   per stream), and all eight steps of a 4-block full-width MXFP8 model on a
   384-token grid (per-step latent cosine >= 0.999).
+* Oracle at full depth: all eight steps of the 48-block full-width MXFP8
+  model on the same 384-token grid (per-step latent cosine >= 0.999).
 
 The audio length follows the workload as written (121 tokens; the reference's
 formula gives 127 at 24 fps, ``components.patchifiers.audio_latent_frames``).
@@ -129,4 +131,80 @@ def test_768x512x121_eight_steps_four_blocks_vs_oracle():
         vlat, alat = ob.model_step(MW, vlat, alat, vctx, actx, sig[step], sig[step + 1], pes)
         cv, ca = cos_sim(got[step][0].numpy(), vlat.numpy()), cos_sim(got[step][1].numpy(), alat.numpy())
         print(f"step {step}: video cos {cv:.6f} audio cos {ca:.6f}", flush=True)
+        assert cv >= 0.999 and ca >= 0.999
+
+
+class _HostBlocks:
+    """The 48 blocks' oracle weights held on the host in bf16 (their decoded
+    values are bf16: exact), fetched from the device one block at a time on
+    first use, and widened to fp32 one block at a time as the oracle walks
+    the blocks: ~31 GB of host memory instead of ~60 GB."""
+
+    def __init__(self, model):
+        self.blocks = model.transformer_blocks
+        self.cache = None
+
+    @staticmethod
+    def _pack(w):
+        if isinstance(w, dict):
+            return {k: _HostBlocks._pack(v) for k, v in w.items()}
+        if isinstance(w, torch.Tensor) and w.dim() == 2:
+            n = w.to(torch.bfloat16)
+            assert torch.equal(n.float(), w)
+            return n
+        return w
+
+    @staticmethod
+    def _widen(w):
+        if isinstance(w, dict):
+            return {k: _HostBlocks._widen(v) for k, v in w.items()}
+        if isinstance(w, torch.Tensor) and w.dtype == torch.bfloat16:
+            return w.float()
+        return w
+
+    def __iter__(self):
+        from _weights import block_weights
+
+        if self.cache is None:
+            self.cache = [self._pack(block_weights(b)) for b in self.blocks]
+        for w in self.cache:
+            yield self._widen(w)
+
+
+def test_48_blocks_full_width_eight_steps_vs_oracle():
+    """All 48 full-width MXFP8 blocks (the workload's depth and widths) on a
+    384-token video grid + 26 audio + 256 text tokens: the eight distilled
+    steps against the oracle, which runs the same 48 blocks from the model's
+    decoded weights.  Gate: per-step latent cosine >= 0.999 for both streams
+    (the north-star trajectory gate, at full depth)."""
+    from test_gpu_model import _model_weights
+
+    from ltx_amd.model.transformer.model import LTXModel
+    from ltx_amd.pipeline import DenoiseState, denoise_step
+
+    print("48 blocks full width, 384 video tokens: 8 steps vs oracle", flush=True)
+    model = LTXModel(num_layers=48, weight_format="mxfp8", seed=23)
+    st = DenoiseState(model, height=256, width=384, frames=25, text_tokens=256, audio_frames=26, seed=9)
+    pes_dev = model.rope(st.video_positions, st.audio_positions)
+    vpos, apos = st.video_positions, st.audio_positions
+    pes = tuple(tuple(torch.from_numpy(a) for a in p) for p in (
+        orope.rope_tables(vpos, 4096, 32, orope.VIDEO_MAX_POS),
+        orope.rope_tables(vpos[:, 0:1], 2048, 32, orope.AUDIO_MAX_POS),
+        orope.rope_tables(apos, 2048, 32, orope.AUDIO_MAX_POS),
+        orope.rope_tables(apos[:, 0:1], 2048, 32, orope.AUDIO_MAX_POS)))
+    vlat, alat = st.video_latent.float().cpu(), st.audio_latent.float().cpu()
+    vctx, actx = st.video_context.float().cpu(), st.audio_context.float().cpu()
+    blocks = model.transformer_blocks
+    model.transformer_blocks = blocks[:0]  # the non-block weights only
+    MW = _model_weights(model)
+    model.transformer_blocks = blocks
+    MW["blocks"] = _HostBlocks(model)
+    sig = st.sigmas
+    for step in range(8):
+        denoise_step(model, st, step, pes_dev)
+        torch.cuda.synchronize()
+        gv, ga = st.video_latent.float().cpu(), st.audio_latent.float().cpu()
+        vlat, alat = ob.model_step(MW, vlat, alat, vctx, actx, sig[step], sig[step + 1], pes)
+        cv, ca = cos_sim(gv.numpy(), vlat.numpy()), cos_sim(ga.numpy(), alat.numpy())
+        print(f"48 blocks step {step}: video cos {cv:.6f} audio cos {ca:.6f}", flush=True)
         assert cv >= 0.999 and ca >= 0.999
