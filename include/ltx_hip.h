@@ -244,12 +244,14 @@ int ltx_broadcast_add_f32(const float* table, const float* vec, float* out, int6
 #define LTX_GEMM_TILE_256_DMA (3 << 8) /* 256x256, LDS-DMA loader */
 #define LTX_GEMM_TILE_256x128 (4 << 8) /* 256 rows x 128 columns */
 /* 256x256, eight waves in two groups that alternate between global->LDS
- * loads / fragment reads and MFMAs; 8-bit weights only (int8, and MXFP8 with
- * K % 512 == 0 and 16-byte aligned scale rows), else LTX_ERR_UNSUPPORTED.
- * The default for MXFP8 weights when 256x256 tiles are chosen. */
+ * loads / fragment reads and MFMAs; every weight format (MXFP8 needs
+ * K % 512 == 0 and 16-byte aligned scale rows, else LTX_ERR_UNSUPPORTED).
+ * The automatic choice for int8 and MXFP8 weights when 256x256 tiles are
+ * chosen, and for bf16 weights on products wider than deep (N > K) or of
+ * 100-159 tiles. */
 #define LTX_GEMM_TILE_G8 (5 << 8)
-/* The eight-wave kernel with 128 x 256 tiles (8-bit weights, same conditions
- * as LTX_GEMM_TILE_G8), for products whose 256 x 256 tiles fill only part of
+/* The eight-wave kernel with 128 x 256 tiles (same conditions as
+ * LTX_GEMM_TILE_G8), for products whose 256 x 256 tiles fill only part of
  * one round; never the automatic choice. */
 #define LTX_GEMM_TILE_G8_128 (6 << 8)
 /* OR-ed into `epilogue`: the bias is added to the bf16-rounded product,

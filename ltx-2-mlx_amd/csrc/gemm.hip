@@ -718,7 +718,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
   }
 }
 
-// ---- 8-wave ping-pong kernel for 8-bit weights ------------------------------
+// ---- 8-wave ping-pong kernel (8-bit weights; bf16 weights in 32-deep stages) --
 // 256x256 tile, K step 64, eight waves (two per SIMD) in two groups of four:
 // group 0 (waves 0-3) owns output rows 0-127 of the tile, group 1 (waves 4-7)
 // rows 128-255; wave w & 3 owns 64 output columns.  The groups run half a
@@ -735,7 +735,9 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
 // global_load_lds (no staging registers, no LDS write instructions): three
 // 48 KB stages of bf16 activations (256 x 128 B) and raw weight codes
 // (256 x 64 B).  The MXFP8 / int8 codes are dequantised per fragment with the
-// exact format arithmetic, so the bf16 MFMA sees bit-exact weights.
+// exact format arithmetic, so the bf16 MFMA sees bit-exact weights.  bf16
+// weights: four 32 KB stages of 32-deep bf16 rows of both operands, the
+// direct loads three stages ahead, 16 MFMAs per cluster, no dequantisation.
 //
 // Inside a stage the k order of the MFMA slots is permuted so that a lane
 // reads the codes of two k-steps with one 16-byte LDS read: k-step 2p+s, lane
@@ -743,13 +745,28 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
 // of that k range is p).  The sum over the stage is the same set of products.
 constexpr int kG8Threads = 512;
 // the automatic tile choice uses the 8-wave kernel for 8-bit weights (MXFP8
-// and int8) on problems of at least 100 256x256 tiles
-constexpr int kG8Stages = 3;
+// and int8) on problems of at least 100 256x256 tiles, and for bf16 weights on
+// problems of at least 160
 
-template <int BKIND, int BM_ = 256, int kG8Stages_ = 3>
+// f(integral_constant<int, I>) for I = I0 .. N-1, in order
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+template <int BKIND, int BM_ = 256, int BF_STAGES = 5>
 struct G8Cfg {
   static constexpr bool MX = BKIND == B_MX;
-  static constexpr int BM = BM_, BN = 256, BK = 64;
+  // bf16 weights: a 64-deep stage of both bf16 operands (64 KB) leaves room
+  // for only two stages, so the stages are 32 deep (64-byte rows of both
+  // operands, laid out like the 8-bit code rows) in a ring of BF_STAGES, the
+  // direct loads running BF_STAGES - 1 stages ahead
+  static constexpr bool BF = BKIND == B_BF16;
+  static constexpr int BM = BM_, BN = 256, BK = BF ? 32 : 64;
+  static constexpr int STAGES = BF ? BF_STAGES : 3;
   // 128x64 wave tiles: each weight fragment is dequantised by the two waves
   // that share its columns rather than four (64x128 tiles read fewer LDS
   // bytes per MFMA, but MXFP8 measured 2.5 % slower with them: the
@@ -760,32 +777,36 @@ struct G8Cfg {
   static constexpr int TM = WM / 32, TN = WN / 32;
   static constexpr int WAVES_M = BM / WM;
   // bf16 activations (MX: 8-bit codes like the weights), 8-bit weight codes
-  static constexpr int A_ROWB = MX ? BK : BK * 2, B_ROWB = BK;
+  // (BF: bf16 weights)
+  static constexpr int A_ROWB = MX ? BK : BK * 2, B_ROWB = BF ? BK * 2 : BK;
   static constexpr int A_BYTES = BM * A_ROWB, B_BYTES = BN * B_ROWB;
   static constexpr int STAGE = A_BYTES + B_BYTES;
-  // LDS: the three A stages, then the three B stages (every fragment read is
-  // then a fixed per-lane register plus an immediate offset below 64 KiB)
-  static constexpr int B_REGION = kG8Stages_ * A_BYTES;
+  // LDS: the A stages, then the B stages (every fragment read is then a fixed
+  // per-lane register plus an immediate offset below 64 KiB)
+  static constexpr int B_REGION = STAGES * A_BYTES;
   static constexpr int A_DMA = A_BYTES / 1024 / 8, B_DMA = B_BYTES / 1024 / 8;  // per wave per stage
   static constexpr int EPI_ROWB = WN * 2 + 16;
   static constexpr int EPI_WAVE = WM * EPI_ROWB;
   static constexpr int EPI_BYTES = 8 * EPI_WAVE;
-  static constexpr int LDS_BYTES = (kG8Stages * STAGE > EPI_BYTES) ? kG8Stages * STAGE : EPI_BYTES;
   static constexpr int COL_BYTES = 2 * BN * 4;
+  // the column values (bias, gate) follow the epilogue's staging area; they
+  // are written after the main loop, so they may lie inside the stage ring
+  static constexpr int COL_OFF = EPI_BYTES;
+  static constexpr int RING = STAGES * STAGE;
+  static constexpr bool COL_IN_RING = COL_OFF < RING;
+  static constexpr int LDS_BYTES = (RING > EPI_BYTES + COL_BYTES) ? RING : EPI_BYTES + COL_BYTES;
   // MXFP8 scales of eight stages (256 rows x 16 E8M0 bytes), double buffered;
   // MX: the weights' then the activations' octets
   static constexpr int SC_OCT = BN * 16;
   static constexpr int SC_BYTES = BKIND == B_MXFP8 ? 2 * SC_OCT : (MX ? 4 * SC_OCT : 0);
-  // column values at LDS_BYTES; the scale octets after them, or (MX) right
-  // after the stages, inside the epilogue's staging area (dead by then: every
-  // scale load has landed before the epilogue's first barrier)
-  static constexpr int COL_OFF = LDS_BYTES;
-  static constexpr int SC_OFF = MX ? kG8Stages * STAGE : LDS_BYTES + COL_BYTES;
-  static constexpr int TOTAL = MX ? LDS_BYTES + COL_BYTES : LDS_BYTES + COL_BYTES + SC_BYTES;
-  static_assert(!MX || SC_OFF + SC_BYTES <= LDS_BYTES, "MX scales inside the staging area");
+  // the scale octets after the column values, or (MX) right after the
+  // stages, inside the epilogue's staging area (dead by then: every scale
+  // load has landed before the epilogue's first barrier)
+  static constexpr int SC_OFF = MX ? RING : LDS_BYTES;
+  static constexpr int TOTAL = MX ? LDS_BYTES : LDS_BYTES + SC_BYTES;
+  static_assert(!MX || SC_OFF + SC_BYTES <= EPI_BYTES, "MX scales inside the staging area");
   static_assert(TOTAL <= 160 * 1024, "LDS");
-  static_assert(BKIND != B_BF16, "8-bit weights only");
-  static_assert(BM == 256 || (BM == 128 && !MX), "256-row tiles, or 128 for 8-bit weights");
+  static_assert(BM == 256 || (BM == 128 && !MX), "256-row tiles, or 128 without MX activations");
 };
 
 template <int BKIND, int EPI, int BM_ = 256>
@@ -797,7 +818,8 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   constexpr int A_DMA = Cfg::A_DMA, B_DMA = Cfg::B_DMA;
   constexpr int EPI_ROWB = Cfg::EPI_ROWB, EPI_WAVE = Cfg::EPI_WAVE;
   constexpr bool RESID = EPI == LTX_GEMM_EPI_RESIDUAL || EPI == LTX_GEMM_EPI_RESIDUAL_ROUND;
-  constexpr bool MX = Cfg::MX;
+  constexpr bool MX = Cfg::MX, BF = Cfg::BF;
+  constexpr int STAGES = Cfg::STAGES, AHEAD = STAGES - 1;
   __shared__ __attribute__((aligned(1024))) char lds[Cfg::TOTAL];
 
   const int tid = threadIdx.x;
@@ -834,17 +856,19 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   // -- no vector instructions per load (vector instructions of one wave take
   // matrix-pipe slots from the other).  The descriptors' record counts bound
   // every load to its operand (g8_ok checks the 32-bit extents).
-  const int a_records = (int)((int64_t)p.M * p.lda * (MX ? 1 : 2)), b_records = (int)((int64_t)p.N * p.ldb);
+  const int a_records = (int)((int64_t)p.M * p.lda * (MX ? 1 : 2)),
+            b_records = (int)((int64_t)p.N * p.ldb * (BF ? 2 : 1));
   uint32_t a_src[A_DMA];
 #pragma unroll
   for (int d = 0; d < A_DMA; ++d) {
-    if constexpr (MX) {
-      // activation codes: 64-byte rows laid out like the weight codes
+    if constexpr (MX || BF) {
+      // activation codes (MX) or 32-deep bf16 rows (BF): 64-byte rows laid
+      // out like the weight codes
       const int r = 16 * (8 * d + wave) + (lane >> 2);
       int gm = m0 + r;
       gm = gm < p.M ? gm : p.M - 1;
       const int chunk = (lane & 3) ^ ((r >> 2) & 3);
-      a_src[d] = (uint32_t)((int64_t)gm * p.lda) + chunk * 16;
+      a_src[d] = (uint32_t)((int64_t)gm * p.lda * (MX ? 1 : 2)) + chunk * 16;
     } else {
       const int r = 8 * (8 * d + wave) + (lane >> 3);
       int gm = m0 + r;
@@ -860,7 +884,7 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
     int gn = n0 + r;
     gn = gn < p.N ? gn : p.N - 1;
     const int chunk = (lane & 3) ^ ((r >> 2) & 3);
-    b_src[d] = (uint32_t)((int64_t)gn * p.ldb) + chunk * 16;
+    b_src[d] = (uint32_t)((int64_t)gn * p.ldb * (BF ? 2 : 1)) + chunk * 16;
   }
   auto dma_stage = [&](int kt, int buf) __attribute__((always_inline)) {
     char* As = lds + buf * A_BYTES;
@@ -870,7 +894,7 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
       buffer_dma16(p.A, a_records, a_src[d], kt * Cfg::A_ROWB, As + (8 * d + wave) * 1024);
 #pragma unroll
     for (int d = 0; d < B_DMA; ++d)
-      buffer_dma16(p.B, b_records, b_src[d], kt * Cfg::BK, Bs + (8 * d + wave) * 1024);
+      buffer_dma16(p.B, b_records, b_src[d], kt * Cfg::B_ROWB, Bs + (8 * d + wave) * 1024);
   };
 
   // ---- per-lane fragment read bases: LDS byte addresses of the lane's first
@@ -890,7 +914,9 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
 #pragma unroll
   for (int pp = 0; pp < 2; ++pp)
     b_base[pp] = B_REGION + (wn * WN + fr) * B_ROWB + (((2 * pp + h) ^ b_swz) * 16);
-  // MX: activation code fragments, read like the weight codes
+  // MX: activation code fragments, read like the weight codes; BF: both
+  // operands' fragments of k-step s (k = 16 s + 8 h + [0, 8)) at a_mx[s] /
+  // b_base[s]
   int a_mx[2];
 #pragma unroll
   for (int pp = 0; pp < 2; ++pp) a_mx[pp] = (wm * WM + fr) * A_ROWB + (((2 * pp + h) ^ b_swz) * 16);
@@ -944,9 +970,10 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   constexpr int VM_DMA = A_DMA + B_DMA;
   constexpr int VM_SCALES = SCALED ? 1 : 0;
 
-  bf16x8 fa[MX ? 1 : 4][TM];  // A fragments of the stage's four k-steps
-  u32x4 fb[2][TN];   // weight codes of the stage's two k-step pairs (16 per lane)
-  u32x4 fa8[2][MX ? TM : 1];  // MX: activation codes, as the weight codes
+  bf16x8 fa[(MX || BF) ? 1 : 4][TM];  // A fragments of the stage's four k-steps
+  u32x4 fb[2][TN];   // weight codes of the stage's two k-step pairs (16 per lane); BF: bf16
+                     // weight fragments of its two k-steps
+  u32x4 fa8[2][(MX || BF) ? TM : 1];  // MX: activation codes, as the weight codes; BF: bf16 fragments
   uint32_t sca[MX ? TM : 1];  // MX: this stage pair's E8M0 bytes of the lane's activation rows
   // fragment reads of stage kt, which sits in buffer BUF (compile-time)
   auto read_stage = [&](int kt, auto bufc) __attribute__((always_inline)) {
@@ -956,10 +983,12 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
 #pragma unroll
       for (int j = 0; j < TN; ++j) scw[j] = *reinterpret_cast<const uint32_t*>(lds + sa + j * 32 * 16);
     }
-    if constexpr (MX) {
-      const int sa = asc_read + ((kt >> 3) & 1) * Cfg::SC_OCT + ((kt & 7) >> 1) * 4;
+    if constexpr (MX || BF) {
+      if constexpr (MX) {
+        const int sa = asc_read + ((kt >> 3) & 1) * Cfg::SC_OCT + ((kt & 7) >> 1) * 4;
 #pragma unroll
-      for (int i = 0; i < TM; ++i) sca[i] = *reinterpret_cast<const uint32_t*>(lds + sa + i * 32 * 16);
+        for (int i = 0; i < TM; ++i) sca[i] = *reinterpret_cast<const uint32_t*>(lds + sa + i * 32 * 16);
+      }
 #pragma unroll
       for (int pp = 0; pp < 2; ++pp) {
 #pragma unroll
@@ -1043,7 +1072,7 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   // end of the memory cluster of stage kt (its fragment reads have landed):
   // the stage's scales and fragments 0 and 1 (MX: nothing to decode)
   auto prep_stage = [&](int kt) __attribute__((always_inline)) {
-    if constexpr (MX) return;
+    if constexpr (MX || BF) return;
 #pragma unroll
     for (int j = 0; j < TN; ++j) decode(kt, 0, j);
     bq[0] = frag_dequant(0);
@@ -1077,6 +1106,16 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
           acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w, a, acc[i][j], 0, 0, 0, ws[j], 0, as[i]);
         }
       }
+    } else if constexpr (BF) {
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fb[st][j]),
+                                                                __builtin_bit_cast(bf16x8, fa8[st][i]),
+                                                                acc[i][j], 0, 0, 0);
     } else {
 #pragma unroll
       for (int f = 0; f < NF; ++f) {
@@ -1089,11 +1128,14 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
     }
   };
 
-  // ---- prologue: scales of octet 0, stages 0 and 1 in flight, then one
+  // ---- prologue: scales of octet 0, stages 0 .. AHEAD-1 in flight, then one
   // barrier for all waves
   dma_scales(0);
   dma_stage(0, 0);
   if (KT > 1) dma_stage(1, 1);
+  static_for<2, AHEAD>([&](auto ic) {
+    if (KT > decltype(ic)::value) dma_stage(decltype(ic)::value, decltype(ic)::value);
+  });
   wait_vmcnt<0>();
   __syncthreads();
   if (grp == 1) barrier_nofence();  // group 1 runs half a stage behind
@@ -1101,10 +1143,10 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   // Clusters are whole stages.  Stage s is first read by group 0's memory
   // cluster of stage s (global half-stage 2s), so its data must be in LDS by
   // the barrier before it.  The direct loads of stage s are issued in the
-  // memory clusters of stage s-2; each group waits for them in its last
+  // memory clusters of stage s-AHEAD; each group waits for them in its last
   // cluster before that barrier -- group 0 at the end of its compute cluster
   // of stage s-1, group 1 at the end of its memory cluster of stage s-1 --
-  // leaving only that stage's own loads in flight.  Past the last stage the
+  // leaving only the loads of the AHEAD-1 later stages in flight.  Past the last stage the
   // direct loads re-read stage KT-1 into the buffer nobody reads any more,
   // so every stage issues the same loads and the waits are exact.  The scales
   // of octet o+1 go out (group 0) with stage 8o's loads.
@@ -1117,13 +1159,13 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
     const bool oct_start = SCALED && (kt & 7) == 0;
     // memory cluster (MX: group 1 moves the activations' scale octets)
     if ((GRP == 0 || MX) && oct_start) dma_scales((kt >> 3) + 1);
-    dma_stage(kt + 2 < KT ? kt + 2 : KT - 1, (BUF + 2) % kG8Stages);
+    dma_stage(kt + AHEAD < KT ? kt + AHEAD : KT - 1, (BUF + AHEAD) % STAGES);
     if (live) read_stage(kt, bufc);
     wait_lgkmcnt0();
     if (live) prep_stage(kt);
     if (GRP == 1) {
       if (MX && oct_start) wait_vmcnt<VM_DMA + VM_SCALES>();
-      else wait_vmcnt<VM_DMA>();
+      else wait_vmcnt<(AHEAD - 1) * VM_DMA>();
     }
     barrier_nofence();
     // compute cluster
@@ -1132,27 +1174,26 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
     __builtin_amdgcn_s_setprio(0);
     if (GRP == 0) {
       if (oct_start) wait_vmcnt<VM_DMA + VM_SCALES>();
-      else wait_vmcnt<VM_DMA>();
+      else wait_vmcnt<(AHEAD - 1) * VM_DMA>();
     }
     barrier_nofence();
   };
-  typedef std::integral_constant<int, 0> B0;
-  typedef std::integral_constant<int, 1> B1;
-  typedef std::integral_constant<int, 2> B2;
+  // the loop unrolled over one turn of the ring, then the remainder (stage
+  // kt + i sits in buffer i)
   auto main_loop = [&](auto grpc) __attribute__((always_inline)) {
     int kt = 0;
-    for (; kt + 2 < KT; kt += 3) {
-      stage_iter(kt, B0{}, grpc);
-      stage_iter(kt + 1, B1{}, grpc);
-      stage_iter(kt + 2, B2{}, grpc);
-    }
-    if (kt < KT) stage_iter(kt, B0{}, grpc);
-    if (kt + 1 < KT) stage_iter(kt + 1, B1{}, grpc);
+    for (; kt + STAGES - 1 < KT; kt += STAGES)
+      static_for<0, STAGES>([&](auto ic) { stage_iter(kt + decltype(ic)::value, ic, grpc); });
+    static_for<0, STAGES - 1>([&](auto ic) {
+      if (kt + decltype(ic)::value < KT) stage_iter(kt + decltype(ic)::value, ic, grpc);
+    });
   };
   if (grp == 0) main_loop(std::integral_constant<int, 0>{});
   else main_loop(std::integral_constant<int, 1>{});
   if (grp == 0) barrier_nofence();
   wait_vmcnt<0>();
+  // column values inside the ring: every wave's last direct loads have landed
+  if constexpr (Cfg::COL_IN_RING) __syncthreads();
 
   // ---- epilogue (every wave is past its last LDS fragment read)
   if (tid < BN) {
@@ -1303,14 +1344,15 @@ static void launch_tile(GemmArgs p, hipStream_t s) {
   gemm_kernel<BM, BN, BK, STAGES, BKIND, EPI, SWZ, LOADER><<<p.tiles_m * p.tiles_n, kGemmThreads, 0, s>>>(p);
 }
 
-// Whether the 8-wave kernel takes a problem: 8-bit weights; for MXFP8 whole
-// eight-stage scale octets (K % 512) in 16-byte aligned pieces.
+// Whether the 8-wave kernel takes a problem: operand extents within its 31-bit
+// buffer record counts; for MXFP8 whole eight-stage scale octets (K % 512) in
+// 16-byte aligned pieces.
 template <int BKIND>
 static bool g8_ok(const GemmArgs& p) {
-  if (BKIND == B_BF16) return false;
   // operand extents are 31-bit buffer record counts in the kernel
   if ((int64_t)p.M * p.lda * (BKIND == B_MX ? 1 : 2) >= ((int64_t)1 << 31) ||
-      (int64_t)p.N * p.ldb >= ((int64_t)1 << 31) || (int64_t)p.N * p.ld_scale >= ((int64_t)1 << 31))
+      (int64_t)p.N * p.ldb * (BKIND == B_BF16 ? 2 : 1) >= ((int64_t)1 << 31) ||
+      (int64_t)p.N * p.ld_scale >= ((int64_t)1 << 31))
     return false;
   if (BKIND == B_MX)
     return p.K % 512 == 0 && p.ld_scale % 16 == 0 && ((uintptr_t)p.bscale & 15u) == 0 &&
@@ -1323,8 +1365,8 @@ static bool g8_ok(const GemmArgs& p) {
 
 // Tile shapes (all K step 64): 256x256 and 128x128 with the register-staged
 // loader (1 and 2; 128x128 runs two workgroups per CU), 256x256 with the
-// LDS-DMA loader (3), 256x128 register-staged (4), and the 8-wave kernel for
-// 8-bit weights with 256x256 (5) or 128x256 tiles (6).
+// LDS-DMA loader (3), 256x128 register-staged (4), and the 8-wave kernel with
+// 256x256 (5) or 128x256 tiles (6).
 template <int BKIND, int EPI>
 static int launch_epi_w(const GemmArgs& p, int tile, hipStream_t s) {
   if (tile == 0) {
@@ -1340,19 +1382,21 @@ static int launch_epi_w(const GemmArgs& p, int tile, hipStream_t s) {
     // 61 us alone, but the step 1.0-1.6 ms slower in two A/B pairs -- 48 %
     // more CU time per launch, which the audio stream's work beside it then
     // lacks: explicit only, LTX_GEMM_TILE_G8_128.)
+    // bf16 weights (32-deep stages) take it where it measured faster at
+    // M = 3456: products wider than deep (FF up 429 -> 411 us, QKV 312 ->
+    // 298, A2V out 60.0 -> 59.1) and the partial round of the A2V query
+    // projection (90 -> 72 us); the square and the FF down products stay on
+    // the 4-wave kernel (4096^2 106 vs 107 us, FF down 394 vs 419).
     const int64_t big = (int64_t)((p.M + 255) / 256) * ((p.N + 255) / 256);
-    const bool g8 = (BKIND == B_MXFP8 || BKIND == B_INT8) && g8_ok<BKIND>(p);
+    const bool g8 = (BKIND == B_MXFP8 || BKIND == B_INT8 || (BKIND == B_BF16 && (p.N > p.K || big < 160))) &&
+                    g8_ok<BKIND>(p);
     tile = big >= 160 ? (g8 ? 5 : 1) : (big >= 100 && g8 ? 5 : 2);
   }
   if (tile == 5 || tile == 6) {
-    if constexpr (BKIND != B_BF16) {
-      if (!g8_ok<BKIND>(p)) return LTX_ERR_UNSUPPORTED;
-      if (tile == 5) launch_g8<BKIND, EPI>(p, s);
-      else launch_g8<BKIND, EPI, 128>(p, s);
-      return LTX_OK;
-    } else {
-      return LTX_ERR_UNSUPPORTED;
-    }
+    if (!g8_ok<BKIND>(p)) return LTX_ERR_UNSUPPORTED;
+    if (tile == 5) launch_g8<BKIND, EPI>(p, s);
+    else launch_g8<BKIND, EPI, 128>(p, s);
+    return LTX_OK;
   }
   if (tile == 1)
     launch_tile<256, 256, 64, 2, BKIND, EPI, 0, LOAD_REG>(p, s);
