@@ -112,18 +112,20 @@ def parse_args(argv=None):
     ap.add_argument("--no-class-stamps", action="store_true",
                     help="stamp only the FF-up launches in the timed graphs (no per-class GEMM timing)")
     ap.add_argument("--cpu-runs", type=int, default=5, help="timed oracle block runs after one warmup")
-    ap.add_argument("--counter-workload", choices=["ff-up", "ff-up-vs-library", "copy", "fused-ops", "attention"],
+    ap.add_argument("--counter-workload",
+                    choices=["ff-up", "ff-up-vs-library", "copy", "fused-ops", "attention", "audio-rows"],
                     default=None,
                     help="run only a short workload for rocprofv3 --pmc passes and exit: the video FF "
                          "up-projection GEMM (4 launches, --weights format), the three row kernels (adaln, "
                          "gated add, QK-norm + RoPE; 4 cache-cold launches each), the video self-attention at "
                          "3456 and 6144 tokens and the 3456 x 256 text cross-attention (4 launches each, 32 "
-                         "heads of 128, gated) or a 1 GiB device copy (3 launches, the FETCH_SIZE / WRITE_SIZE "
-                         "calibration)")
+                         "heads of 128, gated), the audio stream's four 68-row MXFP8 products (4 launches each "
+                         "on distinct weights, automatic split-K path then the one-launch few-row kernel) or a "
+                         "1 GiB device copy (3 launches, the FETCH_SIZE / WRITE_SIZE calibration)")
     ap.add_argument("--counter-tile", choices=["auto", "256", "g8"], default="auto",
                     help="tile choice of the ff-up counter workload: the library's automatic choice (the "
-                         "8-wave kernel for MXFP8 and int8, the 4-wave 256x256 kernel for bf16), the 4-wave "
-                         "256x256 kernel, or the 8-wave kernel")
+                         "8-wave kernel for every format at this shape), the 4-wave 256x256 kernel, or the "
+                         "8-wave kernel")
     return ap.parse_args(argv)
 
 
@@ -155,6 +157,28 @@ def counter_workload(kind: str, weights: str, tile_name: str = "auto") -> None:
             out = torch.empty((tq, 4096), dtype=torch.bfloat16, device="cuda")
             for _ in range(4):
                 flash_attention(q, k, v, 32, gate=gate, out=out)
+    elif kind == "audio-rows":
+        # the audio stream's four 68-row products (QKV + head gates, out, FF up,
+        # FF down; MXFP8 weights), each on four weight copies so every launch
+        # reads its weights from HBM as in the step: first through the
+        # library's automatic path (split-K tile kernel + epilogue kernel),
+        # then through the one-launch few-row kernel
+        g = torch.Generator(device="cuda").manual_seed(0)
+        shapes = ((2048, 6176, gemm.EPI_BIAS), (2048, 2048, gemm.EPI_RESIDUAL), (2048, 8192, gemm.EPI_GELU),
+                  (8192, 2048, gemm.EPI_RESIDUAL))
+        for rows in (False, True):
+            for K, N, epi in shapes:
+                x = torch.randn((68, K), generator=g, device="cuda").bfloat16()
+                res = torch.randn((68, N), generator=g, device="cuda").bfloat16()
+                gate = torch.randn(N, generator=g, device="cuda")
+                wts = [gemm.make_weight((torch.randn((N, K), generator=g, device="cuda") * 0.02).bfloat16(),
+                                        torch.zeros(N, device="cuda"), kind="mxfp8") for _ in range(4)]
+                kw = dict(out=res, residual=res, gate=gate) if epi == gemm.EPI_RESIDUAL else {}
+                for wt in wts:
+                    if rows:
+                        gemm.linear_rows(x, wt, epilogue=epi, **kw)
+                    else:
+                        gemm.linear(x, wt, epilogue=epi, **kw)
     elif kind == "copy":
         src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
