@@ -52,19 +52,36 @@ constexpr int kAttnKB = 64;              // keys per stage
 constexpr int kNumXcdAttn = 8;
 constexpr float kLazyMax = 8.0f;         // log2 headroom before the max is raised
 
-typedef __attribute__((address_space(3))) void* lds_ptr_a;
+typedef __attribute__((address_space(3))) char* lds_cptr_a;
 
 // 16 bytes per lane from base + voff to LDS at lds_dst + 16 * lane: a buffer
 // load with the lds modifier; a per-lane offset voff at or past num_records
 // loads zeros.  The range check covers the vector offset only (a scalar
 // offset is added after it, unchecked), so a key block's advance goes into
 // the descriptor's base and record count, never into the scalar offset.  The
-// descriptor (untyped, 32-bit data format) is built from wave-uniform values,
-// so it lives in scalar registers.
-__device__ __forceinline__ void attn_dma16(const char* base, int num_records, uint32_t voff, char* lds_dst) {
-  const __amdgpu_buffer_rsrc_t r =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, num_records, 0x00020000);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_a)lds_dst, 16, voff, 0, 0, 0);
+// descriptor (untyped: base, stride 0, record count, word 3 as for every
+// buffer load of this library) is built from wave-uniform values in scalar
+// registers; M0 holds the wave's LDS destination (a byte address in LDS).
+// Issued as inline asm: the compiler's wait insertion treats the transposing
+// LDS reads (ds_read_b64_tr_b16) as aliasing every LDS load in flight and put
+// a full vmcnt(0) before the first V read after each stage's loads -- a wait
+// for loads meant for the stages after it.  The kernel orders these loads
+// itself: every stage sync waits vmcnt(0) before its barrier, and a block is
+// read only after the sync that follows its loads.  s_nop 0: one wait state
+// between the M0 write and the LDS-destination load.
+__device__ __forceinline__ uint64_t uniform_addr(const void* p) {
+  const uint64_t a = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a), hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ void attn_dma16(uint64_t base, int num_records, uint32_t voff, uint32_t lds_dst) {
+  i32x4 rsrc;
+  rsrc[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)base);
+  rsrc[1] = __builtin_amdgcn_readfirstlane((int)(uint32_t)((base >> 32) & 0xffffu));
+  rsrc[2] = __builtin_amdgcn_readfirstlane(num_records);
+  rsrc[3] = 0x00020000;
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_dst);
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(m0));
 }
 
 // Position of key j (0..15 within its 16-key group) in the permuted Vt row:
@@ -158,7 +175,8 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
   constexpr int RING = (SPLIT || WAVES == kAttnSplitWaves) ? 2 : 4;
   __shared__ __attribute__((aligned(1024))) char lds[RING * (K_BYTES + V_BYTES)];
   char* const Ks0 = lds;
-  char* const Vs0 = lds + RING * K_BYTES;
+  // LDS byte addresses of the rings (the direct loads' destinations)
+  const uint32_t ks_lds = (uint32_t)(uintptr_t)(lds_cptr_a)lds, vs_lds = ks_lds + RING * K_BYTES;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hh = lane >> 5, l32 = lane & 31;
@@ -178,6 +196,9 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
 
   const bf16* Kh = K + (int64_t)head * DH;
   const bf16* Vh = VROW ? V + (int64_t)head * DH : V + (int64_t)head * DH * v_ld;
+  // the head's K / V base addresses in scalar registers (the direct loads'
+  // descriptors are built from them per key block)
+  const uint64_t kh_addr = uniform_addr(Kh), vh_addr = uniform_addr(Vh);
 
   // ---- Q^T fragments: lane holds Q[q][dstep*16 + hh*8 .. +8] for its query
   bf16x8 qf[DSTEPS];
@@ -238,15 +259,15 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
   const int k_step = (int)(kAttnKB * k_rs * 2);
   const int v_step = VROW ? (int)(kAttnKB * v_ld * 2) : kAttnKB * 2;
   auto issue_k = [&](int kb, int buf) {
-    char* Ks = Ks0 + buf * K_BYTES;
-    const char* base = reinterpret_cast<const char*>(Kh) + (int64_t)kb * k_step;
+    const uint32_t Ks = ks_lds + buf * K_BYTES;
+    const uint64_t base = kh_addr + (uint64_t)((int64_t)kb * k_step);
     const int rec = k_records - kb * k_step;
 #pragma unroll
     for (int i = 0; i < K_DMA; ++i) attn_dma16(base, rec, k_voff[i], Ks + (WAVES * i + wave) * 1024);
   };
   auto issue_v = [&](int kb, int buf) {
-    char* Vs = Vs0 + buf * V_BYTES;
-    const char* base = reinterpret_cast<const char*>(Vh) + (int64_t)kb * v_step;
+    const uint32_t Vs = vs_lds + buf * V_BYTES;
+    const uint64_t base = vh_addr + (uint64_t)((int64_t)kb * v_step);
     const int rec = v_records - kb * v_step;
 #pragma unroll
     for (int i = 0; i < V_DMA; ++i) attn_dma16(base, rec, v_voff[i], Vs + (WAVES * i + wave) * 1024);
