@@ -46,15 +46,79 @@ def _positions_digest(positions: np.ndarray) -> tuple:
 
 @dataclass
 class Modality:
-    """Input modality (model.py:103-118): patchified latent (B, T, 128) bf16,
-    text context (B, S, D) bf16, scalar sigma, positions (B, n_dims, T, 2)."""
+    """Input modality (model.py:103-118): patchified latent (B, T, 128),
+    text context (B, S, D), context mask (B, S) -- boolean (True = attend)
+    or additive -- or None, timesteps (B,) / (B, T) / a scalar, positions
+    (B, n_dims, T, 2), and the prompt-AdaLN sigma (B,) or None (then the
+    timesteps)."""
 
     latent: torch.Tensor
     context: torch.Tensor
-    sigma: float
+    context_mask: torch.Tensor | None
+    timesteps: torch.Tensor | float
     positions: np.ndarray
     enabled: bool = True
-    context_mask: torch.Tensor | None = None
+    sigma: torch.Tensor | float | None = None
+
+
+# An additive context-mask value at or below this excludes its key: the
+# softmax weight exp(s - m + v) of such a key underflows to exactly 0 in fp32
+# for any score range the attention sees, as for the reference's boolean
+# masks, which become -3.4e38 (model.py:208-250).
+MASK_EXCLUDE = -1.0e4
+
+
+def _uniform_value(t, what: str) -> float:
+    """The one value of a scalar / (B,) / (B, T) timestep tensor; distinct
+    values per sample or per token are not supported (the modulation rows of
+    a forward are shared by all of its tokens)."""
+    if isinstance(t, (int, float)):
+        return float(t)
+    v = torch.as_tensor(t).detach().float().reshape(-1).cpu()
+    if v.numel() == 0:
+        raise ValueError(f"empty {what}")
+    if not bool((v == v[0]).all()):
+        raise NotImplementedError(f"{what} differ across samples or tokens: one timestep per forward is "
+                                  "supported (the text-to-video path's uniform denoise mask)")
+    return float(v[0])
+
+
+def context_keep_rows(mask: torch.Tensor | None, batch: int, length: int) -> list[torch.Tensor | None]:
+    """Per sample, the context rows a (B, S) mask keeps (None: all of them).
+
+    Boolean masks keep their True entries; additive float masks keep 0 and
+    drop values <= MASK_EXCLUDE -- a dropped key's softmax weight is exactly 0,
+    so attending over the kept rows only gives the masked attention's result
+    (model.py:208-250 turns a boolean mask into -3.4e38 additive entries).
+    Other additive values, masks that drop every key of a sample (the
+    reference then spreads the weights uniformly) and (B, 1, S, S) masks are
+    not supported."""
+    if mask is None:
+        return [None] * batch
+    m = torch.as_tensor(mask)
+    if m.dim() == 1:
+        m = m[None]
+    if m.dim() != 2 or m.shape[-1] != length or m.shape[0] not in (1, batch):
+        raise NotImplementedError(f"context mask of shape {tuple(m.shape)}: (B, S) masks over the {length} "
+                                  "context tokens are supported")
+    m = m.detach().cpu()
+    if m.dtype == torch.bool:
+        keep = m
+    elif m.is_floating_point():
+        mf = m.float()
+        if not bool(((mf == 0) | (mf <= MASK_EXCLUDE)).all()):
+            raise NotImplementedError("additive context-mask values other than 0 and <= -1e4")
+        keep = mf == 0
+    else:
+        keep = m != 0
+    out = []
+    for b in range(batch):
+        row = keep[b if keep.shape[0] == batch else 0]
+        n = int(row.sum())
+        if n == 0:
+            raise NotImplementedError(f"context mask of sample {b} excludes every key")
+        out.append(None if n == length else torch.nonzero(row).reshape(-1))
+    return out
 
 
 class LTXModel:
@@ -222,15 +286,30 @@ class LTXModel:
         shared (S, D), ``perturbations`` holds one config per pass, and the
         velocities come back as (passes, T, 128).  The batched passes of a
         guided step (av_pipeline.py:688-717 runs them one after another).
+        Latents of shape (B, T, 128) are B samples at one timestep, run the
+        same way (passes = B), each on its own latents.
         """
         vpe, vxpe, ape, axpe = pes
-        run_audio = self.audio_config is not None and audio_latent is not None and audio_latent.shape[0] > 0
+        if video_latent.dim() == 3 and video_latent.shape[0] == 1:  # one sample: the 2-D form
+            video_latent = video_latent[0]
+            audio_latent = audio_latent[0] if audio_latent is not None and audio_latent.dim() == 3 else audio_latent
+        if video_latent.dim() == 3:
+            if passes not in (1, video_latent.shape[0]):
+                raise ValueError(f"{video_latent.shape[0]} latent samples for {passes} passes")
+            passes = video_latent.shape[0]
+        run_audio = self.audio_config is not None and audio_latent is not None and audio_latent.shape[-2] > 0
 
         def stacked(x):  # (T, C) -> (passes, T, C)
             return x if passes == 1 else x.unsqueeze(0).expand(passes, *x.shape).contiguous()
 
+        def project(latent, proj):  # (T, 128) shared by the passes, or (passes, T, 128)
+            if latent.dim() == 3:
+                return gemm.linear(latent.reshape(-1, latent.shape[-1]).contiguous(),
+                                   proj).view(passes, latent.shape[1], -1)
+            return stacked(gemm.linear(latent, proj))
+
         # preprocess
-        vx = stacked(gemm.linear(video_latent, self.patchify_proj))
+        vx = project(video_latent, self.patchify_proj)
         self._timestep_rows(sigma_dev, sigma_dev, video=True)
         stream = _lib.stream_of(vx)
         _lib.call("ltx_broadcast_add_f32", self.video_tables.data_ptr(), self._temb_v.data_ptr(),
@@ -239,7 +318,7 @@ class LTXModel:
                                 cross_positional_embeddings=vxpe)
         audio = None
         if run_audio:
-            ax = stacked(gemm.linear(audio_latent, self.audio_patchify_proj))
+            ax = project(audio_latent, self.audio_patchify_proj)
             self._timestep_rows(sigma_dev, sigma_dev, video=False)
             _lib.call("ltx_broadcast_add_f32", self.audio_tables.data_ptr(), self._temb_a.data_ptr(),
                       self._ada_a.data_ptr(), self.num_layers, ADA_ROWS * self.audio_dim, stream)
@@ -279,9 +358,130 @@ class LTXModel:
                                          self.audio_proj_out))
         return v_out, a_out
 
+    def __call__(self, video: Modality | None = None, audio: Modality | None = None,
+                 perturbations=None) -> tuple[torch.Tensor, torch.Tensor]:
+        """The reference's forward on ``Modality`` inputs (model.py:1344-1486):
+        (video velocity (B, T, 128), audio velocity (B, Ta, 128)); without an
+        audio modality (or with ``enabled=False`` / no tokens) the audio
+        velocity is an empty (B, 0, 128) tensor, as there.
+
+        Covered: B >= 1 samples at one timestep (timesteps, sigma and both
+        modalities share one value), positions shared by the samples, and
+        (B, S) context masks -- the masked keys are dropped from the context
+        (``context_keep_rows``), which gives the masked softmax exactly.  The
+        samples run as one forward (tokens stacked by rows) when their kept
+        contexts have equal lengths, else one after another; ``perturbations``
+        holds one config per sample.  Per-sample or per-token timesteps (the
+        image-conditioned denoise masks) raise NotImplementedError.
+        """
+        if video is None:
+            raise ValueError("Video modality required for video-enabled model")
+        dev = self.device
+
+        def as3(t, dtype=torch.bfloat16):
+            t = torch.as_tensor(t)
+            return (t[None] if t.dim() == 2 else t).to(device=dev, dtype=dtype)
+
+        vlat, vctx = as3(video.latent), as3(video.context)
+        batch = vlat.shape[0]
+        if vctx.shape[0] not in (1, batch):
+            raise ValueError(f"{vctx.shape[0]} video contexts for {batch} samples")
+        use_audio = (audio is not None and audio.enabled and self.audio_config is not None
+                     and torch.as_tensor(audio.latent).shape[-2] > 0)
+        values = [_uniform_value(video.timesteps, "video timesteps")]
+        if video.sigma is not None:
+            values.append(_uniform_value(video.sigma, "video sigma"))
+        alat = actx = None
+        if use_audio:
+            alat, actx = as3(audio.latent), as3(audio.context)
+            if alat.shape[0] != batch or actx.shape[0] not in (1, batch):
+                raise ValueError("audio latents / contexts do not match the video samples")
+            values.append(_uniform_value(audio.timesteps, "audio timesteps"))
+            if audio.sigma is not None:
+                values.append(_uniform_value(audio.sigma, "audio sigma"))
+        if any(v != values[0] for v in values):
+            raise NotImplementedError("video / audio timesteps and sigmas differ: one timestep per forward "
+                                      "is supported")
+        sigma_dev = torch.tensor([values[0]], dtype=torch.float32, device=dev)
+
+        def shared_positions(pos, what):
+            if pos is None:
+                return None
+            pos = pos.detach().cpu().numpy() if torch.is_tensor(pos) else np.asarray(pos)
+            if pos.ndim >= 1 and pos.shape[0] > 1 and not all(np.array_equal(pos[0], p) for p in pos[1:]):
+                raise NotImplementedError(f"{what} positions differ across samples")
+            return pos[0:1] if pos.ndim >= 1 and pos.shape[0] > 1 else pos
+
+        pes = self.rope(shared_positions(video.positions, "video"),
+                        shared_positions(audio.positions, "audio") if use_audio else None)
+        vkeep = context_keep_rows(video.context_mask, batch, vctx.shape[1])
+        akeep = context_keep_rows(audio.context_mask, batch, actx.shape[1]) if use_audio else [None] * batch
+
+        def ctx_of(ctx, keep, b):
+            c = ctx[b if ctx.shape[0] == batch else 0]
+            return c if keep[b] is None else c.index_select(0, keep[b].to(dev)).contiguous()
+
+        vctxs = [ctx_of(vctx, vkeep, b) for b in range(batch)]
+        actxs = [ctx_of(actx, akeep, b) for b in range(batch)] if use_audio else None
+        same = len({c.shape[0] for c in vctxs}) == 1 and (not use_audio or len({c.shape[0] for c in actxs}) == 1)
+        if batch == 1 or same:
+            v, a = self.velocity(vlat if batch > 1 else vlat[0],
+                                 torch.stack(vctxs) if batch > 1 else vctxs[0], sigma_dev, pes,
+                                 (alat if batch > 1 else alat[0]) if use_audio else None,
+                                 (torch.stack(actxs) if batch > 1 else actxs[0]) if use_audio else None,
+                                 perturbations=perturbations, passes=batch)
+            v = v if batch > 1 else v[None]
+            a = (a if batch > 1 else a[None]) if use_audio else None
+        else:
+            from ...components.perturbations import BatchedPerturbationConfig
+
+            vs, as_ = [], []
+            for b in range(batch):
+                pert = None
+                if perturbations is not None:
+                    pert = BatchedPerturbationConfig([perturbations.perturbations[b]])
+                vb, ab = self.velocity(vlat[b], vctxs[b], sigma_dev, pes, alat[b] if use_audio else None,
+                                       actxs[b] if use_audio else None, perturbations=pert)
+                vs.append(vb)
+                as_.append(ab)
+            v = torch.stack(vs)
+            a = torch.stack(as_) if use_audio else None
+        if a is None:
+            a = torch.zeros((batch, 0, AUDIO_IN_CHANNELS), dtype=torch.bfloat16, device=dev)
+        return v, a
+
     def _output(self, x: torch.Tensor, table: torch.Tensor, emb: torch.Tensor, proj: gemm.LinearWeight) -> torch.Tensor:
         t, d = x.shape
         h = torch.empty_like(x)
         _lib.call("ltx_output_norm_modulate_bf16", x.data_ptr(), d, table.data_ptr(), emb.data_ptr(), h.data_ptr(),
                   d, t, d, float(self.norm_eps), _lib.stream_of(x))
         return gemm.linear(h, proj)
+
+
+class X0Model:
+    """Denoised outputs instead of velocities (model.py:1489-1542):
+    ``latent - timestep * velocity`` per modality in fp32, on the device
+    (``ltx_x0_from_velocity_f32``); the video-only case returns the video
+    prediction alone, as there."""
+
+    def __init__(self, velocity_model: LTXModel):
+        self.velocity_model = velocity_model
+
+    def __call__(self, video: Modality | None = None, audio: Modality | None = None, perturbations=None):
+        from ...components.diffusion_steps import to_denoised
+
+        v, a = self.velocity_model(video, audio, perturbations=perturbations)
+        dev = self.velocity_model.device
+
+        def denoised(mod, vel):
+            lat = torch.as_tensor(mod.latent)
+            lat = (lat[None] if lat.dim() == 2 else lat).to(device=dev, dtype=torch.bfloat16)
+            return to_denoised(lat.contiguous(), vel.contiguous(), _uniform_value(mod.timesteps, "timesteps"))
+
+        dv = denoised(video, v)
+        if audio is None:
+            return dv
+        if a.shape[1] == 0:
+            return dv, torch.zeros(a.shape, dtype=torch.float32, device=dev)
+        return dv, denoised(audio, a)
+

@@ -1,0 +1,153 @@
+"""GPU tests of the Modality-level forward (``LTXModel.__call__``,
+model/transformer/model.py:1344-1486) and ``X0Model`` (:1489-1542).
+
+A 2-block full-width AV model on a small grid (48 video tokens, 12 audio
+tokens, 16 text tokens):
+
+* B = 2 samples (own latents and contexts, one timestep) as one stacked
+  forward: each sample's velocity equals its own B = 1 forward to fp32
+  summation order (the stacked rows change the GEMM tiling), and sample 1
+  matches the oracle's ``model_velocity``;
+* (B, S) context masks: a boolean padding mask and an additive 0 / -inf mask
+  with holes give the same bits as the forward on the kept context rows
+  (a dropped key's softmax weight is exactly 0), alone and for samples with
+  different kept lengths (then run one after another);
+* X0Model: ``latent - sigma * velocity`` in fp32, bit for bit, with and
+  without the audio modality; the audio velocity of a video-only call is an
+  empty (B, 0, 128) tensor.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _util import bf16_from_torch, cos_sim, max_rel_err
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _setup(seed=11):
+    from ltx_amd.model.transformer.model import LTXModel
+    from ltx_amd.pipeline import DenoiseState
+
+    model = LTXModel(num_layers=2, weight_format="mxfp8", seed=seed)
+    states = [DenoiseState(model, height=128, width=192, frames=9, text_tokens=16, audio_frames=12, seed=s)
+              for s in (5, 6)]
+    return model, states
+
+
+def _mod(st, latent=None, context=None, mask=None, audio=False, sigma=0.6):
+    from ltx_amd.model.transformer.model import Modality
+
+    if audio:
+        return Modality(latent=st.audio_latent[None] if latent is None else latent,
+                        context=st.audio_context[None] if context is None else context, context_mask=mask,
+                        timesteps=torch.full((1,), sigma), positions=st.audio_positions)
+    return Modality(latent=st.video_latent[None] if latent is None else latent,
+                    context=st.video_context[None] if context is None else context, context_mask=mask,
+                    timesteps=torch.full((1,), sigma), positions=st.video_positions)
+
+
+def _bits(t):
+    return t.contiguous().view(torch.int16).cpu()
+
+
+def test_two_samples_stacked_match_single_sample_forwards_and_oracle():
+    from test_gpu_model import _model_weights
+
+    from oracle import block as ob
+    from oracle import rope as orope
+
+    model, (s0, s1) = _setup()
+    print("modality: B=2 stacked vs B=1 forwards", flush=True)
+    v = torch.stack([s0.video_latent, s1.video_latent])
+    a = torch.stack([s0.audio_latent, s1.audio_latent])
+    vc = torch.stack([s0.video_context, s1.video_context])
+    ac = torch.stack([s0.audio_context, s1.audio_context])
+    vv, av = model(_mod(s0, v, vc), _mod(s0, a, ac, audio=True))
+    torch.cuda.synchronize()
+    assert vv.shape == (2, s0.video_tokens, 128) and av.shape == (2, s0.audio_tokens, 128)
+    for i, st in enumerate((s0, s1)):
+        v1, a1 = model(_mod(st), _mod(st, audio=True))
+        torch.cuda.synchronize()
+        for got, ref in ((vv[i], v1[0]), (av[i], a1[0])):
+            g, r = bf16_from_torch(got), bf16_from_torch(ref)
+            assert max_rel_err(g, r) <= 1e-2 and cos_sim(g, r) >= 0.9999
+    MW = _model_weights(model)
+    vpos, apos = s0.video_positions, s0.audio_positions
+    pes = tuple(tuple(torch.from_numpy(x) for x in p) for p in (
+        orope.rope_tables(vpos, 4096, 32, orope.VIDEO_MAX_POS),
+        orope.rope_tables(vpos[:, 0:1], 2048, 32, orope.AUDIO_MAX_POS),
+        orope.rope_tables(apos, 2048, 32, orope.AUDIO_MAX_POS),
+        orope.rope_tables(apos[:, 0:1], 2048, 32, orope.AUDIO_MAX_POS)))
+    ov, oa = ob.model_velocity(MW, s1.video_latent.float().cpu(), s1.audio_latent.float().cpu(),
+                               s1.video_context.float().cpu(), s1.audio_context.float().cpu(),
+                               float(np.float32(0.6)), pes)
+    assert cos_sim(bf16_from_torch(vv[1]), ov.numpy()) >= 0.999
+    assert cos_sim(bf16_from_torch(av[1]), oa.numpy()) >= 0.999
+
+
+def test_context_masks_equal_the_kept_rows():
+    model, (s0, s1) = _setup()
+    n = s0.video_context.shape[0]
+    print("modality: boolean padding mask and additive mask with holes", flush=True)
+    # boolean padding mask on the video context: the last 4 tokens are padding
+    pad = torch.ones((1, n), dtype=torch.bool)
+    pad[0, n - 4:] = False
+    got, _ = model(_mod(s0, mask=pad))
+    ref, _ = model(_mod(s0, context=s0.video_context[None, : n - 4]))
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(got), _bits(ref))
+    # additive mask with holes on both contexts
+    keep = np.array([0, 2, 3, 5, 8, 9, 10, 13, 15])
+    add = torch.full((1, n), float("-inf"))
+    add[0, keep] = 0.0
+    kv = torch.from_numpy(keep).to(DEV)
+    gv, ga = model(_mod(s0, mask=add), _mod(s0, mask=add.clone(), audio=True))
+    rv, ra = model(_mod(s0, context=s0.video_context.index_select(0, kv)[None]),
+                   _mod(s0, context=s0.audio_context.index_select(0, kv)[None], audio=True))
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(gv), _bits(rv)) and torch.equal(_bits(ga), _bits(ra))
+    # the mask changes the result (the dropped keys mattered)
+    full, _ = model(_mod(s0))
+    torch.cuda.synchronize()
+    assert not torch.equal(_bits(full), _bits(gv))
+
+
+def test_samples_with_unequal_kept_contexts_run_one_after_another():
+    model, (s0, s1) = _setup()
+    n = s0.video_context.shape[0]
+    print("modality: B=2 with kept lengths 16 and 11", flush=True)
+    mask = torch.ones((2, n), dtype=torch.bool)
+    mask[1, 11:] = False
+    v = torch.stack([s0.video_latent, s1.video_latent])
+    vc = torch.stack([s0.video_context, s1.video_context])
+    got, aud = model(_mod(s0, v, vc, mask=mask))
+    r0, _ = model(_mod(s0))
+    r1, _ = model(_mod(s1, context=s1.video_context[None, :11]))
+    torch.cuda.synchronize()
+    assert aud.shape == (2, 0, 128)
+    assert torch.equal(_bits(got[0]), _bits(r0[0])) and torch.equal(_bits(got[1]), _bits(r1[0]))
+
+
+def test_x0_model_is_latent_minus_sigma_velocity():
+    from ltx_amd.model.transformer.model import X0Model
+
+    model, (s0, _) = _setup()
+    print("modality: X0Model", flush=True)
+    sigma = float(np.float32(0.6))
+    dv, da = X0Model(model)(_mod(s0), _mod(s0, audio=True))
+    vv, av = model(_mod(s0), _mod(s0, audio=True))
+    torch.cuda.synchronize()
+    for d, lat, vel in ((dv, s0.video_latent, vv[0]), (da, s0.audio_latent, av[0])):
+        ref = lat.float() - torch.tensor(sigma, device=DEV) * vel.float()
+        assert d.dtype == torch.float32 and torch.equal(d[0], ref)
+    # video-only inference on the AV model (no A2V / V2A): the video alone
+    only = X0Model(model)(_mod(s0))
+    vo, ao = model(_mod(s0))
+    torch.cuda.synchronize()
+    assert ao.shape == (1, 0, 128)
+    assert torch.equal(only[0], s0.video_latent.float() - torch.tensor(sigma, device=DEV) * vo[0].float())
