@@ -83,6 +83,35 @@ def _uniform_value(t, what: str) -> float:
     return float(v[0])
 
 
+@dataclass
+class TokenTimesteps:
+    """Per-token timesteps of one sample as row groups: ``values`` the
+    distinct timesteps (first-occurrence order), ``segments`` the maximal
+    runs of rows [r0, r1) sharing group g, in row order."""
+
+    values: list
+    segments: list
+
+
+def token_timestep_groups(t) -> TokenTimesteps:
+    """Row groups of a (T,) per-token timestep vector (the image-conditioned
+    denoise masks: timesteps = sigma * mask, model.py:160-187)."""
+    v = torch.as_tensor(t).detach().float().reshape(-1).cpu().numpy()
+    if v.size == 0:
+        raise ValueError("empty per-token timesteps")
+    values, index, segments = [], {}, []
+    r0 = 0
+    for r in range(1, v.size + 1):
+        if r == v.size or v[r] != v[r0]:
+            key = float(v[r0])
+            if key not in index:
+                index[key] = len(values)
+                values.append(key)
+            segments.append((r0, r, index[key]))
+            r0 = r
+    return TokenTimesteps(values, segments)
+
+
 def context_keep_rows(mask: torch.Tensor | None, batch: int, length: int) -> list[torch.Tensor | None]:
     """Per sample, the context rows a (B, S) mask keeps (None: all of them).
 
@@ -245,33 +274,63 @@ class LTXModel:
             self._rope_cache.pop(next(iter(self._rope_cache)))
         return hit
 
-    def _timestep_rows(self, sigma_dev: torch.Tensor, cross_sigma_dev: torch.Tensor, video: bool) -> None:
+    def _mlps(self, video: bool) -> tuple:
+        if video:
+            return (self.adaln_single, self.prompt_adaln_single, self.av_ca_video_scale_shift_adaln_single,
+                    self.av_ca_a2v_gate_adaln_single)
+        return (self.audio_adaln_single, self.audio_prompt_adaln_single,
+                self.av_ca_audio_scale_shift_adaln_single, self.av_ca_v2a_gate_adaln_single)
+
+    def _timestep_rows(self, sigma_dev: torch.Tensor, cross_sigma_dev: torch.Tensor, video: bool,
+                       prompt_sigma_dev: torch.Tensor | None = None) -> None:
         """Fill the (16, D) timestep rows of one modality (model.py:160-187,
-        :305-314, :418-497) and its embedded timestep."""
+        :305-314, :418-497) and its embedded timestep: the AdaLN rows 0-8 and
+        the cross scale / shift rows 11-14 from the modality's timestep, the
+        prompt rows 9-10 from its sigma (``prompt_sigma_dev``, default the
+        timestep), the cross gate row 15 from the other modality's sigma."""
         d = self.video_dim if video else self.audio_dim
         temb = self._temb_v if video else self._temb_a
         emb = self._emb_v if video else self._emb_a
         ts = self.timestep_scale_multiplier
-        if video:
-            mlps = (self.adaln_single, self.prompt_adaln_single, self.av_ca_video_scale_shift_adaln_single,
-                    self.av_ca_a2v_gate_adaln_single)
-        else:
-            mlps = (self.audio_adaln_single, self.audio_prompt_adaln_single,
-                    self.av_ca_audio_scale_shift_adaln_single, self.av_ca_v2a_gate_adaln_single)
+        mlps = self._mlps(video)
         flat = temb.view(-1)
         mlps[0](sigma_dev, ts, flat[: 9 * d], embedded=emb)
-        mlps[1](sigma_dev, ts, flat[9 * d: 11 * d])
+        mlps[1](sigma_dev if prompt_sigma_dev is None else prompt_sigma_dev, ts, flat[9 * d: 11 * d])
         if self.audio_config is not None:
             mlps[2](sigma_dev, ts, flat[11 * d: 15 * d])
             mlps[3](cross_sigma_dev, self.av_ca_timestep_scale_multiplier, flat[15 * d: 16 * d])
         else:
             flat[11 * d:].zero_()
 
+    def _token_group_rows(self, groups: TokenTimesteps) -> tuple[torch.Tensor, torch.Tensor]:
+        """Per-token video timesteps as row groups: for each distinct value
+        the (L, 16, D) modulation rows of every block and the embedded
+        timestep, from the rows of the sample (``_temb_v``): rows 0-8 and
+        11-14 and the embedded timestep follow the group's value, the prompt
+        and cross gate rows stay the sample's (model.py:418-497)."""
+        d, dev = self.video_dim, self.device
+        mlps, ts = self._mlps(True), self.timestep_scale_multiplier
+        g_n = len(groups.values)
+        vals = torch.tensor(groups.values, dtype=torch.float32, device=dev)
+        temb = self._temb_v.unsqueeze(0).repeat(g_n, 1, 1)
+        emb = torch.empty((g_n, d), device=dev)
+        ada = torch.empty((g_n,) + tuple(self._ada_v.shape), device=dev)
+        stream = _lib.stream_of(ada)
+        for g in range(g_n):
+            flat = temb[g].view(-1)
+            mlps[0](vals[g:g + 1], ts, flat[: 9 * d], embedded=emb[g])
+            if self.audio_config is not None:
+                mlps[2](vals[g:g + 1], ts, flat[11 * d: 15 * d])
+            _lib.call("ltx_broadcast_add_f32", self.video_tables.data_ptr(), temb[g].data_ptr(), ada[g].data_ptr(),
+                      self.num_layers, ADA_ROWS * d, stream)
+        return ada, emb
+
     def velocity(self, video_latent: torch.Tensor, video_context: torch.Tensor, sigma_dev: torch.Tensor,
                  pes: tuple, audio_latent: torch.Tensor | None = None,
                  audio_context: torch.Tensor | None = None,
                  profile_events: list | None = None,
-                 perturbations=None, passes: int = 1) -> tuple[torch.Tensor, torch.Tensor | None]:
+                 perturbations=None, passes: int = 1, sigmas: tuple | None = None,
+                 video_token_timesteps: TokenTimesteps | None = None) -> tuple[torch.Tensor, torch.Tensor | None]:
         """One transformer forward -> (video velocity (T, 128), audio velocity).
 
         Latents are 2-D (T, 128) bf16; contexts (S, D) bf16; ``sigma_dev`` is
@@ -288,6 +347,15 @@ class LTXModel:
         guided step (av_pipeline.py:688-717 runs them one after another).
         Latents of shape (B, T, 128) are B samples at one timestep, run the
         same way (passes = B), each on its own latents.
+
+        ``sigmas`` = (video timestep, video sigma, audio timestep, audio
+        sigma) fp32 device scalars when they differ (default: ``sigma_dev``
+        for all): each modality's AdaLN and cross scale / shift rows follow
+        its timestep, its prompt rows its sigma, its cross gate the other
+        modality's sigma (model.py:418-497).  ``video_token_timesteps`` gives
+        the video tokens per-token timesteps as row groups (one sample, no
+        perturbations): the block's AdaLN inputs, gated residual adds and the
+        output head then use each row group's modulation.
         """
         vpe, vxpe, ape, axpe = pes
         if video_latent.dim() == 3 and video_latent.shape[0] == 1:  # one sample: the 2-D form
@@ -308,9 +376,23 @@ class LTXModel:
                                    proj).view(passes, latent.shape[1], -1)
             return stacked(gemm.linear(latent, proj))
 
+        groups = video_token_timesteps
+        if groups is not None and len(groups.values) < 2:
+            sigmas = sigmas or (sigma_dev,) * 4
+            val = torch.tensor(groups.values[:1], dtype=torch.float32, device=self.device)
+            sigmas = (val,) + tuple(sigmas[1:])
+            groups = None
+        if groups is not None:
+            if passes != 1 or video_latent.dim() != 2:
+                raise NotImplementedError("per-token timesteps: one sample, unstacked")
+            if groups.segments[-1][1] != video_latent.shape[0]:
+                raise ValueError(f"per-token timesteps cover {groups.segments[-1][1]} rows, the latent has "
+                                 f"{video_latent.shape[0]}")
+        vt, vs, at, as_ = sigmas if sigmas is not None else (sigma_dev,) * 4
+
         # preprocess
         vx = project(video_latent, self.patchify_proj)
-        self._timestep_rows(sigma_dev, sigma_dev, video=True)
+        self._timestep_rows(vt, as_, video=True, prompt_sigma_dev=vs)
         stream = _lib.stream_of(vx)
         _lib.call("ltx_broadcast_add_f32", self.video_tables.data_ptr(), self._temb_v.data_ptr(),
                   self._ada_v.data_ptr(), self.num_layers, ADA_ROWS * self.video_dim, stream)
@@ -319,7 +401,7 @@ class LTXModel:
         audio = None
         if run_audio:
             ax = project(audio_latent, self.audio_patchify_proj)
-            self._timestep_rows(sigma_dev, sigma_dev, video=False)
+            self._timestep_rows(at, vs, video=False, prompt_sigma_dev=as_)
             _lib.call("ltx_broadcast_add_f32", self.audio_tables.data_ptr(), self._temb_a.data_ptr(),
                       self._ada_a.data_ptr(), self.num_layers, ADA_ROWS * self.audio_dim, stream)
             audio = TransformerArgs(x=ax, context=audio_context, timesteps=self._temb_a[:9],
@@ -332,8 +414,12 @@ class LTXModel:
                 self._audio_stream = torch.cuda.Stream(device=vx.device)  # default priority
             side = self._audio_stream
         blocks = self.transformer_blocks
+        ada_g = emb_g = None
+        if groups is not None:
+            ada_g, emb_g = self._token_group_rows(groups)
         for i, block in enumerate(blocks):
-            block.ada_rows_video = self._ada_v[i]
+            block.ada_rows_video = self._ada_v[i] if groups is None else [ada_g[g, i] for g in range(len(groups.values))]
+            block.segments_video = None if groups is None else groups.segments
             block.ada_rows_audio = self._ada_a[i] if run_audio else None
             block.audio_stream = side
             block.audio_fork = i == 0
@@ -351,7 +437,13 @@ class LTXModel:
         def unstack(y):
             return y if passes == 1 else y.view(passes, -1, y.shape[-1])
 
-        v_out = unstack(self._output(rows(video.x), self.scale_shift_table, self._emb_v, self.proj_out))
+        if groups is None:
+            v_out = unstack(self._output(rows(video.x), self.scale_shift_table, self._emb_v, self.proj_out))
+        else:
+            vxr = rows(video.x)
+            v_out = torch.empty((vxr.shape[0], self.proj_out.w.shape[0]), dtype=torch.bfloat16, device=vxr.device)
+            for r0, r1, g in groups.segments:
+                self._output(vxr[r0:r1], self.scale_shift_table, emb_g[g], self.proj_out, out=v_out[r0:r1])
         a_out = None
         if run_audio:
             a_out = unstack(self._output(rows(audio.x), self.audio_scale_shift_table, self._emb_a,
@@ -365,14 +457,16 @@ class LTXModel:
         audio modality (or with ``enabled=False`` / no tokens) the audio
         velocity is an empty (B, 0, 128) tensor, as there.
 
-        Covered: B >= 1 samples at one timestep (timesteps, sigma and both
-        modalities share one value), positions shared by the samples, and
-        (B, S) context masks -- the masked keys are dropped from the context
-        (``context_keep_rows``), which gives the masked softmax exactly.  The
-        samples run as one forward (tokens stacked by rows) when their kept
-        contexts have equal lengths, else one after another; ``perturbations``
-        holds one config per sample.  Per-sample or per-token timesteps (the
-        image-conditioned denoise masks) raise NotImplementedError.
+        Covered: B >= 1 samples sharing their timesteps (each modality's
+        timestep and sigma may differ, model.py:418-497), positions shared by
+        the samples, and (B, S) context masks -- the masked keys are dropped
+        from the context (``context_keep_rows``), which gives the masked
+        softmax exactly.  The samples run as one forward (tokens stacked by
+        rows) when their kept contexts have equal lengths, else one after
+        another; ``perturbations`` holds one config per sample.  Per-token
+        video timesteps (the image-conditioned denoise masks, (1, T)) run as
+        row groups for one sample without perturbations; per-sample
+        timesteps and per-token audio timesteps raise NotImplementedError.
         """
         if video is None:
             raise ValueError("Video modality required for video-enabled model")
@@ -388,21 +482,40 @@ class LTXModel:
             raise ValueError(f"{vctx.shape[0]} video contexts for {batch} samples")
         use_audio = (audio is not None and audio.enabled and self.audio_config is not None
                      and torch.as_tensor(audio.latent).shape[-2] > 0)
-        values = [_uniform_value(video.timesteps, "video timesteps")]
-        if video.sigma is not None:
-            values.append(_uniform_value(video.sigma, "video sigma"))
+
+        def sample_sigma(mod, what):
+            # the prompt / cross-gate sigma: given, or the first token's
+            # timestep (model.py:305-314, :459-461)
+            if mod.sigma is not None:
+                return _uniform_value(mod.sigma, f"{what} sigma")
+            t = mod.timesteps
+            if isinstance(t, (int, float)):
+                return float(t)
+            t = torch.as_tensor(t).detach().float().cpu()
+            return _uniform_value(t.reshape(t.shape[0], -1)[:, 0] if t.dim() >= 2 else t, f"{what} sigma")
+
+        groups = None
+        tv_raw = video.timesteps
+        if not isinstance(tv_raw, (int, float)) and torch.as_tensor(tv_raw).dim() == 2 and \
+                torch.as_tensor(tv_raw).shape[1] == vlat.shape[1] and torch.as_tensor(tv_raw).shape[1] > 1:
+            if batch == 1 and torch.as_tensor(tv_raw).shape[0] == 1:
+                groups = token_timestep_groups(tv_raw)
+                if len(groups.values) == 1:
+                    groups = None
+                elif perturbations is not None:
+                    raise NotImplementedError("per-token timesteps with perturbations")
+        vt = groups.values[0] if groups is not None else _uniform_value(tv_raw, "video timesteps")
+        vs = sample_sigma(video, "video")
         alat = actx = None
+        at, as_ = vt, vs
         if use_audio:
             alat, actx = as3(audio.latent), as3(audio.context)
             if alat.shape[0] != batch or actx.shape[0] not in (1, batch):
                 raise ValueError("audio latents / contexts do not match the video samples")
-            values.append(_uniform_value(audio.timesteps, "audio timesteps"))
-            if audio.sigma is not None:
-                values.append(_uniform_value(audio.sigma, "audio sigma"))
-        if any(v != values[0] for v in values):
-            raise NotImplementedError("video / audio timesteps and sigmas differ: one timestep per forward "
-                                      "is supported")
-        sigma_dev = torch.tensor([values[0]], dtype=torch.float32, device=dev)
+            at = _uniform_value(audio.timesteps, "audio timesteps")
+            as_ = sample_sigma(audio, "audio")
+        sig4 = tuple(torch.tensor([x], dtype=torch.float32, device=dev) for x in (vt, vs, at, as_))
+        sigma_dev = sig4[0]
 
         def shared_positions(pos, what):
             if pos is None:
@@ -429,7 +542,8 @@ class LTXModel:
                                  torch.stack(vctxs) if batch > 1 else vctxs[0], sigma_dev, pes,
                                  (alat if batch > 1 else alat[0]) if use_audio else None,
                                  (torch.stack(actxs) if batch > 1 else actxs[0]) if use_audio else None,
-                                 perturbations=perturbations, passes=batch)
+                                 perturbations=perturbations, passes=batch, sigmas=sig4,
+                                 video_token_timesteps=groups)
             v = v if batch > 1 else v[None]
             a = (a if batch > 1 else a[None]) if use_audio else None
         else:
@@ -441,7 +555,7 @@ class LTXModel:
                 if perturbations is not None:
                     pert = BatchedPerturbationConfig([perturbations.perturbations[b]])
                 vb, ab = self.velocity(vlat[b], vctxs[b], sigma_dev, pes, alat[b] if use_audio else None,
-                                       actxs[b] if use_audio else None, perturbations=pert)
+                                       actxs[b] if use_audio else None, perturbations=pert, sigmas=sig4)
                 vs.append(vb)
                 as_.append(ab)
             v = torch.stack(vs)
@@ -450,12 +564,13 @@ class LTXModel:
             a = torch.zeros((batch, 0, AUDIO_IN_CHANNELS), dtype=torch.bfloat16, device=dev)
         return v, a
 
-    def _output(self, x: torch.Tensor, table: torch.Tensor, emb: torch.Tensor, proj: gemm.LinearWeight) -> torch.Tensor:
+    def _output(self, x: torch.Tensor, table: torch.Tensor, emb: torch.Tensor, proj: gemm.LinearWeight,
+                out: torch.Tensor | None = None) -> torch.Tensor:
         t, d = x.shape
         h = torch.empty_like(x)
         _lib.call("ltx_output_norm_modulate_bf16", x.data_ptr(), d, table.data_ptr(), emb.data_ptr(), h.data_ptr(),
                   d, t, d, float(self.norm_eps), _lib.stream_of(x))
-        return gemm.linear(h, proj)
+        return gemm.linear(h, proj, out=out)
 
 
 class X0Model:
@@ -475,8 +590,18 @@ class X0Model:
 
         def denoised(mod, vel):
             lat = torch.as_tensor(mod.latent)
-            lat = (lat[None] if lat.dim() == 2 else lat).to(device=dev, dtype=torch.bfloat16)
-            return to_denoised(lat.contiguous(), vel.contiguous(), _uniform_value(mod.timesteps, "timesteps"))
+            lat = (lat[None] if lat.dim() == 2 else lat).to(device=dev, dtype=torch.bfloat16).contiguous()
+            vel = vel.contiguous()
+            t = mod.timesteps
+            if not isinstance(t, (int, float)) and torch.as_tensor(t).dim() == 2 and lat.shape[0] == 1 and \
+                    torch.as_tensor(t).shape[1] == lat.shape[1]:
+                # per-token timesteps: latent - t_token * velocity, per row group
+                groups = token_timestep_groups(t)
+                out = torch.empty(lat.shape, dtype=torch.float32, device=dev)
+                for r0, r1, g in groups.segments:
+                    out[0, r0:r1] = to_denoised(lat[0, r0:r1], vel[0, r0:r1], groups.values[g])
+                return out
+            return to_denoised(lat, vel, _uniform_value(t, "timesteps"))
 
         dv = denoised(video, v)
         if audio is None:

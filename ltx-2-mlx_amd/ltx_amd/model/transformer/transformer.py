@@ -128,6 +128,34 @@ def adaln(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, eps: float,
     return out
 
 
+def adaln_groups(x: torch.Tensor, groups: list, segments: list, row_scale: int, row_shift: int, eps: float,
+                 flags: int) -> torch.Tensor:
+    """AdaLN with per-token modulation as row groups: rows [r0, r1) of each
+    segment take group g's (16, D) modulation rows."""
+    t, c = x.shape
+    out = torch.empty((t, c), dtype=torch.bfloat16, device=x.device)
+    for r0, r1, g in segments:
+        xv, xs = _lib.row_view(x[r0:r1], c)
+        fused_ops.adaln_rows(xv, xs, groups[g][row_scale], groups[g][row_shift], out[r0:r1], c, r1 - r0, c, eps,
+                             flags)
+    return out
+
+
+def adaln2_groups(x: torch.Tensor, groups: list, segments: list, rows: tuple, eps: float,
+                  flags: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """``adaln2`` with per-token modulation as row groups (rows = the
+    (scale, shift, scale2, shift2) row indices)."""
+    t, c = x.shape
+    out = torch.empty((t, c), dtype=torch.bfloat16, device=x.device)
+    out2 = torch.empty((t, c), dtype=torch.bfloat16, device=x.device)
+    for r0, r1, g in segments:
+        xv, xs = _lib.row_view(x[r0:r1], c)
+        a = groups[g]
+        fused_ops.adaln_rows2(xv, xs, a[rows[0]], a[rows[1]], out[r0:r1], a[rows[2]], a[rows[3]], out2[r0:r1],
+                              r1 - r0, c, eps, flags)
+    return out, out2
+
+
 def adaln2(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, scale2: torch.Tensor, shift2: torch.Tensor,
            eps: float, flags: int) -> tuple[torch.Tensor, torch.Tensor]:
     """Two AdaLN modulations of the same rows (one read of x, one norm)."""
@@ -170,8 +198,11 @@ class BasicAVTransformerBlock:
         self.video_tables: torch.Tensor | None = weights.get("video_tables")
         self.audio_tables: torch.Tensor | None = weights.get("audio_tables")
         # per-step modulation rows injected by the scheduler (see module doc)
-        self.ada_rows_video: torch.Tensor | None = None
+        self.ada_rows_video: torch.Tensor | list | None = None
         self.ada_rows_audio: torch.Tensor | None = None
+        # per-token video timesteps: ada_rows_video is then a list of (16, D)
+        # row groups and segments_video the (r0, r1, group) row runs
+        self.segments_video: list | None = None
         self.audio_stream: torch.cuda.Stream | None = None
         self.audio_fork = True  # the audio stream waits for the caller's stream first
         # The next block of the same forward (set by the scheduler): its text
@@ -329,6 +360,30 @@ class BasicAVTransformerBlock:
         need_av = run_a2v or run_v2a
         ada_v = self._ada(video, self.video_tables, self.ada_rows_video) if run_vx or need_av else None
         ada_a = self._ada(audio, self.audio_tables, self.ada_rows_audio) if run_ax or need_av else None
+        # per-token video timesteps (row groups): the AdaLN inputs and gated
+        # residual adds of the video stream use each row group's rows; the
+        # prompt rows and the cross gate are the same in every group
+        v_groups = v_segs = None
+        if isinstance(ada_v, list):
+            if npass != 1 or perturbations is not None or not self.segments_video:
+                raise NotImplementedError("per-token timesteps: one unperturbed pass with row segments")
+            v_groups, v_segs, ada_v = ada_v, self.segments_video, ada_v[0]
+
+        def v_adaln(x, row_scale, row_shift, fl):
+            if v_groups is None:
+                return adaln(x, ada_v[row_scale], ada_v[row_shift], eps, fl)
+            return adaln_groups(x, v_groups, v_segs, row_scale, row_shift, eps, fl)
+
+        def v_residual(o, weight, stream_x, owned, row_gate, epi, phase="attn_out"):
+            if v_groups is None:
+                return residual_gemm(o, weight, stream_x, owned, ada_v[row_gate], epi, phase=phase)
+            out = stream_x if owned else torch.empty_like(stream_x)
+            _sp.begin(phase)
+            for r0, r1, g in v_segs:
+                gemm.linear(o[r0:r1], weight, epilogue=epi, out=out[r0:r1], residual=stream_x[r0:r1],
+                            gate=v_groups[g][row_gate])
+            _sp.end(phase)
+            return out
 
         # Audio work on the second stream when both streams run.  Tensors that
         # cross streams are recorded on the consuming stream so the caching
@@ -356,8 +411,8 @@ class BasicAVTransformerBlock:
         if side is not None:
             a2.record_stream(side)
             ada_a.record_stream(side)
-            if ada_v is not None:
-                ada_v.record_stream(side)
+            for t in (v_groups or []) + ([ada_v] if ada_v is not None else []):
+                t.record_stream(side)
 
         ev_kv = kv_v = None
         prefetched, self._prefetched_kv = self._prefetched_kv, None
@@ -385,6 +440,7 @@ class BasicAVTransformerBlock:
                 if nb is not None and nb.attn2 is not None and nb.ada_rows_video is not None and \
                         (run_a2v or run_v2a):
                     ada_n = nb.ada_rows_video
+                    ada_n = ada_n[0] if isinstance(ada_n, list) else ada_n  # prompt rows: every group's
                     cm = adaln(c, ada_n[ROW_SCALE_KV], ada_n[ROW_SHIFT_KV], eps, _lib.ADALN_NO_NORM)
                     nb._prefetched_kv = (nb.attn2.context_kv(cm), cp)
                     nb._prefetched_kv[0].record_stream(main)
@@ -394,11 +450,11 @@ class BasicAVTransformerBlock:
             pe = _tables(video.positional_embeddings)
             rng = runs(keep("skip_video_self_attn"))
             if rng == [(0, npass)]:
-                h = adaln(v2, ada_v[ROW_SCALE_MSA], ada_v[ROW_SHIFT_MSA], eps, flags)
+                h = v_adaln(v2, ROW_SCALE_MSA, ROW_SHIFT_MSA, flags)
                 if side is not None:
                     context_kv_on_side()
                 o = self.attn1.core(h, pe=pe, passes=npass)
-                v2 = residual_gemm(o, self.attn1.to_out, v2, v_owned, ada_v[ROW_GATE_MSA], gemm.EPI_RESIDUAL)
+                v2 = v_residual(o, self.attn1.to_out, v2, v_owned, ROW_GATE_MSA, gemm.EPI_RESIDUAL)
                 v_owned = True
             elif rng:
                 def video_self(dst, src, p0, p1):
@@ -414,7 +470,7 @@ class BasicAVTransformerBlock:
             _sp.begin("video_text_ca")
             if side is not None and kv_v is None:
                 context_kv_on_side()
-            a = adaln(v2, ada_v[ROW_SCALE_Q], ada_v[ROW_SHIFT_Q], eps, rn)
+            a = v_adaln(v2, ROW_SCALE_Q, ROW_SHIFT_Q, rn)
             if kv_v is not None:
                 kv, cp = kv_v
                 if cp == npass:
@@ -431,7 +487,7 @@ class BasicAVTransformerBlock:
                 else:
                     o = torch.cat([self.attn2.core(a[p * tv:(p + 1) * tv], c) for p in range(npass)], 0) \
                         if npass > 1 else self.attn2.core(a, c)
-            v2 = residual_gemm(o, self.attn2.to_out, v2, v_owned, ada_v[ROW_GATE_Q], gemm.EPI_RESIDUAL_ROUND)
+            v2 = v_residual(o, self.attn2.to_out, v2, v_owned, ROW_GATE_Q, gemm.EPI_RESIDUAL_ROUND)
             v_owned = True
             _sp.signpost_barrier(v2)
             _sp.end("video_text_ca")
@@ -481,8 +537,12 @@ class BasicAVTransformerBlock:
             vpe = _tables(video.cross_positional_embeddings)
             ape = _tables(audio.cross_positional_embeddings)
             # modulated inputs of both directions from the pre-A2V streams
-            vs_a2v, vs_v2a = adaln2(v2, ada_v[ROW_SCALE_A2V], ada_v[ROW_SHIFT_A2V], ada_v[ROW_SCALE_V2A],
-                                    ada_v[ROW_SHIFT_V2A], eps, rn)
+            if v_groups is None:
+                vs_a2v, vs_v2a = adaln2(v2, ada_v[ROW_SCALE_A2V], ada_v[ROW_SHIFT_A2V], ada_v[ROW_SCALE_V2A],
+                                        ada_v[ROW_SHIFT_V2A], eps, rn)
+            else:
+                vs_a2v, vs_v2a = adaln2_groups(v2, v_groups, v_segs, (ROW_SCALE_A2V, ROW_SHIFT_A2V, ROW_SCALE_V2A,
+                                                                      ROW_SHIFT_V2A), eps, rn)
             ev_v = main.record_event() if side is not None else None
             rng = runs(keep("skip_a2v_cross_attn")) if run_a2v else []
             kv_a2v = None
@@ -546,12 +606,11 @@ class BasicAVTransformerBlock:
         if run_vx:
             _sp.begin("video_ff")
             _sp.begin("v_ff_adaln")
-            h = adaln(v2, ada_v[ROW_SCALE_MLP], ada_v[ROW_SHIFT_MLP], eps, flags)
+            h = v_adaln(v2, ROW_SCALE_MLP, ROW_SHIFT_MLP, flags)
             _sp.end("v_ff_adaln")
             _sp.begin("v_ff_inner")
             f = self.ff.hidden(h)
-            v2 = residual_gemm(f, self.ff.project_out, v2, v_owned, ada_v[ROW_GATE_MLP], gemm.EPI_RESIDUAL,
-                               phase=None)
+            v2 = v_residual(f, self.ff.project_out, v2, v_owned, ROW_GATE_MLP, gemm.EPI_RESIDUAL, phase=None)
             _sp.end("v_ff_inner")
             _sp.signpost_barrier(v2)
             _sp.end("video_ff")

@@ -127,7 +127,9 @@ def block(W: dict, vx, ax, v_ada, a_ada, vctx, actx, vpe, vxpe, ape, axpe, *, fu
           skips=frozenset()):
     """BasicAVTransformerBlock.__call__ (transformer.py:389-674) on 2-D
     streams; ``*_ada`` are the (16, D) modulation rows
-    [sst(9) | prompt(2) | av(5)] + timestep rows.  ``skips`` holds the
+    [sst(9) | prompt(2) | av(5)] + timestep rows, or (16, T, D) per video
+    token (per-token timesteps; the prompt rows are then the sample's on
+    every token).  ``skips`` holds the
     perturbation kinds applying to this block ("skip_video_self_attn",
     "skip_audio_self_attn", "skip_a2v_cross_attn", "skip_v2a_cross_attn"):
     the sub-layer's whole residual update is skipped (transformer.py:430-470,
@@ -139,7 +141,10 @@ def block(W: dict, vx, ax, v_ada, a_ada, vctx, actx, vpe, vxpe, ape, axpe, *, fu
             h = adaln(vx, r[1], r[0], eps, fused_adaln)
             vx = bf(vx + attention(W["attn1"], h, pe=vpe, heads=vh) * r[2])
         a = adaln(vx, r[7], r[6], eps)
-        c = bf(vctx * (1 + r[10]) + r[9])
+        # the context's prompt rows belong to the sample, not to a video token
+        # (per-token rows (16, T, D) carry the same prompt rows on every token)
+        pk = r[:, 0] if r.dim() == 3 else r
+        c = bf(vctx * (1 + pk[10]) + pk[9])
         vx = bf(vx + bf(attention(W["attn2"], a, c, heads=vh) * r[8]))
     if ax is not None:
         q = a_ada
@@ -191,8 +196,9 @@ def adaln_mlp(w: dict, t: float):
 
 
 def output_head(x, table, emb, w, b, eps=EPS):
-    """model.py:1312-1326: bf16 arithmetic modulation, then proj_out."""
-    ss = bf(table + emb[None, :])
+    """model.py:1312-1326: bf16 arithmetic modulation, then proj_out; ``emb``
+    (D) or per token (T, D)."""
+    ss = bf(table + emb[None, :]) if emb.dim() == 1 else bf(table[:, None, :] + emb[None])
     shift, scale = ss[0], ss[1]
     mu = x.double().mean(-1, keepdim=True)
     var = (x.double() - mu).square().mean(-1, keepdim=True)
@@ -210,9 +216,16 @@ def euler_x0(latent, velocity, sigma: float, sigma_next: float):
 
 
 def model_velocity(MW: dict, vlat, alat, vctx, actx, sigma: float, pes, *, av_ca_mult=1000.0, ts_mult=1000.0,
-                   eps=EPS, skips=None):
+                   eps=EPS, skips=None, video_token_sigmas=None):
     """LTXModel.__call__ (model.py:1344-1486): (video velocity, audio velocity)
     bf16 values.  ``skips(block_index) -> set of perturbation kinds``.
+
+    ``video_token_sigmas`` (T,): per-token video timesteps (model.py:160-187,
+    :418-497 -- the image-conditioned denoise mask): the video AdaLN rows 0-8,
+    the cross scale / shift rows 11-14 and the output head's embedded
+    timestep follow each token's value; the prompt rows and both cross gates
+    keep ``sigma`` (each modality's sample sigma).  The blocks then see
+    (16, T, D) modulation rows, broadcast per token.
 
     MW: {"patchify": (w, b), "audio_patchify": (w, b), "mlps_v": [4 mlp dicts],
     "mlps_a": [...], "tables_v": (L, 16, D), "tables_a": ..., "blocks": [block
@@ -232,8 +245,21 @@ def model_velocity(MW: dict, vlat, alat, vctx, actx, sigma: float, pes, *, av_ca
 
     tv, emb_v = temb(MW["mlps_v"], vx.shape[1])
     ta, emb_a = temb(MW["mlps_a"], ax.shape[1]) if ax is not None else (None, None)
+    if video_token_sigmas is not None:
+        ts_tok = torch.as_tensor(video_token_sigmas, dtype=torch.float32).reshape(-1)
+        d = vx.shape[1]
+        rows = tv[:, None, :].repeat(1, ts_tok.numel(), 1)  # prompt rows and the gate: the sample's
+        emb_tok = emb_v[None, :].repeat(ts_tok.numel(), 1)
+        for u in torch.unique(ts_tok).tolist():
+            sel = ts_tok == u
+            e9, emb_u = adaln_mlp(MW["mlps_v"][0], u * ts_mult)
+            e4, _ = adaln_mlp(MW["mlps_v"][2], u * ts_mult)
+            rows[0:9, sel] = e9.view(9, 1, d)
+            rows[11:15, sel] = e4.view(4, 1, d)
+            emb_tok[sel] = emb_u
+        tv, emb_v = rows, emb_tok
     for i, W in enumerate(MW["blocks"]):
-        v_ada = MW["tables_v"][i] + tv
+        v_ada = (MW["tables_v"][i][:, None, :] if tv.dim() == 3 else MW["tables_v"][i]) + tv
         a_ada = MW["tables_a"][i] + ta if ax is not None else None
         vx, ax = block(W, vx, ax, v_ada, a_ada, vctx, actx, vpe, vxpe, ape, axpe, eps=eps,
                        skips=frozenset() if skips is None else frozenset(skips(i)))

@@ -14,7 +14,11 @@ tokens, 16 text tokens):
   different kept lengths (then run one after another);
 * X0Model: ``latent - sigma * velocity`` in fp32, bit for bit, with and
   without the audio modality; the audio velocity of a video-only call is an
-  empty (B, 0, 128) tensor.
+  empty (B, 0, 128) tensor;
+* per-token video timesteps (an image-conditioned denoise mask: conditioned
+  tokens at 0) run as row groups and match the oracle's per-token forward
+  (cosine >= 0.999, normwise error <= 2e-2), in two and three row segments;
+  one value on every token is the uniform forward bit for bit.
 """
 
 from __future__ import annotations
@@ -151,3 +155,65 @@ def test_x0_model_is_latent_minus_sigma_velocity():
     torch.cuda.synchronize()
     assert ao.shape == (1, 0, 128)
     assert torch.equal(only[0], s0.video_latent.float() - torch.tensor(sigma, device=DEV) * vo[0].float())
+
+
+def _oracle_pes(st):
+    from oracle import rope as orope
+
+    vpos, apos = st.video_positions, st.audio_positions
+    return tuple(tuple(torch.from_numpy(x) for x in p) for p in (
+        orope.rope_tables(vpos, 4096, 32, orope.VIDEO_MAX_POS),
+        orope.rope_tables(vpos[:, 0:1], 2048, 32, orope.AUDIO_MAX_POS),
+        orope.rope_tables(apos, 2048, 32, orope.AUDIO_MAX_POS),
+        orope.rope_tables(apos[:, 0:1], 2048, 32, orope.AUDIO_MAX_POS)))
+
+
+@pytest.mark.parametrize("pattern", ["first_frame", "middle_run"])
+def test_per_token_video_timesteps_match_the_oracle(pattern):
+    """Image-conditioned denoise mask: the conditioned video tokens at t = 0,
+    the rest at the sample sigma 0.6 (given as ``sigma``): the block's AdaLN
+    inputs, gated residual adds and the output head run per row group (two
+    or three segments) and match the oracle's per-token forward."""
+    from test_gpu_model import _model_weights
+
+    from ltx_amd.model.transformer.model import Modality, X0Model
+    from oracle import block as ob
+
+    model, (s0, _) = _setup()
+    t = s0.video_tokens
+    tok = torch.full((1, t), float(np.float32(0.6)))
+    if pattern == "first_frame":
+        tok[0, : t // 2] = 0.0          # latent frame 0 of 2
+    else:
+        tok[0, 8:16] = 0.0              # a run inside the first frame: three segments
+    print(f"modality: per-token timesteps ({pattern})", flush=True)
+    vmod = Modality(latent=s0.video_latent[None], context=s0.video_context[None], context_mask=None, timesteps=tok,
+                    positions=s0.video_positions, sigma=torch.full((1,), 0.6))
+    v, a = model(vmod, _mod(s0, audio=True))
+    uv, _ = model(_mod(s0), _mod(s0, audio=True))
+    torch.cuda.synchronize()
+    assert not torch.equal(_bits(v), _bits(uv))
+    ov, oa = ob.model_velocity(_model_weights(model), s0.video_latent.float().cpu(), s0.audio_latent.float().cpu(),
+                               s0.video_context.float().cpu(), s0.audio_context.float().cpu(),
+                               float(np.float32(0.6)), _oracle_pes(s0), video_token_sigmas=tok[0])
+    gv, ga = bf16_from_torch(v[0]), bf16_from_torch(a[0])
+    assert cos_sim(gv, ov.numpy()) >= 0.999 and cos_sim(ga, oa.numpy()) >= 0.999
+    assert max_rel_err(gv, ov.numpy()) <= 2e-2
+    # X0: latent - t_token * velocity per token
+    dv, _ = X0Model(model)(vmod, _mod(s0, audio=True))
+    torch.cuda.synchronize()
+    ref = s0.video_latent.float() - tok[0].to(DEV)[:, None] * v[0].float()
+    assert torch.equal(dv[0], ref)
+
+
+def test_per_token_timesteps_all_equal_are_the_uniform_forward():
+    from ltx_amd.model.transformer.model import Modality
+
+    model, (s0, _) = _setup()
+    print("modality: per-token timesteps, one value", flush=True)
+    vmod = Modality(latent=s0.video_latent[None], context=s0.video_context[None], context_mask=None,
+                    timesteps=torch.full((1, s0.video_tokens), 0.6), positions=s0.video_positions)
+    v, a = model(vmod, _mod(s0, audio=True))
+    uv, ua = model(_mod(s0), _mod(s0, audio=True))
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(v), _bits(uv)) and torch.equal(_bits(a), _bits(ua))

@@ -9,8 +9,9 @@ and the one-timestep rule.
   reference's -3.4e38 mask entries to the scores (pins the equivalence the
   GPU path relies on, including that a mask which drops a key changes the
   result).
-* ``_uniform_value``: one timestep per forward; per-sample / per-token
-  timesteps raise NotImplementedError.
+* ``_uniform_value``: one timestep where the forward needs one (per sample,
+  per audio token); ``token_timestep_groups``: per-token video timesteps as
+  (row range, group) segments.
 """
 
 from __future__ import annotations
@@ -91,3 +92,15 @@ def test_one_timestep_per_forward():
     t[0, :2] = 0.0                                               # conditioned tokens at t = 0
     with pytest.raises(NotImplementedError):
         _uniform_value(t, "t")
+
+
+def test_token_timestep_groups():
+    from ltx_amd.model.transformer.model import token_timestep_groups
+
+    g = token_timestep_groups(torch.tensor([[0.0, 0.0, 0.6, 0.6, 0.6, 0.0, 0.6]]))
+    assert g.values == [0.0, pytest.approx(0.6)]
+    assert g.segments == [(0, 2, 0), (2, 5, 1), (5, 6, 0), (6, 7, 1)]
+    one = token_timestep_groups(torch.full((5,), 0.25))
+    assert one.values == [0.25] and one.segments == [(0, 5, 0)]
+    with pytest.raises(ValueError):
+        token_timestep_groups(torch.zeros(0))
