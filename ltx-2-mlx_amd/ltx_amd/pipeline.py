@@ -225,6 +225,66 @@ def denoise(model: LTXModel, state: DenoiseState, callback=None) -> DenoiseState
     return state
 
 
+def condition_video(state: DenoiseState, denoise_mask, clean_latent: torch.Tensor) -> None:
+    """Image / keyframe conditioning of the video tokens: a 0 / 1 denoise
+    mask (T,) -- 0 on conditioned tokens -- and the clean latent rows (T, 128)
+    they hold.  The conditioned rows of the state's latent become the clean
+    rows (noisers.py:40-80 with a hard mask: ``clean + mask * (noise -
+    clean)``); ``denoise_conditioned`` then keeps them there."""
+    from .model.transformer.model import token_timestep_groups
+
+    mask = torch.as_tensor(denoise_mask).detach().float().reshape(-1).cpu()
+    if mask.numel() != state.video_tokens or not bool(((mask == 0) | (mask == 1)).all()):
+        raise ValueError(f"a 0 / 1 denoise mask over the {state.video_tokens} video tokens is expected")
+    clean = clean_latent.to(device=state.video_latent.device, dtype=torch.bfloat16).reshape(state.video_tokens, -1)
+    state.video_denoise_mask = mask
+    state.video_clean_latent = clean.contiguous()
+    for r0, r1, g in token_timestep_groups(mask).segments:
+        if float(mask[r0]) == 0.0:
+            state.video_latent[r0:r1].copy_(state.video_clean_latent[r0:r1])
+
+
+def denoise_conditioned(model: LTXModel, state: DenoiseState, callback=None) -> DenoiseState:
+    """The distilled loop (av_pipeline.py:899-1146) with the non-uniform video
+    denoise mask of ``condition_video``: per step the video timesteps are
+    ``sigma * mask`` (common.py:194-204) -- per-token, as row groups -- the X0
+    prediction ``latent - t * velocity`` per row group (model.py:1519-1525),
+    blended with the clean latent where the mask is 0 (common.py:169-191,
+    :299-318), then the Euler step (diffusion_steps.py:19-69); the audio
+    stream's mask is uniform."""
+    from .components.diffusion_steps import to_denoised
+    from .model.transformer.model import TokenTimesteps, token_timestep_groups
+
+    mask = state.video_denoise_mask
+    base = token_timestep_groups(mask)
+    pes = model.rope(state.video_positions, state.audio_positions)
+    stepper = EulerDiffusionStep()
+    dev = state.video_latent.device
+    audio = state.audio_tokens > 0
+    for step in range(len(state.sigmas) - 1):
+        sigma, sigma_next = state.sigmas[step], state.sigmas[step + 1]
+        values = [float(np.float32(np.float32(v) * np.float32(sigma))) for v in base.values]
+        groups = TokenTimesteps(values, base.segments)
+        sig = state.sigmas_dev[step:step + 1]
+        t0 = torch.tensor(values[:1], dtype=torch.float32, device=dev)
+        v_vel, a_vel = model.velocity(state.video_latent, state.video_context, sig, pes,
+                                      state.audio_latent if audio else None, state.audio_context if audio else None,
+                                      sigmas=(t0, sig, sig, sig),
+                                      video_token_timesteps=groups if len(values) > 1 else None)
+        denoised = torch.empty(state.video_latent.shape, dtype=torch.float32, device=dev)
+        for r0, r1, g in groups.segments:
+            if float(mask[r0]) == 0.0:
+                denoised[r0:r1] = state.video_clean_latent[r0:r1].float()  # the clean rows (mask 0)
+            else:
+                denoised[r0:r1] = to_denoised(state.video_latent[r0:r1], v_vel[r0:r1], values[g])
+        stepper.step(state.video_latent, denoised, state.sigmas, step, out=state.video_latent)
+        if a_vel is not None:
+            stepper.step_from_velocity(state.audio_latent, a_vel, sigma, sigma_next, out=state.audio_latent)
+        if callback is not None:
+            callback(step, state)
+    return state
+
+
 def _velocities(model: LTXModel, state: DenoiseState, sig, pes, video_context, audio_context, perturbations=None):
     audio = state.audio_tokens > 0
     return model.velocity(state.video_latent, video_context, sig, pes,
