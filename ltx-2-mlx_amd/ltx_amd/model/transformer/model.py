@@ -549,17 +549,17 @@ class LTXModel:
         else:
             from ...components.perturbations import BatchedPerturbationConfig
 
-            vs, as_ = [], []
+            v_outs, a_outs = [], []
             for b in range(batch):
                 pert = None
                 if perturbations is not None:
                     pert = BatchedPerturbationConfig([perturbations.perturbations[b]])
                 vb, ab = self.velocity(vlat[b], vctxs[b], sigma_dev, pes, alat[b] if use_audio else None,
                                        actxs[b] if use_audio else None, perturbations=pert, sigmas=sig4)
-                vs.append(vb)
-                as_.append(ab)
-            v = torch.stack(vs)
-            a = torch.stack(as_) if use_audio else None
+                v_outs.append(vb)
+                a_outs.append(ab)
+            v = torch.stack(v_outs)
+            a = torch.stack(a_outs) if use_audio else None
         if a is None:
             a = torch.zeros((batch, 0, AUDIO_IN_CHANNELS), dtype=torch.bfloat16, device=dev)
         return v, a
