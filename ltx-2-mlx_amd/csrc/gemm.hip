@@ -724,25 +724,28 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(GemmArgs p) {
 // rows 128-255; wave w & 3 owns 64 output columns.  The groups run half a
 // stage apart: while one group issues its memory cluster (LDS fragment reads
 // of a stage, its share of the direct global->LDS loads two stages ahead, the
-// scale loads), the other group's compute cluster (the stage's 32 MFMAs with
-// the weight dequantisation of fragments 2-7 interleaved) keeps the SIMD's
-// matrix pipe busy.  The memory cluster ends, once its fragment reads have
-// landed, by decoding the stage's E8M0 scales and dequantising fragments 0
-// and 1, so the compute cluster's first MFMAs issue right after the barrier
-// (FF up 402 -> 382 us: the dependent decode -> convert chain had left the
-// matrix pipe idle at the start of every compute cluster).
+// scale loads), the other group's compute cluster (the stage's 64 16x16x32
+// MFMAs with the weight dequantisation of fragments 2-7 interleaved) keeps
+// the SIMD's matrix pipe busy.  The memory cluster ends, once its fragment
+// reads have landed, by decoding the stage's E8M0 scales and dequantising
+// fragments 0 and 1, so the compute cluster's first MFMAs issue right after
+// the barrier (FF up 402 -> 382 us: the dependent decode -> convert chain had
+// left the matrix pipe idle at the start of every compute cluster).
 // A workgroup barrier separates the clusters.  Both operands reach LDS by
 // global_load_lds (no staging registers, no LDS write instructions): three
 // 48 KB stages of bf16 activations (256 x 128 B) and raw weight codes
 // (256 x 64 B).  The MXFP8 / int8 codes are dequantised per fragment with the
 // exact format arithmetic, so the bf16 MFMA sees bit-exact weights.  bf16
-// weights: four 32 KB stages of 32-deep bf16 rows of both operands, the
-// direct loads three stages ahead, 16 MFMAs per cluster, no dequantisation.
+// weights: five 32 KB stages of 32-deep bf16 rows of both operands, the
+// direct loads four stages ahead, 32 MFMAs per cluster, no dequantisation.
+// MX (8-bit codes of both operands): 16 scaled 32x32x64 MFMAs per cluster.
 //
 // Inside a stage the k order of the MFMA slots is permuted so that a lane
-// reads the codes of two k-steps with one 16-byte LDS read: k-step 2p+s, lane
-// half h covers k = 32p + 16h + 8s + [0, 8) for both operands (the E8M0 block
-// of that k range is p).  The sum over the stage is the same set of products.
+// reads the codes of both k-steps of the stage with one 16-byte LDS read:
+// k-step s, lane quarter q covers k = 16q + 8s + [0, 8) for both operands
+// (the E8M0 block of that k range is q / 2).  MX: k-step pair p of the
+// scaled MFMA, lane half h, k = 32p + 16h + [0, 16).  The sum over the stage
+// is the same set of products.
 constexpr int kG8Threads = 512;
 // the automatic tile choice uses the 8-wave kernel for 8-bit weights (MXFP8
 // and int8) on problems of at least 100 256x256 tiles, and for bf16 weights on
@@ -776,6 +779,13 @@ struct G8Cfg {
   static constexpr int WM = BM / 2, WN = 64;
   static constexpr int TM = WM / 32, TN = WN / 32;
   static constexpr int WAVES_M = BM / WM;
+  // bf16 MFMAs (bf16 or dequantised 8-bit weights) in the 16x16x32 shape:
+  // same flops per cycle as 32x32x16, but the chip holds a ~12 % higher clock
+  // under it at full load (2.0 vs 1.7-1.8 GHz in a register-only loop of
+  // either shape on all 256 CUs); the wave tile, hence the LDS reads and the
+  // accumulator registers, is unchanged.  MX keeps the scaled 32x32x64.
+  static constexpr bool S16 = !MX;
+  static constexpr int TM16 = WM / 16, TN16 = WN / 16;
   // bf16 activations (MX: 8-bit codes like the weights), 8-bit weight codes
   // (BF: bf16 weights)
   static constexpr int A_ROWB = MX ? BK : BK * 2, B_ROWB = BF ? BK * 2 : BK;
@@ -818,7 +828,8 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   constexpr int A_DMA = Cfg::A_DMA, B_DMA = Cfg::B_DMA;
   constexpr int EPI_ROWB = Cfg::EPI_ROWB, EPI_WAVE = Cfg::EPI_WAVE;
   constexpr bool RESID = EPI == LTX_GEMM_EPI_RESIDUAL || EPI == LTX_GEMM_EPI_RESIDUAL_ROUND;
-  constexpr bool MX = Cfg::MX, BF = Cfg::BF;
+  constexpr bool MX = Cfg::MX, BF = Cfg::BF, S16 = Cfg::S16;
+  constexpr int TM16 = Cfg::TM16, TN16 = Cfg::TN16;
   constexpr int STAGES = Cfg::STAGES, AHEAD = STAGES - 1;
   __shared__ __attribute__((aligned(1024))) char lds[Cfg::TOTAL];
 
@@ -898,28 +909,36 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   };
 
   // ---- per-lane fragment read bases: LDS byte addresses of the lane's first
-  // fragment for each XOR pattern -- A per (pair pp, step s) of a stage and
-  // a low / high base (stage buffers 0-1 / 1-2 within the 16-bit immediate),
-  // B per pair pp -- so that every fragment read is base + immediate
+  // fragment per XOR pattern, so that every fragment read is base + immediate.
+  // MX (32x32x64): lane (row fr, half h) reads chunk 2 pp + h of its 64-byte
+  // code rows for the stage's k-step pair pp, both operands.
   const int fr = lane & 31, h = lane >> 5;
-  const int a_swz = (fr >> 1) & 7;  // rows i*32 + fr share it
   const int b_swz = (fr >> 2) & 3;
-  int a_lo[4], a_hi[4], b_base[2];
+  int b_base[2], a_mx[2];
 #pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int pp = v >> 1, s = v & 1;
-    a_lo[v] = (wm * WM + fr) * A_ROWB + (((4 * pp + 2 * h + s) ^ a_swz) * 16);
-    a_hi[v] = a_lo[v] + A_BYTES;
-  }
-#pragma unroll
-  for (int pp = 0; pp < 2; ++pp)
+  for (int pp = 0; pp < 2; ++pp) {
     b_base[pp] = B_REGION + (wn * WN + fr) * B_ROWB + (((2 * pp + h) ^ b_swz) * 16);
-  // MX: activation code fragments, read like the weight codes; BF: both
-  // operands' fragments of k-step s (k = 16 s + 8 h + [0, 8)) at a_mx[s] /
-  // b_base[s]
-  int a_mx[2];
+    a_mx[pp] = (wm * WM + fr) * A_ROWB + (((2 * pp + h) ^ b_swz) * 16);
+  }
+  // 16x16x32 fragments: lane (r16, q) = row r16 of a 16-row block, k-quarter
+  // q.  Weights: one 16-byte read per block and stage, chunk q of the 64-byte
+  // row (8-bit codes: k = 16 q + [0, 16), both k-steps; BF: bf16 k = 8 q +
+  // [0, 8) of the 32-deep stage).  8-bit codes: k-step s of the stage is
+  // k = 16 q + 8 s + [0, 8) in lane q for both operands -- the activation
+  // fragment is chunk 2 q + s of the 128-byte row -- so the E8M0 block of a
+  // lane's codes is q / 2 in both k-steps.  Every 16 lanes read 16
+  // consecutive rows of one logical chunk: conflict-free under the swizzle.
+  // The activation bases come as a low / high pair (stage buffers 0-1 / 1-2
+  // of the 8-bit-code ring) so that the offsets fit the 16-bit immediate.
+  const int r16 = lane & 15, q = lane >> 4;
+  const int w16 = B_REGION + (wn * WN + r16) * B_ROWB + ((q ^ ((r16 >> 2) & 3)) * 16);
+  int x16_lo[2], x16_hi[2];
 #pragma unroll
-  for (int pp = 0; pp < 2; ++pp) a_mx[pp] = (wm * WM + fr) * A_ROWB + (((2 * pp + h) ^ b_swz) * 16);
+  for (int s = 0; s < 2; ++s) {
+    x16_lo[s] = BF ? (wm * WM + r16) * A_ROWB + ((q ^ ((r16 >> 2) & 3)) * 16)
+                   : (wm * WM + r16) * A_ROWB + (((2 * q + s) ^ ((r16 >> 1) & 7)) * 16);
+    x16_hi[s] = x16_lo[s] + A_BYTES;
+  }
   // MXFP8 scales reach LDS by direct loads too, eight stages at a time: the
   // loop then holds no register-destined global load, whose first use would
   // make the compiler wait for every load in flight (its wait counting does
@@ -933,7 +952,7 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   constexpr bool SCALED = BKIND == B_MXFP8 || MX;
   const int sc_records = SCALED ? (int)((int64_t)p.N * p.ld_scale) : 0;
   const int asc_records = MX ? (int)((int64_t)p.M * p.ld_ascale) : 0;
-  const int sc_read = Cfg::SC_OFF + (wn * WN + fr) * 16;
+  const int sc_read = Cfg::SC_OFF + (wn * WN + (S16 ? r16 : fr)) * 16;
   const int asc_read = Cfg::SC_OFF + 2 * Cfg::SC_OCT + (wm * WM + fr) * 16;
   uint32_t sc_src = 0;
   if (grp == 0 || !MX) {
@@ -956,39 +975,43 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
                      sc_lds + (2 + (oct & 1)) * Cfg::SC_OCT + (wave & 3) * 1024);
     }
   };
-  float s_i8[TN];
+  // weight row blocks of a wave: TN of 32 rows, or (S16) TN16 of 16
+  constexpr int NWB = S16 ? TN16 : TN, WB_ROWS = S16 ? 16 : 32;
+  float s_i8[NWB];
 #pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    int gn = n0 + wn * WN + j * 32 + fr;
+  for (int j = 0; j < NWB; ++j) {
+    int gn = n0 + wn * WN + j * WB_ROWS + (S16 ? r16 : fr);
     gn = gn < p.N ? gn : p.N - 1;
     if (BKIND == B_INT8) s_i8[j] = ((const float*)p.bscale)[gn];
   }
-  uint32_t scw[TN];  // this stage pair's E8M0 bytes of the lane's weight rows
+  uint32_t scw[NWB];  // this stage pair's E8M0 bytes of the lane's weight rows
   // global memory instructions of a stage's first memory cluster: the direct
   // loads of stage kt+2, plus (group 0, MXFP8) the scales in the first stage
   // of an octet
   constexpr int VM_DMA = A_DMA + B_DMA;
   constexpr int VM_SCALES = SCALED ? 1 : 0;
 
-  bf16x8 fa[(MX || BF) ? 1 : 4][TM];  // A fragments of the stage's four k-steps
-  u32x4 fb[2][TN];   // weight codes of the stage's two k-step pairs (16 per lane); BF: bf16
-                     // weight fragments of its two k-steps
-  u32x4 fa8[2][(MX || BF) ? TM : 1];  // MX: activation codes, as the weight codes; BF: bf16 fragments
-  uint32_t sca[MX ? TM : 1];  // MX: this stage pair's E8M0 bytes of the lane's activation rows
+  // MX: the scaled 32x32x64 fragments
+  u32x4 fb[2][MX ? TN : 1];   // weight codes of the stage's two k-step pairs (16 per lane)
+  u32x4 fa8[2][MX ? TM : 1];  // activation codes, read like the weight codes
+  uint32_t sca[MX ? TM : 1];  // this stage pair's E8M0 bytes of the lane's activation rows
+  // 16x16x32: the stage's weight fragments (codes, or bf16 weights) and its
+  // activation fragments per k-step
+  constexpr int XS = BF ? 1 : 2;
+  u32x4 w16f[S16 ? TN16 : 1];
+  bf16x8 x16f[XS][S16 ? TM16 : 1];
   // fragment reads of stage kt, which sits in buffer BUF (compile-time)
   auto read_stage = [&](int kt, auto bufc) __attribute__((always_inline)) {
     constexpr int BUF = decltype(bufc)::value;
     if constexpr (SCALED) {
       const int sa = sc_read + ((kt >> 3) & 1) * Cfg::SC_OCT + ((kt & 7) >> 1) * 4;
 #pragma unroll
-      for (int j = 0; j < TN; ++j) scw[j] = *reinterpret_cast<const uint32_t*>(lds + sa + j * 32 * 16);
+      for (int j = 0; j < NWB; ++j) scw[j] = *reinterpret_cast<const uint32_t*>(lds + sa + j * WB_ROWS * 16);
     }
-    if constexpr (MX || BF) {
-      if constexpr (MX) {
-        const int sa = asc_read + ((kt >> 3) & 1) * Cfg::SC_OCT + ((kt & 7) >> 1) * 4;
+    if constexpr (MX) {
+      const int sa = asc_read + ((kt >> 3) & 1) * Cfg::SC_OCT + ((kt & 7) >> 1) * 4;
 #pragma unroll
-        for (int i = 0; i < TM; ++i) sca[i] = *reinterpret_cast<const uint32_t*>(lds + sa + i * 32 * 16);
-      }
+      for (int i = 0; i < TM; ++i) sca[i] = *reinterpret_cast<const uint32_t*>(lds + sa + i * 32 * 16);
 #pragma unroll
       for (int pp = 0; pp < 2; ++pp) {
 #pragma unroll
@@ -1000,30 +1023,29 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
       }
     } else {
 #pragma unroll
-      for (int pp = 0; pp < 2; ++pp) {
+      for (int jb = 0; jb < TN16; ++jb)
+        w16f[jb] = *reinterpret_cast<const u32x4*>(lds + w16 + BUF * B_BYTES + jb * 16 * B_ROWB);
+      const int* base = BUF == 0 ? x16_lo : x16_hi;
+      constexpr int rel = (BUF == 0 ? 0 : BUF - 1) * A_BYTES;
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-          fb[pp][j] = *reinterpret_cast<const u32x4*>(lds + b_base[pp] + BUF * B_BYTES + j * 32 * B_ROWB);
+      for (int s = 0; s < XS; ++s)
 #pragma unroll
-        for (int s = 0; s < 2; ++s)
-#pragma unroll
-          for (int i = 0; i < TM; ++i) {
-            const int* base = BUF == 0 ? a_lo : a_hi;
-            constexpr int rel = (BUF == 0 ? 0 : BUF - 1) * A_BYTES;
-            fa[2 * pp + s][i] =
-                *reinterpret_cast<const bf16x8*>(lds + base[2 * pp + s] + rel + i * 32 * A_ROWB);
-          }
-      }
+        for (int ib = 0; ib < TM16; ++ib)
+          x16f[s][ib] = *reinterpret_cast<const bf16x8*>(lds + base[s] + rel + ib * 16 * A_ROWB);
     }
   };
 
-  f32x16 acc[TM][TN];
+  // accumulators: (32x32) TM x TN blocks of 16 values, or (16x16) TM16 x TN16
+  // blocks of 4 -- the same 128 per lane
+  constexpr int AM = S16 ? TM16 : TM, AN = S16 ? TN16 : TN, AE = S16 ? 4 : 16;
+  using AccT = std::conditional_t<S16, f32x4, f32x16>;
+  AccT acc[AM][AN];
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+  for (int i = 0; i < AM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
+    for (int j = 0; j < AN; ++j)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+      for (int e = 0; e < AE; ++e) acc[i][j][e] = 0.0f;
 
   // codes of one k-step (two 4-byte words) -> bf16 fragment
   auto dequant = [&](uint32_t w0, uint32_t w1, float sc) -> bf16x8 {
@@ -1053,35 +1075,34 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
     return __builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]});
   };
 
-  // Weight fragment f of a stage (k-step f / TN, column block f % TN) in two
-  // alternating register sets; the E8M0 scales of the stage's two k-step
-  // pairs decoded once per stage.
-  float scf[2][TN];
+  // Weight fragment f of a stage (k-step f / TN16, row block f % TN16) in two
+  // alternating register sets; the scale of each row block (its E8M0 byte of
+  // the lane's k-block q / 2, or the int8 row scale) set once per stage.
+  float scf[NWB];
   bf16x8 bq[2];
-  constexpr int NF = 4 * TN;
-  auto decode = [&](int kt, int pp, int j) {
-    if constexpr (BKIND == B_MXFP8)
-      scf[pp][j] = e8m0_to_f32_valu(__builtin_amdgcn_ubfe(scw[j], 16 * (kt & 1) + 8 * pp, 8));
-    else
-      scf[pp][j] = s_i8[j];
-  };
+  constexpr int NF = XS * TN16;
+  const int q_sh = 8 * (q >> 1);
   auto frag_dequant = [&](int f) -> bf16x8 {
-    const int kk = f / TN, j = f % TN, pp = kk >> 1, s = kk & 1;
-    return dequant(fb[pp][j][2 * s], fb[pp][j][2 * s + 1], scf[pp][j]);
+    const int s = f / TN16, jb = f % TN16;
+    return dequant(w16f[jb][2 * s], w16f[jb][2 * s + 1], scf[jb]);
   };
   // end of the memory cluster of stage kt (its fragment reads have landed):
-  // the stage's scales and fragments 0 and 1 (MX: nothing to decode)
+  // the stage's scales and fragments 0 and 1 (MX, bf16: nothing to decode)
   auto prep_stage = [&](int kt) __attribute__((always_inline)) {
     if constexpr (MX || BF) return;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) decode(kt, 0, j);
+    for (int j = 0; j < NWB; ++j) {
+      if constexpr (BKIND == B_MXFP8)
+        scf[j] = e8m0_to_f32_valu(__builtin_amdgcn_ubfe(scw[j], 16 * (kt & 1) + q_sh, 8));
+      else
+        scf[j] = s_i8[j];
+    }
     bq[0] = frag_dequant(0);
-#pragma unroll
-    for (int j = 0; j < TN; ++j) decode(kt, 1, j);
     bq[1] = frag_dequant(1);
   };
-  // compute cluster of stage kt: 4 k-steps x TN weight fragments x TM MFMAs.
-  // Fragment f+1 (f >= 1) is dequantised while the MFMAs of fragment f run.
+  // compute cluster of stage kt.  8-bit codes: 2 k-steps x TN16 weight
+  // fragments x TM16 MFMAs; fragment f+1 (f >= 1) is dequantised while the
+  // MFMAs of fragment f run.  bf16: TN16 x TM16 MFMAs of the stage's 32 k.
   // MX: TN x TM scaled fp8 MFMAs of 64 k.  Their operand contract (probed on
   // the device): lane (row r, half h) holds k = 16h + [0, 16) in bytes 0-15
   // and k = 32 + 16h + [0, 16) in bytes 16-31 -- the two 16-byte code chunks
@@ -1108,22 +1129,19 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
       }
     } else if constexpr (BF) {
 #pragma unroll
-      for (int st = 0; st < 2; ++st)
+      for (int jb = 0; jb < TN16; ++jb)
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-          for (int i = 0; i < TM; ++i)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fb[st][j]),
-                                                                __builtin_bit_cast(bf16x8, fa8[st][i]),
-                                                                acc[i][j], 0, 0, 0);
+        for (int ib = 0; ib < TM16; ++ib)
+          acc[ib][jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w16f[jb]), x16f[0][ib],
+                                                                acc[ib][jb], 0, 0, 0);
     } else {
 #pragma unroll
       for (int f = 0; f < NF; ++f) {
-        const int kk = f / TN, j = f % TN;
+        const int s = f / TN16, jb = f % TN16;
         if (f >= 1 && f + 1 < NF) bq[(f + 1) & 1] = frag_dequant(f + 1);
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bq[f & 1], fa[kk][i], acc[i][j], 0, 0, 0);
+        for (int ib = 0; ib < TM16; ++ib)
+          acc[ib][jb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bq[f & 1], x16f[s][ib], acc[ib][jb], 0, 0, 0);
       }
     }
   };
@@ -1217,15 +1235,17 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   auto phase1 = [&](auto sig_tag, auto rtb_tag) {
     constexpr bool SIG = decltype(sig_tag)::value;
     constexpr bool RTB = decltype(rtb_tag)::value;
+    // accumulator block (i, j), values 4 g .. 4 g + 3: output columns nl ..
+    // nl + 3 of tile row (32x32) i * 32 + fr, or (16x16) i * 16 + r16
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
+    for (int j = 0; j < AN; ++j) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int nl = j * 32 + 8 * g + 4 * h;
+      for (int g = 0; g < AE / 4; ++g) {
+        const int nl = S16 ? j * 16 + 4 * q : j * 32 + 8 * g + 4 * h;
         const int gn = n0 + wn * WN + nl;
         const f32x4 bias4 = *reinterpret_cast<const f32x4*>(col_lds + wn * WN + nl);
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
+        for (int i = 0; i < AM; ++i) {
           // bf16 roundings two at a time (one conversion per pair)
           float y[4];
 #pragma unroll
@@ -1250,7 +1270,7 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
           bf16x4 v;
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[e] = (bf16)y[e];
-          *reinterpret_cast<bf16x4*>(E + (i * 32 + fr) * EPI_ROWB + nl * 2) = v;
+          *reinterpret_cast<bf16x4*>(E + (S16 ? i * 16 + r16 : i * 32 + fr) * EPI_ROWB + nl * 2) = v;
         }
       }
     }
