@@ -247,8 +247,8 @@ int ltx_broadcast_add_f32(const float* table, const float* vec, float* out, int6
  * loads / fragment reads and MFMAs; every weight format (MXFP8 needs
  * K % 512 == 0 and 16-byte aligned scale rows, else LTX_ERR_UNSUPPORTED).
  * The automatic choice for int8 and MXFP8 weights when 256x256 tiles are
- * chosen, and for bf16 weights on products wider than deep (N > K) or of
- * 100-159 tiles. */
+ * chosen, and for bf16 weights on products at least as wide as deep
+ * (N >= K) or of 100-159 tiles. */
 #define LTX_GEMM_TILE_G8 (5 << 8)
 /* The eight-wave kernel with 128 x 256 tiles (same conditions as
  * LTX_GEMM_TILE_G8), for products whose 256 x 256 tiles fill only part of

@@ -1403,12 +1403,13 @@ static int launch_epi_w(const GemmArgs& p, int tile, hipStream_t s) {
     // more CU time per launch, which the audio stream's work beside it then
     // lacks: explicit only, LTX_GEMM_TILE_G8_128.)
     // bf16 weights (32-deep stages) take it where it measured faster at
-    // M = 3456: products wider than deep (FF up 429 -> 411 us, QKV 312 ->
-    // 298, A2V out 60.0 -> 59.1) and the partial round of the A2V query
-    // projection (90 -> 72 us); the square and the FF down products stay on
-    // the 4-wave kernel (4096^2 106 vs 107 us, FF down 394 vs 419).
+    // M = 3456 (16x16x32 MFMAs, one box): products at least as wide as deep
+    // (FF up 396 vs 422 us on the 4-wave kernel, QKV 291 vs 302, 4096^2 98.8
+    // vs 103.7, A2V out 57.5 vs 59.9) and the partial round of the A2V query
+    // projection (81 vs 87 us); the FF down product stays on the 4-wave
+    // kernel (393 vs 402 us).
     const int64_t big = (int64_t)((p.M + 255) / 256) * ((p.N + 255) / 256);
-    const bool g8 = (BKIND == B_MXFP8 || BKIND == B_INT8 || (BKIND == B_BF16 && (p.N > p.K || big < 160))) &&
+    const bool g8 = (BKIND == B_MXFP8 || BKIND == B_INT8 || (BKIND == B_BF16 && (p.N >= p.K || big < 160))) &&
                     g8_ok<BKIND>(p);
     tile = big >= 160 ? (g8 ? 5 : 1) : (big >= 100 && g8 ? 5 : 2);
   }
