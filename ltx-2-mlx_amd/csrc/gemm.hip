@@ -1383,12 +1383,50 @@ static bool g8_ok(const GemmArgs& p) {
   return true;
 }
 
+// Automatic 8-wave launches split M when that shortens a partial last round:
+// rows [0, r0) in 256-row tiles, rows [r0, M) in 128-row tiles by a second
+// launch of the 128-row form (same per-element arithmetic, bit-identical
+// outputs).  Cost model in rounds of one workgroup per CU on the MI355X's
+// 256 CUs: a round of 128-row tiles takes 0.67 of a 256-row round (FF up
+// alone: 1728 tiles of 128 rows in 7 rounds, 436 us, against 896 of 256 rows
+// in 4 rounds, 373 us).  At M = 3456 the FF up-projection (14 x 64 tiles =
+// 3.5 rounds, i.e. 4) runs 12 tile rows of 256 (3 rounds) plus 3 of 128
+// (one partial round): 392.5 -> 373.1 us alone.  A split must model >= 3 %
+// faster; r0 = M means one launch.
+constexpr int kG8Cus = 256;
+static int g8_split_rows(int M, int N) {
+  const int64_t tn = (N + 255) / 256, tm = (M + 255) / 256;
+  auto rounds = [](int64_t tiles) { return (double)((tiles + kG8Cus - 1) / kG8Cus); };
+  const double one = rounds(tm * tn);
+  double best = one;
+  int r0 = M;
+  for (int64_t b = tm - 1; b >= 1 && b >= tm - 8; --b) {
+    const int64_t small = (M - 256 * b + 127) / 128;
+    const double t = rounds(b * tn) + 0.67 * rounds(small * tn);
+    if (t < best && t < 0.97 * one) {
+      best = t;
+      r0 = (int)(256 * b);
+    }
+  }
+  return r0;
+}
+// The rows [r0, M) of a product: the same operands from row r0 on.
+static GemmArgs rows_from(const GemmArgs& p, int r0) {
+  GemmArgs q = p;
+  q.A = p.A + (int64_t)r0 * p.lda;
+  q.C = p.C + (int64_t)r0 * p.ldc;
+  if (p.R) q.R = p.R + (int64_t)r0 * p.ldr;
+  q.M = p.M - r0;
+  return q;
+}
+
 // Tile shapes (all K step 64): 256x256 and 128x128 with the register-staged
 // loader (1 and 2; 128x128 runs two workgroups per CU), 256x256 with the
 // LDS-DMA loader (3), 256x128 register-staged (4), and the 8-wave kernel with
 // 256x256 (5) or 128x256 tiles (6).
 template <int BKIND, int EPI>
 static int launch_epi_w(const GemmArgs& p, int tile, hipStream_t s) {
+  const bool auto_tile = tile == 0;
   if (tile == 0) {
     // Large tiles when they still give most CUs a tile; 128x128 otherwise.
     // 8-bit weights take the 8-wave kernel from 100 tiles of 256x256: the A2V
@@ -1415,8 +1453,17 @@ static int launch_epi_w(const GemmArgs& p, int tile, hipStream_t s) {
   }
   if (tile == 5 || tile == 6) {
     if (!g8_ok<BKIND>(p)) return LTX_ERR_UNSUPPORTED;
-    if (tile == 5) launch_g8<BKIND, EPI>(p, s);
-    else launch_g8<BKIND, EPI, 128>(p, s);
+    const int r0 = (tile == 5 && auto_tile) ? g8_split_rows(p.M, p.N) : p.M;
+    if (tile == 6) {
+      launch_g8<BKIND, EPI, 128>(p, s);
+    } else if (r0 < p.M) {
+      GemmArgs top = p;
+      top.M = r0;
+      launch_g8<BKIND, EPI>(top, s);
+      launch_g8<BKIND, EPI, 128>(rows_from(p, r0), s);
+    } else {
+      launch_g8<BKIND, EPI>(p, s);
+    }
     return LTX_OK;
   }
   if (tile == 1)

@@ -334,6 +334,41 @@ def test_gemm8_epilogues(epi, kind, M, K, N, rows):
     assert (ulp_diff_bf16(bf16_from_torch(out), bf16_from_torch(ref_old)) <= 1).mean() >= 0.99
 
 
+@pytest.mark.parametrize("M", [3456, 1296])
+@pytest.mark.parametrize("epi", ["bias", "gelu", "residual", "residual_round"])
+@pytest.mark.parametrize("kind", ["bf16", "int8", "mxfp8"])
+def test_gemm8_row_split_matches_one_launch(kind, epi, M):
+    """At 3456 and 1296 rows x 16384 columns the automatic choice runs the
+    first rows in 256-row tiles and the rest (384 / 272 rows) by a second
+    launch of the 128-row form, whose activation, output and residual rows
+    are offset views of the same buffers: bit-identical to one launch of
+    256-row tiles for every epilogue, in place on the residual for the gated
+    forms, and the bias form with head-gate columns."""
+    from ltx_amd.kernels import gemm
+
+    codes = {"bias": gemm.EPI_BIAS, "gelu": gemm.EPI_GELU, "residual": gemm.EPI_RESIDUAL,
+             "residual_round": gemm.EPI_RESIDUAL_ROUND}
+    K, N = 512, 16384
+    print(f"gemm8 row split {kind} {epi} M={M}", flush=True)
+    rng = np.random.default_rng(M + len(epi))
+    x = _t(_bf(rng, (M, K)))
+    wt = gemm.make_weight(_t(_bf(rng, (N, K), 0.05)), _t(rng.standard_normal(N).astype(np.float32) * 0.1,
+                                                        torch.float32), kind=kind)
+    outs = []
+    for tile in (gemm.TILE_AUTO, gemm.TILE_G8):
+        if epi.startswith("residual"):
+            r = _t(_bf(np.random.default_rng(7), (M, N)))
+            g = _t(np.random.default_rng(8).standard_normal(N).astype(np.float32) * 0.5, torch.float32)
+            out = gemm.linear(x, wt, epilogue=codes[epi], out=r, residual=r, gate=g, tile=tile)
+            assert out.data_ptr() == r.data_ptr()
+        else:
+            out = gemm.linear(x, wt, epilogue=codes[epi], tile=tile, sigmoid_from=N - 40 if epi == "bias" else None)
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.isfinite(outs[0].float()).all()
+    assert torch.equal(outs[0], outs[1])
+
+
 def test_gemm8_rejects_what_it_does_not_cover():
     from ltx_amd import _lib
     from ltx_amd.kernels import gemm
