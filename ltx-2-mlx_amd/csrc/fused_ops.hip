@@ -322,7 +322,14 @@ __global__ __launch_bounds__(THREADS, 4) void qknorm_rope_kernel(
   }
   __syncthreads();
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t wave0 = (int64_t)blockIdx.x * WAVES + (threadIdx.x >> 6);
+  // 16-wave workgroups (at most one per CU, at most 256 of them) number the
+  // tasks across the grid: wave pair i of workgroup b takes tasks 2 (i G +
+  // b) + {0, 1} (G = grid size) and then every 16 G-th after them, so a
+  // second pass over the tasks is spread over every CU instead of filling
+  // the first workgroups' waves; 8-wave ones take consecutive tasks
+  const int64_t lw = threadIdx.x >> 6;
+  const int64_t wave0 = THREADS == 1024 ? 2 * ((lw >> 1) * gridDim.x + blockIdx.x) + (lw & 1)
+                                        : (int64_t)blockIdx.x * WAVES + lw;
   const int64_t nwaves = (int64_t)gridDim.x * WAVES;
   const int64_t half = D / 2;
   // tasks [0, 2 mn) pair the operands' rows; the rest are the larger
@@ -674,8 +681,12 @@ static int qknorm_rope_launch(void* q, int64_t q_stride, int64_t rows_q, const f
   // fastest for each: 3456-row Q + K 42.2 -> 39.9 us, 2 x 14640 rows 149.7 ->
   // 142.6 us against 4-wave workgroups; 68 + 68 rows 7.9 against 10.9 us in
   // 16-wave ones)
+  // Past 4096 tasks the 16-wave grid stops at one workgroup per CU (256 on
+  // the MI355X): the 6912 tasks of the step's Q + K rows then run as 27 per
+  // CU (at most 28: 16 in the first pass, 10-12 in the second) rather than 32
+  // on 176 CUs and 16 on the other 80 (432 workgroups of 16 tasks).
   const bool wide = tasks > 1024 && tasks <= kFewRows;
-  const int grid = row_grid(tasks, kMaxRowBlocks, wide ? 16 : 8);
+  const int grid = wide ? row_grid(tasks, 256, 16) : row_grid(tasks, kMaxRowBlocks, 8);
   bf16* qp = (bf16*)q;
   bf16* kp = (bf16*)k;
 #define LTX_QK_LAUNCH(PPL, HV)                                                                            \

@@ -265,6 +265,16 @@ def test_qknorm_no_rope_text():
     _qk_case(68, 256, 2048, 32, None, None, seed=5)
 
 
+def test_qknorm_rope_two_passes_unequal_operands():
+    """More rows than one pass of the 16-wave grid holds (4096 tasks), with
+    unequal operands: the paired Q / K tasks, then the longer operand's
+    remaining rows, each run once (RoPE on Q only, no RoPE on K)."""
+    pos = orope.video_positions(10, 20, 25, fps=24.0)
+    tab = orope.rope_tables(pos, 2048, 32, orope.VIDEO_MAX_POS)
+    _qk_case(5000, 2100, 2048, 32, tab, None, seed=6)
+    _qk_case(1900, 5100, 2048, 32, None, None, seed=7)
+
+
 def test_output_norm_modulate():
     from ltx_amd import _lib
 
