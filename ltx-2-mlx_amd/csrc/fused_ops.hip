@@ -139,14 +139,20 @@ __global__ __launch_bounds__(THREADS) void adaln_kernel(
 
 // ---------------------------------------------------------------------------
 // Gated residual add: out = bf16(gate * branch + residual)
+// One-wave workgroups: the hardware spreads them over the CUs one by one, so
+// 3456 rows put 13-14 on every CU (four-wave workgroups: up to 16 on some
+// while others hold 12): 17.2 -> 16.7 us at 3456 x 4096, 9.0 -> 8.0 us at
+// 1296 x 4096, 61.0 -> 60.4 us at 14640 x 4096.
+constexpr int kGatedAddThreads = kWave;
 template <int VPL>
-__global__ __launch_bounds__(kRowBlock) void gated_add_kernel(
+__global__ __launch_bounds__(kGatedAddThreads) void gated_add_kernel(
     const bf16* residual, int64_t res_stride, const bf16* __restrict__ branch,
     int64_t br_stride, const float* __restrict__ gate, bf16* out, int64_t out_stride,
     int64_t rows, int flags) {
+  constexpr int WAVES = kGatedAddThreads / kWave;
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t wave0 = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-  const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
+  const int64_t wave0 = (int64_t)blockIdx.x * WAVES + (threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * WAVES;
   const bool round_prod = (flags & LTX_GATED_ROUND_PRODUCT) != 0;
 
   float g[VPL][8];
@@ -590,15 +596,29 @@ static int adaln_launch(const void* x, int64_t x_stride, const float* scale, con
   const bf16* xp = (const bf16*)x;
   bf16* op = (bf16*)out;
   bf16* op2 = (bf16*)out2;
-  // few rows: 16-wave workgroups (one LDS copy of the modulation per 16 rows)
+  // few rows: large workgroups (one LDS copy of the modulation per
+  // workgroup), W waves: from 1024 to 4096 rows the smallest of 8, 12, 14
+  // and 16 that needs at most 256 workgroups -- at most one per CU of the
+  // MI355X, every CU holding about the same rows (3456 rows: 14 waves, 247
+  // workgroups, 11.8 vs 11.9 us at C = 4096 and 6.3 vs 6.6 us at C = 2048
+  // against 216 of 16; 1296 rows: 8 waves, 5.7 vs 8.4 us against 81 of 16);
+  // 16 below and above that range.
   const bool few = rows <= kFewRows;
-  const int grid = few ? row_grid(rows, kMaxStreamRowBlocks, 16) : row_grid(rows, kMaxStreamRowBlocks);
+  int W = 16;
+  if (rows > 1024 && rows <= 4096) {
+    const int64_t need = (rows + 255) / 256;
+    W = need <= 8 ? 8 : need <= 12 ? 12 : need <= 14 ? 14 : 16;
+  }
+  const int grid = few ? row_grid(rows, kMaxStreamRowBlocks, W) : row_grid(rows, kMaxStreamRowBlocks);
 #define LTX_ADALN_ARGS xp, x_stride, scale, shift, op, out_stride, scale2, shift2, op2, out2_stride, rows, eps, flags
+#define LTX_ADALN_FEW(V, N)                                                                         \
+  (W == 8    ? adaln_kernel<V, 512, N><<<grid, 512, 0, s>>>(LTX_ADALN_ARGS)                         \
+   : W == 12 ? adaln_kernel<V, 768, N><<<grid, 768, 0, s>>>(LTX_ADALN_ARGS)                         \
+   : W == 14 ? adaln_kernel<V, 896, N><<<grid, 896, 0, s>>>(LTX_ADALN_ARGS)                         \
+             : adaln_kernel<V, 1024, N><<<grid, 1024, 0, s>>>(LTX_ADALN_ARGS))
 #define LTX_ADALN_LAUNCH(V)                                                                                   \
-  (dual ? (few ? (adaln_kernel<V, 1024, 2><<<grid, 1024, 0, s>>>(LTX_ADALN_ARGS))                             \
-               : (adaln_kernel<V, kRowBlock, 2><<<grid, kRowBlock, 0, s>>>(LTX_ADALN_ARGS)))                    \
-        : (few ? (adaln_kernel<V, 1024, 1><<<grid, 1024, 0, s>>>(LTX_ADALN_ARGS))                             \
-               : (adaln_kernel<V, kRowBlock, 1><<<grid, kRowBlock, 0, s>>>(LTX_ADALN_ARGS))))
+  (dual ? (few ? LTX_ADALN_FEW(V, 2) : (adaln_kernel<V, kRowBlock, 2><<<grid, kRowBlock, 0, s>>>(LTX_ADALN_ARGS))) \
+        : (few ? LTX_ADALN_FEW(V, 1) : (adaln_kernel<V, kRowBlock, 1><<<grid, kRowBlock, 0, s>>>(LTX_ADALN_ARGS))))
   switch (C / 512) {
     case 1: LTX_ADALN_LAUNCH(1); break;
     case 2: LTX_ADALN_LAUNCH(2); break;
@@ -607,6 +627,7 @@ static int adaln_launch(const void* x, int64_t x_stride, const float* scale, con
     default: return LTX_ERR_UNSUPPORTED;
   }
 #undef LTX_ADALN_LAUNCH
+#undef LTX_ADALN_FEW
 #undef LTX_ADALN_ARGS
   return ltx_launch_status();
 }
@@ -644,12 +665,12 @@ extern "C" int ltx_gated_add_fused_bf16(const void* residual, int64_t residual_s
   const bf16* rp = (const bf16*)residual;
   const bf16* bp = (const bf16*)branch;
   bf16* op = (bf16*)out;
-  const int grid = row_grid(rows, kMaxStreamRowBlocks);
+  const int grid = row_grid(rows, kMaxStreamRowBlocks * kWavesPerBlock, kGatedAddThreads / kWave);
   switch (C / 512) {
-    case 1: gated_add_kernel<1><<<grid, kRowBlock, 0, s>>>(rp, residual_stride, bp, branch_stride, gate, op, out_stride, rows, flags); break;
-    case 2: gated_add_kernel<2><<<grid, kRowBlock, 0, s>>>(rp, residual_stride, bp, branch_stride, gate, op, out_stride, rows, flags); break;
-    case 4: gated_add_kernel<4><<<grid, kRowBlock, 0, s>>>(rp, residual_stride, bp, branch_stride, gate, op, out_stride, rows, flags); break;
-    case 8: gated_add_kernel<8><<<grid, kRowBlock, 0, s>>>(rp, residual_stride, bp, branch_stride, gate, op, out_stride, rows, flags); break;
+    case 1: gated_add_kernel<1><<<grid, kGatedAddThreads, 0, s>>>(rp, residual_stride, bp, branch_stride, gate, op, out_stride, rows, flags); break;
+    case 2: gated_add_kernel<2><<<grid, kGatedAddThreads, 0, s>>>(rp, residual_stride, bp, branch_stride, gate, op, out_stride, rows, flags); break;
+    case 4: gated_add_kernel<4><<<grid, kGatedAddThreads, 0, s>>>(rp, residual_stride, bp, branch_stride, gate, op, out_stride, rows, flags); break;
+    case 8: gated_add_kernel<8><<<grid, kGatedAddThreads, 0, s>>>(rp, residual_stride, bp, branch_stride, gate, op, out_stride, rows, flags); break;
     default: return LTX_ERR_UNSUPPORTED;
   }
   return ltx_launch_status();
