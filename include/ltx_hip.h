@@ -227,7 +227,9 @@ int ltx_broadcast_add_f32(const float* table, const float* vec, float* out, int6
  * Requirements: K % 64 == 0, N % 8 == 0, 16-byte aligned pointers and row
  * strides; MXFP8 scales 4-byte aligned with ld_scale % 4 == 0.  `epilogue` is
  * one of LTX_GEMM_EPI_* optionally OR-ed with a tile override
- * (LTX_GEMM_TILE_256 / _128 / _256_DMA / _256x128 / _G8; default: by problem size).
+ * (LTX_GEMM_TILE_256 / _128 / _256_DMA / _256x128 / _G8; default: by problem size;
+ * the default may run the product as two launches on `stream`, 256-row tiles
+ * for the first rows and 128-row tiles for the rest, bit-identical to one).
  * With LTX_GEMM_EPI_BIAS, output columns n >= sigmoid_from get the head-gate
  * epilogue of LTX_GEMM_EPI_SIGMOID2 instead (pass N for none): the per-head
  * gate logits ride along with the Q / QKV projection in one GEMM.
