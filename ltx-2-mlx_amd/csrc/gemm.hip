@@ -760,6 +760,23 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
+// 16-byte chunk XOR of row r in the 8-wave kernel's stages, 64-byte rows (4
+// chunks) and 128-byte rows (8 chunks).  ds_read_b128 services a wave's lanes
+// 16 at a time, in the lane-octet pairs (0, 3), (1, 2), (4, 7), (5, 6)
+// (probed: two octets reading the same banks at other addresses conflict only
+// in those pairs), and its conflicts were probed per read pattern (rocprofv3
+// SQ_LDS_BANK_CONFLICT of a one-read kernel over 290 lane -> address tables):
+// the 32x32 fragment reads (lane = row 0-31, lane / 32 = chunk half) are
+// conflict-free under chunk ^ ((r / 4) % 4) and chunk ^ ((r / 2) % 8), but the
+// 16x16 reads (lane % 16 = row, lane / 16 = chunk quarter) conflict under
+// those (the FF up-projection: 36-39 M conflict cycles per launch) and not
+// under chunk ^ (r bit 0 | r bit 2 << 1) and chunk ^ (r bit 1 | r bit 0 << 1
+// | r bit 2 << 2).
+__device__ __forceinline__ int g8_swz64(int r, bool s16) { return s16 ? ((r & 1) | ((r >> 1) & 2)) : ((r >> 2) & 3); }
+__device__ __forceinline__ int g8_swz128(int r, bool s16) {
+  return s16 ? (((r >> 1) & 1) | ((r & 1) << 1) | (r & 4)) : ((r >> 1) & 7);
+}
+
 template <int BKIND, int BM_ = 256, int BF_STAGES = 5>
 struct G8Cfg {
   static constexpr bool MX = BKIND == B_MX;
@@ -857,10 +874,10 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
 
   // ---- direct-load sources.  A wave instruction fills one contiguous 1 KiB
   // block of LDS, lane j its 16-byte slot j; the lane's source address picks
-  // the logical chunk that the slot holds under the XOR swizzle: 128-byte A
-  // rows (8 per block) use chunk ^ ((row / 2) % 8), 64-byte code rows (16 per
-  // block) chunk ^ ((row / 4) % 4); each conflict-free for 16 lanes reading
-  // one chunk of 16 consecutive rows.  Rows past M / N re-read the last row.
+  // the logical chunk that the slot holds under the XOR swizzle of its row
+  // (g8_swz128 for the 128-byte A rows, 8 per block; g8_swz64 for the 64-byte
+  // rows, 16 per block), the one under which this kernel's fragment reads are
+  // conflict-free.  Rows past M / N re-read the last row.
   // Direct loads as buffer loads: a buffer descriptor per operand (scalar
   // registers), a fixed 32-bit per-lane byte offset in one vector register,
   // the stage's advance as the scalar offset and the LDS destination in M0
@@ -878,13 +895,13 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
       const int r = 16 * (8 * d + wave) + (lane >> 2);
       int gm = m0 + r;
       gm = gm < p.M ? gm : p.M - 1;
-      const int chunk = (lane & 3) ^ ((r >> 2) & 3);
+      const int chunk = (lane & 3) ^ g8_swz64(r, S16);
       a_src[d] = (uint32_t)((int64_t)gm * p.lda * (MX ? 1 : 2)) + chunk * 16;
     } else {
       const int r = 8 * (8 * d + wave) + (lane >> 3);
       int gm = m0 + r;
       gm = gm < p.M ? gm : p.M - 1;
-      const int chunk = (lane & 7) ^ ((r >> 1) & 7);
+      const int chunk = (lane & 7) ^ g8_swz128(r, S16);
       a_src[d] = (uint32_t)((int64_t)gm * p.lda * 2) + chunk * 16;
     }
   }
@@ -894,7 +911,7 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
     const int r = 16 * (8 * d + wave) + (lane >> 2);
     int gn = n0 + r;
     gn = gn < p.N ? gn : p.N - 1;
-    const int chunk = (lane & 3) ^ ((r >> 2) & 3);
+    const int chunk = (lane & 3) ^ g8_swz64(r, S16);
     b_src[d] = (uint32_t)((int64_t)gn * p.ldb * (BF ? 2 : 1)) + chunk * 16;
   }
   auto dma_stage = [&](int kt, int buf) __attribute__((always_inline)) {
@@ -913,7 +930,7 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   // MX (32x32x64): lane (row fr, half h) reads chunk 2 pp + h of its 64-byte
   // code rows for the stage's k-step pair pp, both operands.
   const int fr = lane & 31, h = lane >> 5;
-  const int b_swz = (fr >> 2) & 3;
+  const int b_swz = g8_swz64(fr, false);
   int b_base[2], a_mx[2];
 #pragma unroll
   for (int pp = 0; pp < 2; ++pp) {
@@ -927,16 +944,17 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   // k = 16 q + 8 s + [0, 8) in lane q for both operands -- the activation
   // fragment is chunk 2 q + s of the 128-byte row -- so the E8M0 block of a
   // lane's codes is q / 2 in both k-steps.  Every 16 lanes read 16
-  // consecutive rows of one logical chunk: conflict-free under the swizzle.
+  // consecutive rows of one logical chunk (conflict-free under g8_swz64 /
+  // g8_swz128 of the 16x16 form; the row's bits 0-3 are those of r16).
   // The activation bases come as a low / high pair (stage buffers 0-1 / 1-2
   // of the 8-bit-code ring) so that the offsets fit the 16-bit immediate.
   const int r16 = lane & 15, q = lane >> 4;
-  const int w16 = B_REGION + (wn * WN + r16) * B_ROWB + ((q ^ ((r16 >> 2) & 3)) * 16);
+  const int w16 = B_REGION + (wn * WN + r16) * B_ROWB + ((q ^ g8_swz64(r16, true)) * 16);
   int x16_lo[2], x16_hi[2];
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
-    x16_lo[s] = BF ? (wm * WM + r16) * A_ROWB + ((q ^ ((r16 >> 2) & 3)) * 16)
-                   : (wm * WM + r16) * A_ROWB + (((2 * q + s) ^ ((r16 >> 1) & 7)) * 16);
+    x16_lo[s] = BF ? (wm * WM + r16) * A_ROWB + ((q ^ g8_swz64(r16, true)) * 16)
+                   : (wm * WM + r16) * A_ROWB + (((2 * q + s) ^ g8_swz128(r16, true)) * 16);
     x16_hi[s] = x16_lo[s] + A_BYTES;
   }
   // MXFP8 scales reach LDS by direct loads too, eight stages at a time: the
