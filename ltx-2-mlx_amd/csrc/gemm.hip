@@ -812,7 +812,11 @@ struct G8Cfg {
   // per-lane register plus an immediate offset below 64 KiB)
   static constexpr int B_REGION = STAGES * A_BYTES;
   static constexpr int A_DMA = A_BYTES / 1024 / 8, B_DMA = B_BYTES / 1024 / 8;  // per wave per stage
-  static constexpr int EPI_ROWB = WN * 2 + 16;
+  // epilogue staging rows: 16x16 accumulators, 128-byte rows with their
+  // 16-byte chunks XORed by (row / 2) % 8 (conflict-free for both the 8-byte
+  // accumulator writes and the 16-byte row reads, probed); 32x32 (MX), rows
+  // padded to 144 bytes
+  static constexpr int EPI_ROWB = S16 ? WN * 2 : WN * 2 + 16;
   static constexpr int EPI_WAVE = WM * EPI_ROWB;
   static constexpr int EPI_BYTES = 8 * EPI_WAVE;
   static constexpr int COL_BYTES = 2 * BN * 4;
@@ -1288,7 +1292,12 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
           bf16x4 v;
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[e] = (bf16)y[e];
-          *reinterpret_cast<bf16x4*>(E + (S16 ? i * 16 + r16 : i * 32 + fr) * EPI_ROWB + nl * 2) = v;
+          if constexpr (S16) {
+            const int row = i * 16 + r16;
+            *reinterpret_cast<bf16x4*>(E + row * EPI_ROWB + ((((nl >> 3) ^ (row >> 1)) & 7) << 4) + (nl & 7) * 2) = v;
+          } else {
+            *reinterpret_cast<bf16x4*>(E + (i * 32 + fr) * EPI_ROWB + nl * 2) = v;
+          }
         }
       }
     }
@@ -1328,7 +1337,7 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
   for (int it = 0; it < ITS; ++it) {
     const int ml = it * ROWS_PER_IT + rsub;
     const int gm = m0 + wm * WM + ml;
-    bf16x8 v = *reinterpret_cast<const bf16x8*>(E + ml * EPI_ROWB + ch * 16);
+    bf16x8 v = *reinterpret_cast<const bf16x8*>(E + ml * EPI_ROWB + (S16 ? ((ch ^ (ml >> 1)) & 7) : ch) * 16);
     if constexpr (RESID) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
