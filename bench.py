@@ -931,8 +931,8 @@ def guided_step_ms(model, args, ta: int, s: int) -> dict:
 def main(argv=None):
     args = parse_args(argv)
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU; the denoise step does not shard across GPUs "
-                                   "here (see DESIGN.md for the sharding design)", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "one GPU only: the denoise step runs whole on one MI355X (all 48 blocks' "
+                                   "weights resident in its HBM) and is not sharded across GPUs", "n_gpus": args.gpus}))
         return 2
     if args.counter_workload:
         counter_workload(args.counter_workload, args.weights, args.counter_tile)
