@@ -334,22 +334,23 @@ def test_gemm8_epilogues(epi, kind, M, K, N, rows):
     assert (ulp_diff_bf16(bf16_from_torch(out), bf16_from_torch(ref_old)) <= 1).mean() >= 0.99
 
 
-@pytest.mark.parametrize("M", [3456, 1296])
+@pytest.mark.parametrize("M,N", [(3456, 16384), (1296, 16384), (6144, 4096)])
 @pytest.mark.parametrize("epi", ["bias", "gelu", "residual", "residual_round"])
 @pytest.mark.parametrize("kind", ["bf16", "int8", "mxfp8"])
-def test_gemm8_row_split_matches_one_launch(kind, epi, M):
-    """At 3456 and 1296 rows x 16384 columns the automatic choice runs the
-    first rows in 256-row tiles and the rest (384 / 272 rows) by a second
-    launch of the 128-row form, whose activation, output and residual rows
-    are offset views of the same buffers: bit-identical to one launch of
-    256-row tiles for every epilogue, in place on the residual for the gated
-    forms, and the bias form with head-gate columns."""
+def test_gemm8_row_split_matches_one_launch(kind, epi, M, N):
+    """At 3456 and 1296 rows x 16384 columns and 6144 rows x 4096 columns the
+    automatic choice runs the first rows in 256-row tiles and the rest (384 /
+    272 / 2048 rows) by a second launch of the 128-row form, whose activation,
+    output and residual rows are offset views of the same buffers:
+    bit-identical to one launch of 256-row tiles for every epilogue, in place
+    on the residual for the gated forms, and the bias form with head-gate
+    columns."""
     from ltx_amd.kernels import gemm
 
     codes = {"bias": gemm.EPI_BIAS, "gelu": gemm.EPI_GELU, "residual": gemm.EPI_RESIDUAL,
              "residual_round": gemm.EPI_RESIDUAL_ROUND}
-    K, N = 512, 16384
-    print(f"gemm8 row split {kind} {epi} M={M}", flush=True)
+    K = 512
+    print(f"gemm8 row split {kind} {epi} M={M} N={N}", flush=True)
     rng = np.random.default_rng(M + len(epi))
     x = _t(_bf(rng, (M, K)))
     wt = gemm.make_weight(_t(_bf(rng, (N, K), 0.05)), _t(rng.standard_normal(N).astype(np.float32) * 0.1,
