@@ -280,6 +280,24 @@ int ltx_gemm_mxfp8_bf16(const void* A, int64_t lda, const uint8_t* Wq, int64_t l
                         const void* residual, int64_t ldr, const float* gate, int64_t sigmoid_from,
                         void* stream);
 
+/* The bias-epilogue product (LTX_GEMM_EPI_BIAS, optionally OR-ed with
+ * LTX_GEMM_ROUND_THEN_BIAS and LTX_GEMM_TILE_G8 / _G8_128) of one weight
+ * format -- wformat 0: bf16 W as ltx_gemm_bf16, 1: int8 W + fp32 w_scale as
+ * ltx_gemm_w8a16_bf16, 2: MXFP8 W + E8M0 w_scale (ld_scale) as
+ * ltx_gemm_mxfp8_bf16 -- plus the per-row sums of squares of its bf16
+ * outputs in columns [0, ss_cols):
+ *   rowss[m * ld_rowss + j] = sum_{n in [64 j, 64 j + 64)} C[m, n]^2 (fp32).
+ * ss_cols % 64 == 0, ss_cols <= min(N, sigmoid_from), ld_rowss >= ss_cols / 64,
+ * rowss 4-byte aligned.  Always the eight-wave kernel (LTX_ERR_UNSUPPORTED
+ * where it does not apply); C equals the plain entry point's result on that
+ * kernel bit for bit.  No counterpart in the reference: the row statistics of
+ * the query RMS norm (attention.py:578-580) for ltx_flash_attn_qnorm_v_bf16,
+ * which then needs no separate pass over Q. */
+int ltx_gemm_rowss_bf16(int wformat, const void* A, int64_t lda, const void* W, int64_t ldw,
+                        const void* w_scale, int64_t ld_scale, const float* bias, void* C, int64_t ldc,
+                        int64_t M, int64_t N, int64_t K, int epilogue, int64_t sigmoid_from,
+                        float* rowss, int64_t ld_rowss, int64_t ss_cols, void* stream);
+
 /* MXFP8 activations x MXFP8 weights on the gfx950 scaled fp8 MFMA
  * (v_mfma_scale_f32_32x32x64_f8f6f4), an opt-in path.  No counterpart in the
  * reference: its MXFP8 weights (loader/transformer_cache.py:177-193) are
@@ -510,6 +528,28 @@ int ltx_flash_attn_bf16(const void* Q, int64_t q_rs, const void* K, int64_t k_rs
                         const void* Vt, int64_t tk_pad, void* O, int64_t o_rs,
                         const void* gate, int64_t gate_rs, int64_t Tq, int64_t Tk,
                         int64_t H, int64_t head_dim, float scale, void* stream);
+
+/* ltx_flash_attn_v_bf16 on the raw query projection: the kernel applies the
+ * query RMS norm and split RoPE of ltx_qknorm_rope_bf16 / _axes_bf16 as it
+ * loads Q (attention.py:578-584 fused into the attention core,
+ * attention.py:283-302), from ss (Tq, ss_parts) fp32 per-row partial sums of
+ * squares over the whole inner dim H*head_dim (ss_parts a multiple of 4 in
+ * [4, 64], row stride ld_ss a multiple of 4, 16-byte aligned; e.g. the rowss
+ * of ltx_gemm_rowss_bf16 for the Q columns), the norm weights wq (fp32,
+ * H*head_dim, 16-byte aligned) and eps:
+ *   x = bf16(q * rsqrt(sum(ss[q, :]) / (H*head_dim) + eps) * wq)
+ * then the pair (d, d + head_dim/2) of each head rotated by the fp32 tables
+ * cos / sin of H*head_dim/2 columns (16-byte aligned): one row per query
+ * (idx NULL, tab_rows >= Tq) or `axes` (1-3) factored rows per query at
+ * idx[q * axes + a] (int32, clamped to [0, tab_rows)), combined as for
+ * ltx_qknorm_rope_axes_bf16; cos = sin = NULL: no RoPE.  Single pass (no
+ * split-KV form), token-major V. */
+int ltx_flash_attn_qnorm_v_bf16(const void* Q, int64_t q_rs, const void* K, int64_t k_rs,
+                                const void* V, int64_t v_rs, void* O, int64_t o_rs, const void* gate,
+                                int64_t gate_rs, int64_t Tq, int64_t Tk, int64_t H, int64_t head_dim,
+                                float scale, const float* ss, int64_t ld_ss, int64_t ss_parts,
+                                const float* wq, float eps, const float* cos, const float* sin,
+                                const int* idx, int64_t axes, int64_t tab_rows, void* stream);
 
 /* Split-KV form of ltx_flash_attn_bf16 for few queries over many keys (the
  * audio-query V2A cross-attention: 68-121 queries x 3456-6144 video keys):

@@ -130,6 +130,37 @@ struct SplitOut {
   int splits;
 };
 
+// Q's RMS norm and split RoPE applied as the kernel loads Q (the rows hold
+// the projection's raw output).  ss: per-row partial sums of squares over the
+// whole inner dim (Tq rows of `parts` fp32 values, row stride ld_ss); w: the
+// norm weights (H * dh); cos / sin: RoPE tables of (H * dh / 2) columns, one
+// row per query (idx null) or `axes` factored rows per query at
+// idx[q * axes + a] (clamped to tab_rows); cos null: no RoPE.  ss null: Q is
+// used as given.
+struct QNorm {
+  const float* ss;
+  int64_t ld_ss;
+  int parts;
+  const float* w;
+  float inv_d;
+  float eps;
+  const float* cos;
+  const float* sin;
+  const int* idx;
+  int axes;
+  int64_t tab_rows;
+};
+
+__device__ __forceinline__ void attn_load8f(const float* p, float* out) {
+  const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+  const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[i] = a[i];
+    out[4 + i] = b[i];
+  }
+}
+
 // Softmax schedule of one key block over the MFMA slots of the pipeline:
 // slots 0..NP-1 are the P.V half that follows the block's S^T (row max in
 // slots < F, running-max update in slot F, exps after it), slots NP.. are the
@@ -158,7 +189,8 @@ template <int DH, bool GATED, int WAVES, bool SPLIT, bool VROW>
 __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
     const bf16* __restrict__ Q, int64_t q_rs, const bf16* __restrict__ K, int64_t k_rs,
     const bf16* __restrict__ V, int64_t v_ld, bf16* __restrict__ O, int64_t o_rs,
-    const bf16* __restrict__ G, int64_t g_rs, int Tq, int Tk, int H, float scale_log2, SplitOut so) {
+    const bf16* __restrict__ G, int64_t g_rs, int Tq, int Tk, int H, float scale_log2, SplitOut so,
+    QNorm qn) {
   using Cfg = AttnCfg<DH, WAVES, VROW>;
   constexpr int kAttnQ = Cfg::QT;
   constexpr int DSTEPS = Cfg::DSTEPS, DTILES = Cfg::DTILES;
@@ -209,6 +241,109 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
 #pragma unroll
     for (int s = 0; s < DSTEPS; ++s) qf[s] = *reinterpret_cast<const bf16x8*>(qrow + s * 16);
   }
+  // Q's norm and RoPE (QNorm), applied once this workgroup's first K / V
+  // loads are in flight, so that its own loads (row statistics, weights,
+  // tables) wait behind them rather than ahead of them.  Every load is
+  // unconditional (clamped indices), so each batch goes out at once.
+  auto apply_qnorm = [&]() __attribute__((always_inline)) {
+    int q = q0 + l32;
+    q = q < Tq ? q : Tq - 1;
+    // sum of the row's partials: lane hh takes the 4-value chunks c with
+    // c % 2 == hh, the pair adds both halves in the same order
+    const float* sp = qn.ss + (int64_t)q * qn.ld_ss;
+    const int nch = qn.parts >> 2;
+    f32x4 pv[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int ch = 2 * c + hh;
+      pv[c] = *reinterpret_cast<const f32x4*>(sp + 4 * (ch < nch ? ch : 0));
+    }
+    const bool rope = qn.cos != nullptr;
+    const int naxes = !rope ? 0 : (qn.idx != nullptr ? qn.axes : 1);
+    const int64_t tw = (int64_t)H * (DH / 2);
+    constexpr int NS = DSTEPS / 2;
+    // weights of every pair (independent of the table rows)
+    float wa[NS][8], wb[NS][8];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int c1 = head * DH + s * 16 + hh * 8;  // weight of x1; x2's is c1 + DH / 2
+      attn_load8f(qn.w + c1, wa[s]);
+      attn_load8f(qn.w + c1 + DH / 2, wb[s]);
+    }
+    int64_t rows[3] = {(int64_t)q * tw, (int64_t)q * tw, (int64_t)q * tw};
+    if (qn.idx != nullptr) {
+      const int* ip = qn.idx + (int64_t)q * qn.axes;
+      int r[3];
+#pragma unroll
+      for (int a = 0; a < 3; ++a) r[a] = ip[a < qn.axes ? a : 0];
+#pragma unroll
+      for (int a = 0; a < 3; ++a) {
+        const int64_t row = r[a] < 0 ? 0 : (r[a] < qn.tab_rows ? r[a] : qn.tab_rows - 1);
+        rows[a] = row * tw;
+      }
+    }
+    float half = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const float v4 = (pv[c][0] + pv[c][1]) + (pv[c][2] + pv[c][3]);
+      half += (2 * c + hh < nch) ? v4 : 0.0f;
+    }
+    // after the swap, element 0 holds the hh = 0 lane's half, element 1 the
+    // hh = 1 lane's: both lanes add them in that order
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(half), __float_as_uint(half), false, false);
+    const float ss = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    const float inv = rsqrt_rn(ss * qn.inv_d + qn.eps);
+    float x1[NS][8], x2[NS][8];
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        x1[s][i] = round_bf((float)qf[s][i] * inv * wa[s][i]);
+        x2[s][i] = round_bf((float)qf[s + NS][i] * inv * wb[s][i]);
+      }
+    if (rope) {
+      // two pairs' table entries per batch of loads; factored rows combine
+      // as cos = c0 c1 c2, sin = s0 + s1 + s2
+#pragma unroll
+      for (int s0 = 0; s0 < NS; s0 += 2) {
+        float c[2][3][8], sn[2][3][8];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int t1 = head * (DH / 2) + (s0 + u) * 16 + hh * 8;  // table column of the pair
+#pragma unroll
+          for (int a = 0; a < 3; ++a) {
+            attn_load8f(qn.cos + rows[a] + t1, c[u][a]);
+            attn_load8f(qn.sin + rows[a] + t1, sn[u][a]);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int s = s0 + u;
+#pragma unroll
+          for (int a = 1; a < 3; ++a)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              c[u][0][i] = a < naxes ? c[u][0][i] * c[u][a][i] : c[u][0][i];
+              sn[u][0][i] = a < naxes ? sn[u][0][i] + sn[u][a][i] : sn[u][0][i];
+            }
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float o1 = x1[s][i] * c[u][0][i] - x2[s][i] * sn[u][0][i];
+            const float o2 = x1[s][i] * sn[u][0][i] + x2[s][i] * c[u][0][i];
+            x1[s][i] = o1;
+            x2[s][i] = o2;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        qf[s][i] = (bf16)x1[s][i];
+        qf[s + NS][i] = (bf16)x2[s][i];
+      }
+  };
 
   // ---- DMA sources.  Wave instruction i fills the 1 KiB LDS block
   // WAVES*i + wave.  K: 1024/K_ROWB rows per block.  Buffer loads: per key
@@ -532,9 +667,11 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
         issue_k(kb0 + i, i);
         issue_v(kb0 + i, i);
       }
+      if (qn.ss != nullptr && live) apply_qnorm();
       sync_stage();
     } else {
       issue_k(kb0, 0);
+      if (qn.ss != nullptr && live) apply_qnorm();
       sync_stage();
       if (nb > 1) issue_k(kb0 + 1, 1);
       issue_v(kb0, 0);
@@ -766,7 +903,8 @@ static int attn_check_v(const void* V, int64_t v_rs, int64_t Tk, int64_t H, int6
 template <bool VROW>
 static int launch_attn(const void* Q, int64_t q_rs, const void* K, int64_t k_rs, const void* V, int64_t v_ld,
                        void* O, int64_t o_rs, const void* gate, int64_t gate_rs, int64_t Tq, int64_t Tk,
-                       int64_t H, int64_t head_dim, float scale, hipStream_t s) {
+                       int64_t H, int64_t head_dim, float scale, hipStream_t s,
+                       const QNorm& qn = QNorm{}) {
   if (Tq == 0) return LTX_OK;
   // Short key ranges (text contexts, audio keys) leave a workgroup mostly
   // waiting on its loads and its epilogue: 128-query workgroups with rings of
@@ -781,7 +919,7 @@ static int launch_attn(const void* Q, int64_t q_rs, const void* K, int64_t k_rs,
 #define LTX_FA(DH, G, W)                                                                           \
   flash_attn_kernel<DH, G, W, false, VROW><<<(int)nwg, 64 * W, 0, s>>>(                            \
       (const bf16*)Q, q_rs, (const bf16*)K, k_rs, (const bf16*)V, v_ld, (bf16*)O, o_rs,             \
-      (const bf16*)gate, gate_rs, (int)Tq, (int)Tk, (int)H, scale_log2, none)
+      (const bf16*)gate, gate_rs, (int)Tq, (int)Tk, (int)H, scale_log2, none, qn)
   if (small) {
     if (head_dim == 128) {
       if (gate) LTX_FA(128, true, kAttnSplitWaves); else LTX_FA(128, false, kAttnSplitWaves);
@@ -821,6 +959,42 @@ extern "C" int ltx_flash_attn_v_bf16(const void* Q, int64_t q_rs, const void* K,
                            (hipStream_t)stream);
 }
 
+// ltx_flash_attn_v_bf16 on the raw query projection: the kernel applies the
+// query's RMS norm and split RoPE as it loads Q (QNorm above), from the
+// per-row partial sums of squares that ltx_gemm_rowss_bf16 writes next to
+// the projection.
+extern "C" int ltx_flash_attn_qnorm_v_bf16(const void* Q, int64_t q_rs, const void* K, int64_t k_rs,
+                                           const void* V, int64_t v_rs, void* O, int64_t o_rs, const void* gate,
+                                           int64_t gate_rs, int64_t Tq, int64_t Tk, int64_t H, int64_t head_dim,
+                                           float scale, const float* ss, int64_t ld_ss, int64_t ss_parts,
+                                           const float* wq, float eps, const float* cos, const float* sin,
+                                           const int* idx, int64_t axes, int64_t tab_rows, void* stream) {
+  int st = attn_check(Q, q_rs, K, k_rs, O, o_rs, gate, gate_rs, Tq, Tk, H, head_dim, scale);
+  if (st == LTX_OK) st = attn_check_v(V, v_rs, Tk, H, head_dim);
+  if (st != LTX_OK) return st;
+  if (!ss || !wq || ss_parts < 4 || ss_parts > 64 || ss_parts % 4 || ld_ss < ss_parts || !(eps >= 0.0f))
+    return LTX_ERR_INVALID_ARG;
+  if ((cos == nullptr) != (sin == nullptr)) return LTX_ERR_INVALID_ARG;
+  if (idx != nullptr && (cos == nullptr || axes < 1 || axes > 3 || tab_rows < 1)) return LTX_ERR_INVALID_ARG;
+  if (cos != nullptr && idx == nullptr && tab_rows < Tq) return LTX_ERR_INVALID_ARG;
+  if (!al16a(ss) || ld_ss % 4 || !al16a(wq) || (cos && (!al16a(cos) || !al16a(sin)))) return LTX_ERR_ALIGNMENT;
+  if (Tq > 0 && ld_ss > INT64_MAX / Tq) return LTX_ERR_UNSUPPORTED;
+  QNorm qn{};
+  qn.ss = ss;
+  qn.ld_ss = ld_ss;
+  qn.parts = (int)ss_parts;
+  qn.w = wq;
+  qn.inv_d = 1.0f / (float)(H * head_dim);
+  qn.eps = eps;
+  qn.cos = cos;
+  qn.sin = sin;
+  qn.idx = idx;
+  qn.axes = idx ? (int)axes : 1;
+  qn.tab_rows = tab_rows;
+  return launch_attn<true>(Q, q_rs, K, k_rs, V, v_rs, O, o_rs, gate, gate_rs, Tq, Tk, H, head_dim, scale,
+                           (hipStream_t)stream, qn);
+}
+
 extern "C" int64_t ltx_attn_splitkv_workspace_bytes(int64_t Tq, int64_t H, int64_t head_dim, int64_t splits) {
   if (Tq < 0 || H <= 0 || head_dim <= 0 || splits <= 0) return -1;
   // -1 for sizes whose byte count does not fit an int64 (no wrapped result)
@@ -854,7 +1028,7 @@ static int launch_attn_splitkv(const void* Q, int64_t q_rs, const void* K, int64
   do {                                                                                              \
     flash_attn_kernel<DH, false, kAttnSplitWaves, true, VROW><<<(int)nwg, 64 * kAttnSplitWaves, 0, s>>>( \
         (const bf16*)Q, q_rs, (const bf16*)K, k_rs, (const bf16*)V, v_ld, nullptr, 0, nullptr,      \
-        0, (int)Tq, (int)Tk, (int)H, scale_log2, so);                                               \
+        0, (int)Tq, (int)Tk, (int)H, scale_log2, so, QNorm{});                                      \
     attn_combine_kernel<DH, G><<<cblocks, 256, 0, s>>>(so, (bf16*)O, o_rs, (const bf16*)gate,       \
                                                        gate_rs, (int)Tq, (int)H);                    \
   } while (0)

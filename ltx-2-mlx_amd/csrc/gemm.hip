@@ -75,6 +75,12 @@ struct GemmArgs {
   int64_t ld_cscale;
   int M, N, K;         // split-K: K is the per-split depth
   int tiles_m, tiles_n;
+  // 8-wave bias epilogue: per-row sums of squares of the bf16 outputs of
+  // columns [0, ss_cols), one fp32 partial per 64-column slice at
+  // rowss[row * ld_rowss + col / 64] (null: none)
+  float* rowss = nullptr;
+  int64_t ld_rowss = 0;
+  int ss_cols = 0;
 };
 
 constexpr int kGemmThreads = 256;
@@ -1374,6 +1380,22 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(GemmArgs p) {
     } else {
       if (gm < p.M && col_ok) *reinterpret_cast<bf16x8*>(p.C + (int64_t)gm * p.ldc + gn2) = v;
     }
+    if constexpr (EPI == LTX_GEMM_EPI_BIAS) {
+      // the row's sum of squares over this wave's 64 columns: eight per lane,
+      // then over the row's eight lanes (consecutive: lane = 8 rsub + ch)
+      if (p.rowss != nullptr && n0 + wn * WN < p.ss_cols) {
+        float q = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float f = (float)v[e];
+          q = fmaf(f, f, q);
+        }
+        q += __shfl_xor(q, 1, 64);
+        q += __shfl_xor(q, 2, 64);
+        q += __shfl_xor(q, 4, 64);
+        if (ch == 0 && gm < p.M) p.rowss[(int64_t)gm * p.ld_rowss + (n0 + wn * WN) / WN] = q;
+      }
+    }
   }
 }
 
@@ -1443,6 +1465,7 @@ static GemmArgs rows_from(const GemmArgs& p, int r0) {
   q.A = p.A + (int64_t)r0 * p.lda;
   q.C = p.C + (int64_t)r0 * p.ldc;
   if (p.R) q.R = p.R + (int64_t)r0 * p.ldr;
+  if (p.rowss) q.rowss = p.rowss + (int64_t)r0 * p.ld_rowss;
   q.M = p.M - r0;
   return q;
 }
@@ -1477,7 +1500,10 @@ static int launch_epi_w(const GemmArgs& p, int tile, hipStream_t s) {
     const bool g8 = (BKIND == B_MXFP8 || BKIND == B_INT8 || (BKIND == B_BF16 && (p.N >= p.K || big < 160))) &&
                     g8_ok<BKIND>(p);
     tile = big >= 160 ? (g8 ? 5 : 1) : (big >= 100 && g8 ? 5 : 2);
+    // row sums of squares come from the 8-wave kernel's epilogue only
+    if (p.rowss && tile != 5) tile = 5;
   }
+  if (p.rowss && tile != 5 && tile != 6) return LTX_ERR_UNSUPPORTED;
   if (tile == 5 || tile == 6) {
     if (!g8_ok<BKIND>(p)) return LTX_ERR_UNSUPPORTED;
     const int r0 = (tile == 5 && auto_tile) ? g8_split_rows(p.M, p.N) : p.M;
@@ -1738,6 +1764,44 @@ extern "C" int ltx_gemm_mxfp8_bf16(const void* A, int64_t lda, const uint8_t* Wq
   if (K == 0) return LTX_ERR_UNSUPPORTED;
   GemmArgs p = make_args(A, lda, Wq, ldw, w_scale, ld_scale, bias, C, ldc, M, N, K, residual, ldr,
                          gate, sigmoid_from);
+  return launch_kind<B_MXFP8>(p, epilogue, (hipStream_t)stream);
+}
+
+// The bias-epilogue product of one of the three weight formats (wformat 0:
+// bf16 as ltx_gemm_bf16, 1: int8 as ltx_gemm_w8a16_bf16, 2: MXFP8 as
+// ltx_gemm_mxfp8_bf16) with the per-row sums of squares of its bf16 outputs in
+// columns [0, ss_cols): rowss[m * ld_rowss + j] = sum of C[m, n]^2 over
+// n in [64 j, 64 j + 64).  Always the 8-wave kernel (its epilogue computes
+// them); C is bit-identical to the plain entry point's on that kernel.
+extern "C" int ltx_gemm_rowss_bf16(int wformat, const void* A, int64_t lda, const void* W, int64_t ldw,
+                                   const void* w_scale, int64_t ld_scale, const float* bias, void* C,
+                                   int64_t ldc, int64_t M, int64_t N, int64_t K, int epilogue,
+                                   int64_t sigmoid_from, float* rowss, int64_t ld_rowss, int64_t ss_cols,
+                                   void* stream) {
+  if (wformat < 0 || wformat > 2) return LTX_ERR_INVALID_ARG;
+  if ((epilogue & 0xff) != LTX_GEMM_EPI_BIAS) return LTX_ERR_INVALID_ARG;
+  const int tile = (epilogue >> 8) & 0xf;
+  if (tile != 0 && tile != 5 && tile != 6) return LTX_ERR_UNSUPPORTED;
+  int st = gemm_check(A, lda, W, ldw, C, ldc, M, N, K, epilogue, nullptr, 0, nullptr, wformat == 0 ? 2 : 1);
+  if (st != LTX_OK) return st;
+  if (!rowss || ss_cols <= 0 || ss_cols % 64 || ss_cols > N || ss_cols > sigmoid_from || ld_rowss < ss_cols / 64)
+    return LTX_ERR_INVALID_ARG;
+  if (((uintptr_t)rowss & 3u) != 0) return LTX_ERR_ALIGNMENT;
+  if (M > 0 && ld_rowss > (INT64_MAX / M)) return LTX_ERR_UNSUPPORTED;
+  if (wformat == 1 && !w_scale) return LTX_ERR_INVALID_ARG;
+  if (wformat == 2) {
+    if (!w_scale || ld_scale < K / 32) return LTX_ERR_INVALID_ARG;
+    if (ld_scale % 4 || ((uintptr_t)w_scale & 3u)) return LTX_ERR_ALIGNMENT;
+  }
+  if (M == 0 || N == 0) return LTX_OK;
+  if (K == 0) return LTX_ERR_UNSUPPORTED;
+  GemmArgs p = make_args(A, lda, W, ldw, wformat == 0 ? nullptr : w_scale, wformat == 2 ? ld_scale : 0, bias, C,
+                         ldc, M, N, K, nullptr, 0, nullptr, sigmoid_from);
+  p.rowss = rowss;
+  p.ld_rowss = ld_rowss;
+  p.ss_cols = (int)ss_cols;
+  if (wformat == 0) return launch_kind<B_BF16>(p, epilogue, (hipStream_t)stream);
+  if (wformat == 1) return launch_kind<B_INT8>(p, epilogue, (hipStream_t)stream);
   return launch_kind<B_MXFP8>(p, epilogue, (hipStream_t)stream);
 }
 

@@ -41,6 +41,8 @@ SIGNATURES: dict[str, list] = {
                             _i64, _vp],
     "ltx_gemm_mxfp8_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64,
                             _vp, _i64, _vp],
+    "ltx_gemm_rowss_bf16": [_int, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _int, _i64,
+                            _vp, _i64, _i64, _vp],
     "ltx_gemm_splitk_bf16": [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64, _vp, _i64,
                              _int, _vp, _i64, _vp],
     "ltx_gemm_splitk_w8a16_bf16": [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64,
@@ -74,6 +76,8 @@ SIGNATURES: dict[str, list] = {
                                   _vp, _i64, _i64, _i64, _i64, _f32, _vp],
     "ltx_flash_attn_v_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _f32,
                               _vp],
+    "ltx_flash_attn_qnorm_v_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64,
+                                    _i64, _f32, _vp, _i64, _i64, _vp, _f32, _vp, _vp, _vp, _i64, _i64, _vp],
     "ltx_flash_attn_splitkv_v_bf16": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64,
                                       _i64, _f32, _i64, _vp, _i64, _vp],
     "ltx_broadcast_add_f32": [_vp, _vp, _vp, _i64, _i64, _vp],

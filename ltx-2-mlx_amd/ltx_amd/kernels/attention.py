@@ -55,7 +55,7 @@ def kv_splits(tq: int, tk: int, heads: int) -> int:
 def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor | None, heads: int, *,
                     vt: torch.Tensor | None = None, gate: torch.Tensor | None = None,
                     out: torch.Tensor | None = None, scale: float | None = None,
-                    splits: int | None = None) -> torch.Tensor:
+                    splits: int | None = None, qnorm: tuple | None = None) -> torch.Tensor:
     """softmax(q k^T * scale) v per head, optionally times a per-head gate.
 
     q (Tq, H*dh), k/v (Tk, H*dh) bf16 row views; the kernel reads V in that
@@ -65,6 +65,12 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor | None, he
     given).  ``splits`` forces the number of key ranges (default
     :func:`kv_splits`); more than one runs the split-KV kernel pair with a
     workspace from the torch allocator.
+
+    ``qnorm`` = (ss, wq, pe, eps): q holds the raw query projection and the
+    kernel applies the query RMS norm (weights wq, fp32 (H*dh)) and split RoPE
+    (pe as for :func:`rope_ops.qknorm_rope_`, or None) as it loads Q, with
+    the row statistics ss (Tq, parts) fp32 from :func:`gemm.linear_rowss`
+    (single pass, token-major V only).
     """
     d = q.shape[-1]
     dh = d // heads
@@ -95,6 +101,31 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor | None, he
         gptr = gv.data_ptr()
     if splits is None:
         splits = kv_splits(tq, tk, heads)
+    if qnorm is not None:
+        if splits > 1 or vt is not None:
+            raise ValueError("the fused query norm runs in the single-pass kernel on token-major V")
+        ss, wq, pe, eps = qnorm
+        if ss.dtype != torch.float32 or ss.dim() != 2 or ss.shape[0] != tq or ss.stride(1) != 1:
+            raise ValueError(f"row statistics must be fp32 ({tq}, parts) rows, got {tuple(ss.shape)}")
+        if wq.dtype != torch.float32 or wq.numel() != d:
+            raise ValueError("query norm weights must be fp32 with H*dh elements")
+        cos = sin = idx = None
+        axes, rows = 1, 0
+        if pe is not None:
+            cos, sin = pe[0], pe[1]
+            if cos.dtype != torch.float32 or cos.shape[-1] != d // 2 or sin.shape != cos.shape:
+                raise ValueError(f"RoPE tables must be fp32 (R, {d // 2})")
+            rows = cos.numel() // (d // 2)
+            if len(pe) > 2:
+                idx = pe[2].contiguous()
+                if idx.dtype != torch.int32 or idx.dim() != 2 or idx.shape[0] < tq:
+                    raise ValueError(f"RoPE row index must be int32 (T, axes) covering {tq} rows")
+                axes = idx.shape[1]
+        _lib.call("ltx_flash_attn_qnorm_v_bf16", _lib.ptr(qv), qs, _lib.ptr(kv), ks, vptr, vld, ov.data_ptr(), os_,
+                  gptr, gs, tq, tk, heads, dh, float(scale), ss.data_ptr(), ss.stride(0), ss.shape[1],
+                  wq.contiguous().data_ptr(), float(eps), _lib.ptr(cos), _lib.ptr(sin), _lib.ptr(idx), axes, rows,
+                  _lib.stream_of(q), detail=f"qnorm Tq={tq} Tk={tk} H={heads} dh={dh}")
+        return out
     if splits > 1:
         nbytes = _lib.lib().ltx_attn_splitkv_workspace_bytes(tq, heads, dh, splits)
         ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)

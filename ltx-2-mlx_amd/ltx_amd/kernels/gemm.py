@@ -388,6 +388,62 @@ def _mx_eligible(m: int, n: int, k: int, weight: LinearWeight, tile: int) -> boo
             and ((m + 255) // 256) * ((n + 255) // 256) >= MX_MIN_TILES)
 
 
+def rowss_eligible(x: torch.Tensor, weight: LinearWeight) -> bool:
+    """Whether :func:`linear_rowss` takes this product: bf16 activations,
+    weights of one of the three formats, at least 100 tiles of 256x256 (where
+    the automatic choice of :func:`linear` is the 8-wave kernel for a
+    projection at least as wide as half its depth, so both give the same
+    outputs) and the 8-wave kernel's conditions (MXFP8 weights: K a multiple
+    of 512), outside the opt-in MX path."""
+    if isinstance(x, MxRows) or x.dtype != torch.bfloat16 or weight.kind not in ("bf16", "int8", "mxfp8"):
+        return False
+    k, n = weight.in_features, weight.out_features
+    m = x.numel() // max(k, 1)
+    tiles = ((m + 255) // 256) * ((n + 255) // 256)
+    if tiles < 100 or (weight.kind == "bf16" and tiles >= 160 and n < k):
+        return False
+    if weight.kind == "mxfp8" and (k % 512 or _mx_eligible(m, n, k, weight, TILE_AUTO)):
+        return False
+    return True
+
+
+def linear_rowss(x: torch.Tensor, weight: LinearWeight, ss_cols: int, *,
+                 sigmoid_from: int | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """:func:`linear` with the bias epilogue on the 8-wave kernel, plus the
+    per-row sums of squares of the bf16 outputs of columns [0, ss_cols) in
+    fp32 partials of 64 columns: returns (out (M, N) bf16, ss (M, ss_cols/64)
+    fp32) (ltx_gemm_rowss_bf16).  ``out`` is bit-identical to :func:`linear`
+    on that kernel."""
+    k = weight.in_features
+    n = weight.out_features
+    if not rowss_eligible(x, weight):
+        raise ValueError(f"linear_rowss does not take {weight.kind} weights / {x.dtype} activations here")
+    xv, lda = _lib.row_view(x, k)
+    m = x.numel() // k
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
+    parts = ss_cols // 64
+    ss = torch.empty((m, parts), dtype=torch.float32, device=x.device)
+    flags = EPI_BIAS
+    if weight.qlinear and weight.bias is not None:
+        flags |= _lib.GEMM_ROUND_THEN_BIAS
+    sig = n if sigmoid_from is None else int(sigmoid_from)
+    bptr = None if weight.bias is None else weight.bias.data_ptr()
+    fmt = {"bf16": 0, "int8": 1, "mxfp8": 2}[weight.kind]
+    sptr, lds = (None, 0) if weight.kind == "bf16" else (
+        weight.scale.data_ptr(), weight.scale.stride(0) if weight.kind == "mxfp8" else 0)
+    hook = LAUNCH_HOOK
+    info = (weight.kind, m, n, k, EPI_BIAS) if hook is not None else None
+    if hook is not None:
+        hook("pre", info)
+    if m > 0:
+        _lib.call("ltx_gemm_rowss_bf16", fmt, xv.data_ptr(), lda, weight.w.data_ptr(), weight.w.stride(0), sptr,
+                  lds, bptr, out.data_ptr(), n, m, n, k, flags, sig, ss.data_ptr(), parts, ss_cols,
+                  _lib.stream_of(x), detail=f"rowss {weight.kind} M={m} N={n} K={k} ss_cols={ss_cols}")
+    if hook is not None:
+        hook("post", info)
+    return out, ss
+
+
 def linear(x: torch.Tensor, weight: LinearWeight, *, epilogue: int = EPI_BIAS,
            out: torch.Tensor | None = None, residual: torch.Tensor | None = None,
            gate: torch.Tensor | None = None, tile: int = TILE_AUTO,

@@ -9,13 +9,19 @@ fused into as few GEMMs as the data flow allows:
   get the 2*sigmoid epilogue in the same launch);
 * cross-attention: [Wq; Wg] on the query input and [Wk; Wv] on the context.
 
-QK-norm + RoPE run in place on the fused output, the attention kernel reads
-V where the projection wrote it, the head gate is applied inside the attention
-kernel, and ``to_out`` is left to the caller so it can fuse the block's
-residual update into its epilogue.
+K-norm + RoPE run in place on the fused output.  In the cross-attentions the
+query's norm and RoPE are applied by the attention kernel as it loads Q, from
+per-row sums of squares that the query projection's epilogue writes
+(``FUSED_QNORM``); in the self-attention, and with ``FUSED_QNORM`` off, Q is
+normalised in place with K.  The attention kernel reads V where the
+projection wrote it, the head gate is applied inside the attention kernel, and
+``to_out`` is left to the caller so it can fuse the block's residual update
+into its epilogue.
 """
 
 from __future__ import annotations
+
+import os
 
 import torch
 
@@ -23,6 +29,17 @@ from ...kernels import attention as attn_k
 from ...kernels import gemm
 from ...kernels.rope_ops import qknorm_rope_
 from ...utils import signpost as _sp
+
+# The query RMS norm + RoPE inside the attention kernel's Q load (row
+# statistics from the Q projection's epilogue) instead of an in-place pass
+# over Q; LTX_FUSED_QNORM=0 runs the in-place pass for Q and K together.
+# Default for the cross-attentions only: in the 48-block step that measured
+# 0.2-0.6 ms faster than the in-place pass (two A/B pairs on one box), while
+# the video self-attention's form (three factored table rows per query, 8 us
+# more per attention workgroup than it saves) measured 0.1-0.2 ms slower;
+# LTX_FUSED_QNORM_SELF=1 adds it.
+FUSED_QNORM = os.environ.get("LTX_FUSED_QNORM", "1") == "1"
+FUSED_QNORM_SELF = os.environ.get("LTX_FUSED_QNORM_SELF", "0") == "1"
 
 
 class Attention:
@@ -83,14 +100,26 @@ class Attention:
         """
         inner, heads = self.inner_dim, self.heads
         gate_cols = heads if self.gated else 0
+        tq_all = x.shape[0]
+        tk_all = tq_all if self.self_attention else (kv if kv is not None else context).shape[0]
+        fused = (FUSED_QNORM and (FUSED_QNORM_SELF or not self.self_attention) and inner % 64 == 0
+                 and gemm.rowss_eligible(x, self.proj_q)
+                 and attn_k.kv_splits(tq_all // passes, tk_all // passes, heads) == 1)
+        ss = None
         _sp.begin("attn_qkv")
         if self.self_attention:
-            buf = gemm.linear(x, self.proj_q, sigmoid_from=3 * inner)
+            if fused:
+                buf, ss = gemm.linear_rowss(x, self.proj_q, inner, sigmoid_from=3 * inner)
+            else:
+                buf = gemm.linear(x, self.proj_q, sigmoid_from=3 * inner)
             q, k, v = buf[:, :inner], buf[:, inner:2 * inner], buf[:, 2 * inner:3 * inner]
             g = buf[:, 3 * inner:3 * inner + gate_cols] if self.gated else None
             k_tab = pe
         else:
-            qb = gemm.linear(x, self.proj_q, sigmoid_from=inner)
+            if fused:
+                qb, ss = gemm.linear_rowss(x, self.proj_q, inner, sigmoid_from=inner)
+            else:
+                qb = gemm.linear(x, self.proj_q, sigmoid_from=inner)
             kvb = gemm.linear(context, self.proj_kv) if kv is None else kv
             q = qb[:, :inner]
             g = qb[:, inner:inner + gate_cols] if self.gated else None
@@ -100,12 +129,16 @@ class Attention:
                 k_tab = None
         k_done = kv is not None  # keys already normalised by context_kv
         if passes == 1:
-            qknorm_rope_(q, self.q_norm, pe, k[:0] if k_done else k, self.k_norm, k_tab, heads, self.norm_eps)
+            if not fused:
+                qknorm_rope_(q, self.q_norm, pe, k[:0] if k_done else k, self.k_norm, k_tab, heads, self.norm_eps)
+            elif not k_done:
+                qknorm_rope_(q[:0], self.q_norm, None, k, self.k_norm, k_tab, heads, self.norm_eps)
             _sp.end("attn_qkv")
             if kv_ready is not None:
                 torch.cuda.current_stream().wait_event(kv_ready)
             with _sp.signpost("attn_sdpa"):
-                return attn_k.flash_attention(q, k, v, heads, gate=g)
+                return attn_k.flash_attention(q, k, v, heads, gate=g,
+                                              qnorm=(ss, self.q_norm, pe, self.norm_eps) if fused else None)
         _sp.end("attn_qkv")
         tq, tk = q.shape[0] // passes, k.shape[0] // passes
         if tq * passes != q.shape[0] or tk * passes != k.shape[0]:
@@ -116,8 +149,13 @@ class Attention:
         for p in range(passes):
             qp, kp, vp = q[p * tq:(p + 1) * tq], k[p * tk:(p + 1) * tk], v[p * tk:(p + 1) * tk]
             gp = None if g is None else g[p * tq:(p + 1) * tq]
-            qknorm_rope_(qp, self.q_norm, pe, kp[:0] if k_done else kp, self.k_norm, k_tab, heads, self.norm_eps)
-            attn_k.flash_attention(qp, kp, vp, heads, gate=gp, out=out[p * tq:(p + 1) * tq])
+            if not fused:
+                qknorm_rope_(qp, self.q_norm, pe, kp[:0] if k_done else kp, self.k_norm, k_tab, heads,
+                             self.norm_eps)
+            elif not k_done:
+                qknorm_rope_(qp[:0], self.q_norm, None, kp, self.k_norm, k_tab, heads, self.norm_eps)
+            qn = (ss[p * tq:(p + 1) * tq], self.q_norm, pe, self.norm_eps) if fused else None
+            attn_k.flash_attention(qp, kp, vp, heads, gate=gp, out=out[p * tq:(p + 1) * tq], qnorm=qn)
         return out
 
     def __call__(self, x: torch.Tensor, context: torch.Tensor | None = None, mask=None,
