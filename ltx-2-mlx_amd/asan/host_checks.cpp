@@ -148,6 +148,46 @@ int main(int argc, char** argv) {
          LTX_ERR_INVALID_ARG);  // tk_pad below the padded length
   EXPECT(ltx_attn_transpose_v_bf16(d, 4096, 4, 32, 96, d, 64, nullptr), LTX_ERR_UNSUPPORTED);
   EXPECT(ltx_attn_splitkv_workspace_bytes(68, 32, 64, 16) > 0, 1);
+  // query norm inside the attention kernel: row statistics and table forms
+  EXPECT(ltx_flash_attn_qnorm_v_bf16(d, 4096, d, 4096, d, 4096, d, 4096, nullptr, 0, 4, 4, 32, 128, 0.1f, nullptr,
+                                     64, 64, fd, 1e-6f, nullptr, nullptr, nullptr, 1, 0, nullptr),
+         LTX_ERR_INVALID_ARG);  // no row statistics
+  EXPECT(ltx_flash_attn_qnorm_v_bf16(d, 4096, d, 4096, d, 4096, d, 4096, nullptr, 0, 4, 4, 32, 128, 0.1f, fd, 68,
+                                     68, fd, 1e-6f, nullptr, nullptr, nullptr, 1, 0, nullptr),
+         LTX_ERR_INVALID_ARG);  // more than 64 partials
+  EXPECT(ltx_flash_attn_qnorm_v_bf16(d, 4096, d, 4096, d, 4096, d, 4096, nullptr, 0, 4, 4, 32, 128, 0.1f,
+                                     static_cast<const float*>(m), 64, 64, fd, 1e-6f, nullptr, nullptr, nullptr, 1, 0,
+                                     nullptr),
+         LTX_ERR_ALIGNMENT);
+  EXPECT(ltx_flash_attn_qnorm_v_bf16(d, 4096, d, 4096, d, 4096, d, 4096, nullptr, 0, 4, 4, 32, 128, 0.1f, fd, 64,
+                                     64, fd, 1e-6f, fd, nullptr, nullptr, 1, 0, nullptr),
+         LTX_ERR_INVALID_ARG);  // cos without sin
+  EXPECT(ltx_flash_attn_qnorm_v_bf16(d, 4096, d, 4096, d, 4096, d, 4096, nullptr, 0, 4, 4, 32, 128, 0.1f, fd, 64,
+                                     64, fd, 1e-6f, fd, fd, nullptr, 1, 3, nullptr),
+         LTX_ERR_INVALID_ARG);  // per-query table shorter than Tq
+  EXPECT(ltx_flash_attn_qnorm_v_bf16(d, 4096, d, 4096, d, 4096, d, 4096, nullptr, 0, 4, 4, 32, 128, 0.1f, fd, 64,
+                                     64, fd, 1e-6f, fd, fd, id, 4, 10, nullptr),
+         LTX_ERR_INVALID_ARG);  // more than three axes
+  EXPECT(ltx_flash_attn_qnorm_v_bf16(d, 4096, d, 4096, d, 4096, d, 4096, nullptr, 0, 0, 4, 32, 128, 0.1f, fd, 64,
+                                     64, fd, 1e-6f, nullptr, nullptr, nullptr, 1, 0, nullptr),
+         LTX_OK);
+  EXPECT(ltx_gemm_rowss_bf16(3, d, 4096, d, 4096, nullptr, 0, fd, d, 4128, 4, 4128, 4096, 0, 4096, fo, 64, 4096,
+                             nullptr), LTX_ERR_INVALID_ARG);  // no such weight format
+  EXPECT(ltx_gemm_rowss_bf16(0, d, 4096, d, 4096, nullptr, 0, fd, d, 4128, 4, 4128, 4096, 1, 4096, fo, 64, 4096,
+                             nullptr), LTX_ERR_INVALID_ARG);  // GELU epilogue
+  EXPECT(ltx_gemm_rowss_bf16(0, d, 4096, d, 4096, nullptr, 0, fd, d, 4128, 4, 4128, 4096, 1 << 8, 4096, fo, 64,
+                             4096, nullptr), LTX_ERR_UNSUPPORTED);  // a 4-wave tile
+  EXPECT(ltx_gemm_rowss_bf16(0, d, 4096, d, 4096, nullptr, 0, fd, d, 4128, 4, 4128, 4096, 0, 4096, fo, 64, 4000,
+                             nullptr), LTX_ERR_INVALID_ARG);  // not whole 64-column slices
+  EXPECT(ltx_gemm_rowss_bf16(0, d, 4096, d, 4096, nullptr, 0, fd, d, 4128, 4, 4128, 4096, 0, 4096, fo, 32, 4096,
+                             nullptr), LTX_ERR_INVALID_ARG);  // row stride below the slice count
+  EXPECT(ltx_gemm_rowss_bf16(0, d, 4096, d, 4096, nullptr, 0, fd, d, 4128, 4, 4128, 4096, 0, 4096,
+                             reinterpret_cast<float*>(static_cast<char*>(m) + 2), 64, 4096, nullptr),
+         LTX_ERR_ALIGNMENT);
+  EXPECT(ltx_gemm_rowss_bf16(2, d, 4096, d, 4096, nullptr, 128, fd, d, 4128, 4, 4128, 4096, 0, 4096, fo, 64, 4096,
+                             nullptr), LTX_ERR_INVALID_ARG);  // MXFP8 without scales
+  EXPECT(ltx_gemm_rowss_bf16(0, d, 4096, d, 4096, nullptr, 0, fd, d, 4128, 0, 4128, 4096, 0, 4096, fo, 64, 4096,
+                             nullptr), LTX_OK);
   EXPECT(ltx_attn_splitkv_workspace_bytes(68, 0, 64, 16), -1);
   EXPECT(ltx_flash_attn_splitkv_v_bf16(d, 2048, d, 2048, d, 2048, d, 2048, nullptr, 0, 68, 3456, 32, 64, 0.125f, 0,
                                        d, 1 << 20, nullptr), LTX_ERR_INVALID_ARG);  // zero splits
@@ -238,6 +278,14 @@ int main(int argc, char** argv) {
         }
       }
       if (sh.k % 512 == 0 && sh.m >= 256) {
+        // the query projections' row statistics, every weight format
+        const int64_t ssc = (sh.n >= 4096 ? 4096 : sh.n) / 64 * 64;
+        EXPECT(ltx_gemm_rowss_bf16(0, d, sh.k, d, sh.k, nullptr, 0, fd, d, sh.n, sh.m, sh.n, sh.k, 0, ssc, fo,
+                                   ssc / 64, ssc, nullptr), LTX_ERR_HIP);
+        EXPECT(ltx_gemm_rowss_bf16(1, d, sh.k, i8, sh.k, fd, 0, fd, d, sh.n, sh.m, sh.n, sh.k, 0, ssc, fo, ssc / 64,
+                                   ssc, nullptr), LTX_ERR_HIP);
+        EXPECT(ltx_gemm_rowss_bf16(2, d, sh.k, q8, sh.k, q8, sh.k / 32, fd, d, sh.n, sh.m, sh.n, sh.k,
+                                   LTX_GEMM_ROUND_THEN_BIAS, ssc, fo, ssc / 64, ssc, nullptr), LTX_ERR_HIP);
         EXPECT(ltx_gemm_mx_bf16(q8, sh.k, q8, sh.k / 32, q8, sh.k, q8, sh.k / 32, fd, d, sh.n, sh.m, sh.n, sh.k, 2, d,
                                 sh.n, fd, sh.n, nullptr), LTX_ERR_HIP);
         EXPECT(ltx_gemm_mx_gelu_mxfp8(q8, sh.k, q8, sh.k / 32, q8, sh.k, q8, sh.k / 32, fd,
@@ -264,6 +312,17 @@ int main(int argc, char** argv) {
       EXPECT(ltx_flash_attn_bf16(d, rs, d, rs, d, tkp, d, rs, nullptr, 0, a.tq, a.tk, a.h, a.dh, 0.1f, nullptr),
              LTX_ERR_HIP);
       EXPECT(ltx_attn_transpose_v_bf16(d, rs, a.tk, a.h, a.dh, d, tkp, nullptr), LTX_ERR_HIP);
+      if (rs % 256 == 0 && rs / 64 <= 64) {  // query norm in the kernel: no RoPE, per-query and 3-axis tables
+        EXPECT(ltx_flash_attn_qnorm_v_bf16(d, rs, d, rs, d, rs, d, rs, d, a.h, a.tq, a.tk, a.h, a.dh, 0.1f, fd,
+                                           rs / 64, rs / 64, fd, 1e-6f, nullptr, nullptr, nullptr, 1, 0, nullptr),
+               LTX_ERR_HIP);
+        EXPECT(ltx_flash_attn_qnorm_v_bf16(d, rs, d, rs, d, rs, d, rs, d, a.h, a.tq, a.tk, a.h, a.dh, 0.1f, fd,
+                                           rs / 64, rs / 64, fd, 1e-6f, fd, fd, nullptr, 1, a.tq, nullptr),
+               LTX_ERR_HIP);
+        EXPECT(ltx_flash_attn_qnorm_v_bf16(d, rs, d, rs, d, rs, d, rs, d, a.h, a.tq, a.tk, a.h, a.dh, 0.1f, fd,
+                                           rs / 64, rs / 64, fd, 1e-6f, fd, fd, id, 3, 49, nullptr),
+               LTX_ERR_HIP);
+      }
       for (int64_t splits : {int64_t(2), int64_t(16), int64_t(54)}) {
         const int64_t need = ltx_attn_splitkv_workspace_bytes(a.tq, a.h, a.dh, splits);
         EXPECT(need > 0, 1);
