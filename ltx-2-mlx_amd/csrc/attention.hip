@@ -241,10 +241,10 @@ __global__ __launch_bounds__(64 * WAVES, 8 / WAVES) void flash_attn_kernel(
 #pragma unroll
     for (int s = 0; s < DSTEPS; ++s) qf[s] = *reinterpret_cast<const bf16x8*>(qrow + s * 16);
   }
-  // Q's norm and RoPE (QNorm), applied once this workgroup's first K / V
-  // loads are in flight, so that its own loads (row statistics, weights,
-  // tables) wait behind them rather than ahead of them.  Every load is
-  // unconditional (clamped indices), so each batch goes out at once.
+  // Q's norm and RoPE (QNorm), applied after this workgroup's first K / V
+  // loads are issued, so that the latency of its own loads (row statistics,
+  // weights, tables) overlaps theirs.  Every load is unconditional (clamped
+  // indices), so each batch of them goes out at once.
   auto apply_qnorm = [&]() __attribute__((always_inline)) {
     int q = q0 + l32;
     q = q < Tq ? q : Tq - 1;
